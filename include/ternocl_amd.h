@@ -1,0 +1,106 @@
+/*
+ * ternocl_amd.h -- C ABI of the MI355X (gfx950) ternary GEMV/GEMM library.
+ *
+ * Drop-in for the kernel surface of TernOCL (OpenCL kernels for Intel Xe2).
+ * Every entry point keeps the reference kernel's tensors, layouts and argument
+ * order; the OpenCL build-time switches (-DBF16, -DPOSTOP, -DOUT_F32, -DHB, ...)
+ * become ordinary arguments.  All pointers are device pointers (hipMalloc'd),
+ * `stream` is a hipStream_t (NULL = the default stream); every call is
+ * stream-ordered and asynchronous and validates its arguments on the host
+ * before any launch, returning a status (it never exits the process).
+ *
+ * Data formats (shared with the reference):
+ *   A    : DT [M, K] row-major (DT = fp16 or bf16 raw bits)
+ *   B    : uint32 [K/16, N]; word (kp, n) holds the 2-bit codes of rows
+ *          16*kp .. 16*kp+15 of column n, row 16*kp+j at bits 2j..2j+1;
+ *          codes {0, 1, 3} = {0, +1, -1} (code 2 is unspecified)
+ *   S    : DT [K/128, N] per-128-group scales
+ *   C    : DT [M, N], or fp32 with out_f32
+ *   Other: DT [M, N]   (postop 1, 2, 5)     Bias: C's type [N] (postop 3, 5)
+ * Constraints: N % 16 == 0, K % 128 == 0, M >= 1 (ragged M is fine).
+ *
+ * Epilogue (postop), applied to the fp32 accumulator before the output cast,
+ * as common/epilogue.clh:27-37 and common/epilogue.hpp:98-115:
+ *   0 none, 1 silu(acc)*other, 2 acc+other, 3 acc+bias[n], 4 sigmoid(acc)
+ *   (0 for acc <= -10), and 5 = (acc + bias[n]) + other[m,n] (an extension:
+ *   bias add and residual add fused in one pass; no reference counterpart).
+ */
+#ifndef TERNOCL_AMD_H
+#define TERNOCL_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    TERNOCL_OK = 0,
+    TERNOCL_ERR_INVALID_ARG = 1,       /* null pointer, bad enum, bad postop */
+    TERNOCL_ERR_UNSUPPORTED_SHAPE = 2, /* N % 16, K % 128, BITCOS K % (64*ls), ... */
+    TERNOCL_ERR_WORKSPACE = 3,         /* workspace missing or too small */
+    TERNOCL_ERR_LAUNCH = 4             /* the HIP runtime reported an error */
+} ternocl_status;
+
+typedef enum { TERNOCL_FP16 = 0, TERNOCL_BF16 = 1 } ternocl_dtype;
+
+/* Human-readable status and the last HIP error text seen by this thread. */
+const char *ternocl_status_string(int status);
+const char *ternocl_last_error(void);
+/* Library version, e.g. "0.1.0". */
+const char *ternocl_version(void);
+
+/* ---- int2 upcvt GEMV / GEMM -------------------------------------------
+ * Replaces int2_fp16_upcvt_gemm (decode, int2_fp16_upcvt/int2_fp16_upcvt.cl:196-198)
+ * and int2_fp16_upcvt_gemm_mt (prefill, :341-343):
+ *   C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(B[k,n])))
+ * The library picks the kernel: a decode GEMV for M <= 16, an MFMA GEMM above.
+ * ws / ws_bytes: optional device scratch, kept from the XeTLA plugin's entry
+ * (the acc/cnt buffers of int2_upcvt_gemm_impl,
+ * tools/xetla_epilogue_parity/parity.cpp:26-41); ternocl_int2_gemm_ws_bytes()
+ * says how much a shape uses (0: pass NULL).  The GEMVs need none: each
+ * workgroup owns whole columns, so no call keeps state between launches. */
+size_t ternocl_int2_gemm_ws_bytes(int M, int N, int K);
+ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
+                                            const void *S, void *C, const void *Other,
+                                            const void *Bias, int M, int N, int K, int postop,
+                                            int out_f32, void *ws, size_t ws_bytes, void *stream);
+
+/* Decode-GEMV tile, the reference's -DSGM/-DNSG_N/-DLS/-DU knobs for this
+ * hardware.  Every field 0 = automatic. */
+typedef struct {
+    int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: MFMA GEMV (M <= 16) */
+    int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
+    int cols_per_lane;   /* MFMA: adjacent columns per lane, 1 or 2 (16- or 32-column strips) */
+    int groups_per_wave; /* MFMA: 128-row groups per wave per LDS window, 1..16 (power of
+                            two, times M rounded up to a power of two <= 16) */
+    int col_lanes;       /* VALU: lanes across a strip of 4*col_lanes columns, 4, 8 or 16 */
+} ternocl_gemv_tile;
+
+/* Same as ternocl_int2_fp16_upcvt_gemm with an explicit GEMV tile (NULL = automatic).
+ * The tile is ignored when M > 16. */
+ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const uint32_t *B,
+                                               const void *S, void *C, const void *Other,
+                                               const void *Bias, int M, int N, int K,
+                                               int postop, int out_f32, void *ws,
+                                               size_t ws_bytes, const ternocl_gemv_tile *tile,
+                                               void *stream);
+/* Zero-fill device memory with a fill kernel (no hipMemset: graph-capturable). */
+ternocl_status ternocl_workspace_zero(void *ws, size_t ws_bytes, void *stream);
+
+/* Bit-exact test hook for the int2 unpack (no reference counterpart as an
+ * entry point; it materialises the B operand the reference's dq_word builds,
+ * int2_fp16_upcvt.cl:118-150): W[k][n] = +0 / S / S^0x8000 for codes 0 / 1 / 3,
+ * W is DT [K, N].  The GEMVs' own in-register decodes are exported for testing
+ * too: ternocl_int2_gemv_decode writes, per B word, the 8 packed DT pairs that
+ * engine (1 = VALU, 2 = MFMA) builds (layout [K/16][N][8] uint32). */
+ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
+                                    int N, void *stream);
+ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,
+                                        int K, int N, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,139 @@
+"""ternocl_amd -- MI355X (gfx950) ternary GEMV/GEMM library, Python mirror.
+
+The product is the C ABI in ``include/ternocl_amd.h`` (shared library
+``ternocl_amd/_lib/libternocl_amd.so``).  This module is a thin ctypes mirror of
+the reference's kernel interface: the same kernel names and argument order as
+TernOCL's OpenCL kernels, with torch tensors (device memory) in place of
+``cl_mem`` buffers.  It never falls back to a CPU path: if the library is
+missing, every call raises.
+
+Errors: the reference's host drivers print and exit on a shape violation
+(e.g. ``int2_fp16_upcvt/main.cpp:159``); here every check happens on the host
+before any launch and raises :class:`TernoclError` carrying the C status.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+from . import _abi
+
+__all__ = [
+    "TernoclError", "lib", "library_path", "FP16", "BF16",
+    "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
+    "int2_gemv_decode", "gemv_tile", "GemvTile", "VALU", "MFMA",
+]
+
+FP16, BF16 = 0, 1
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libternocl_amd.so"
+_lib = None
+
+
+class TernoclError(RuntimeError):
+    """A C-ABI call returned a non-OK status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} (status {status})")
+        self.status = status
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        path = Path(os.environ.get("TERNOCL_AMD_LIB", _LIB_PATH))
+        if not path.exists():
+            raise TernoclError(-1, f"{path} is missing: run `python -m ternocl_amd.build` first")
+        _lib = ctypes.CDLL(str(path))
+        _abi.declare(_lib)
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        L = lib()
+        raise TernoclError(status, f"{L.ternocl_status_string(status).decode()}: "
+                                   f"{L.ternocl_last_error().decode()}")
+
+
+def _ptr(x) -> int | None:
+    """Device pointer of a torch tensor (None -> NULL, int passes through)."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _dtype_of(t) -> int:
+    import torch
+    if t.dtype == torch.float16:
+        return FP16
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise TernoclError(1, f"activations must be float16 or bfloat16, got {t.dtype}")
+
+
+def _nbytes(t) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
+
+
+# ---- int2 upcvt (int2_fp16_upcvt/int2_fp16_upcvt.cl) --------------------
+
+def int2_gemm_ws_bytes(M: int, N: int, K: int) -> int:
+    """Workspace bytes of ``int2_fp16_upcvt_gemm`` (0 when none is needed)."""
+    return lib().ternocl_int2_gemm_ws_bytes(M, N, K)
+
+
+def workspace_zero(ws, stream=None) -> None:
+    """Zero a workspace once before its first use (the library keeps it zeroed)."""
+    _check(lib().ternocl_workspace_zero(_ptr(ws), _nbytes(ws), _stream(stream)))
+
+
+GemvTile = _abi.GemvTile
+VALU, MFMA = 1, 2
+
+
+def gemv_tile(engine: int = 0, waves: int = 0, cols_per_lane: int = 0, groups_per_wave: int = 0,
+              col_lanes: int = 0) -> "GemvTile":
+    """A decode-GEMV tile (0 = automatic for every field)."""
+    return GemvTile(engine, waves, cols_per_lane, groups_per_wave, col_lanes)
+
+
+def int2_fp16_upcvt_gemm(A, B, S, C, Other, Bias, M: int, N: int, K: int, postop: int = 0,
+                         out_f32: bool = False, ws=None, stream=None, tile=None) -> None:
+    """C = ct(epi(A x dequant(B, S))) -- int2_fp16_upcvt_gemm{,_mt}(A, B, S, C, Other,
+    Bias, M, N, K) of int2_fp16_upcvt.cl:196 / :341.  ``tile`` (a GemvTile)
+    overrides the automatic decode-GEMV tile."""
+    L = lib()
+    args = (_dtype_of(A), _ptr(A), _ptr(B), _ptr(S), _ptr(C), _ptr(Other), _ptr(Bias), M, N, K,
+            postop, int(bool(out_f32)), _ptr(ws), _nbytes(ws))
+    if tile is None:
+        _check(L.ternocl_int2_fp16_upcvt_gemm(*args, _stream(stream)))
+    else:
+        _check(L.ternocl_int2_fp16_upcvt_gemm_ex(*args, ctypes.byref(tile), _stream(stream)))
+
+
+def int2_dequant(B, S, W, K: int, N: int, stream=None) -> None:
+    """W = the DT B operand the reference's dq_word builds (+0, +s, s^0x8000)."""
+    _check(lib().ternocl_int2_dequant(_dtype_of(W), _ptr(B), _ptr(S), _ptr(W), K, N, _stream(stream)))
+
+
+def int2_gemv_decode(B, D, K: int, N: int, bf16: bool, engine: int = MFMA, stream=None) -> None:
+    """D[word][j] = the packed DT pair j a GEMV engine builds from each B word (test hook)."""
+    _check(lib().ternocl_int2_gemv_decode(BF16 if bf16 else FP16, engine, _ptr(B), _ptr(D), K, N,
+                                          _stream(stream)))

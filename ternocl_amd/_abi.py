@@ -1,0 +1,40 @@
+"""ctypes signatures of the C ABI (include/ternocl_amd.h).
+
+``SYMBOLS`` lists every exported entry point; tests check that the header
+declares exactly these and that the built library exports all of them.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+P = C.c_void_p
+
+
+class GemvTile(C.Structure):
+    """ternocl_gemv_tile (include/ternocl_amd.h)."""
+    _fields_ = [("engine", C.c_int), ("waves", C.c_int), ("cols_per_lane", C.c_int),
+                ("groups_per_wave", C.c_int), ("col_lanes", C.c_int)]
+
+I = C.c_int
+Z = C.c_size_t
+
+# name -> (restype, argtypes)
+SYMBOLS: dict[str, tuple] = {
+    "ternocl_status_string": (C.c_char_p, [I]),
+    "ternocl_last_error": (C.c_char_p, []),
+    "ternocl_version": (C.c_char_p, []),
+    "ternocl_int2_gemm_ws_bytes": (Z, [I, I, I]),
+    "ternocl_workspace_zero": (I, [P, Z, P]),
+    "ternocl_int2_fp16_upcvt_gemm": (I, [I, P, P, P, P, P, P, I, I, I, I, I, P, Z, P]),
+    "ternocl_int2_fp16_upcvt_gemm_ex": (I, [I, P, P, P, P, P, P, I, I, I, I, I, P, Z,
+                                            C.POINTER(GemvTile), P]),
+    "ternocl_int2_dequant": (I, [I, P, P, P, I, I, P]),
+    "ternocl_int2_gemv_decode": (I, [I, I, P, P, I, I, P]),
+}
+
+
+def declare(lib: C.CDLL) -> None:
+    for name, (res, args) in SYMBOLS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args

@@ -1,0 +1,151 @@
+// api.cpp -- the C ABI (include/ternocl_amd.h): host-side argument validation
+// and dispatch to the kernels of the other translation units.  Nothing here
+// allocates device memory or synchronises the stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+
+#include "common.hpp"
+
+namespace tcl {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char *msg) { std::snprintf(g_err, sizeof g_err, "%s", msg); }
+
+ternocl_status launch_status(hipError_t e) {
+    if (e == hipSuccess) return TERNOCL_OK;
+    std::snprintf(g_err, sizeof g_err, "HIP error %d: %s", (int)e, hipGetErrorString(e));
+    return TERNOCL_ERR_LAUNCH;
+}
+
+ternocl_status check_launch() { return launch_status(hipGetLastError()); }
+
+// kernels (int2_gemv.hip)
+ternocl_status int2_gemv_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
+                             const void *Other, const void *Bias, int M, int N, int K, int postop,
+                             int out_f32, int waves, int lc, hipStream_t st);
+ternocl_status int2_dequant_run(int dtype, const uint32_t *B, const void *S, void *W, int K, int N,
+                                hipStream_t st);
+ternocl_status int2_gemv_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N,
+                                    hipStream_t st);
+// kernels (int2_gemv_mfma.hip)
+ternocl_status int2_gemv_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
+                                  const void *Other, const void *Bias, int M, int N, int K,
+                                  int postop, int out_f32, int waves, int cpl, int gpw,
+                                  hipStream_t st);
+ternocl_status int2_mfma_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N,
+                                    hipStream_t st);
+// kernels (misc.hip)
+ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st);
+
+}  // namespace tcl
+
+using namespace tcl;
+
+#define FAIL(code, msg)          \
+    do {                         \
+        set_error(msg);          \
+        return (code);           \
+    } while (0)
+
+static ternocl_status check_dtype(int dtype) {
+    if (dtype != TERNOCL_FP16 && dtype != TERNOCL_BF16) FAIL(TERNOCL_ERR_INVALID_ARG, "dtype must be TERNOCL_FP16 or TERNOCL_BF16");
+    return TERNOCL_OK;
+}
+
+// Shared checks of the int2 / int8 / BITCOS GEMM family.
+static ternocl_status check_gemm_common(int dtype, const void *A, const void *B, const void *S,
+                                        const void *C, const void *Other, const void *Bias, int M,
+                                        int N, int K, int postop, int out_f32) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!A || !B || !S || !C) FAIL(TERNOCL_ERR_INVALID_ARG, "A, B, S and C must be non-null");
+    if (M < 1 || N < 1 || K < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "M, N and K must be positive");
+    if (N % 16) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "N must be a multiple of 16");
+    if (K % kGS) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "K must be a multiple of 128");
+    if (postop < 0 || postop > 5) FAIL(TERNOCL_ERR_INVALID_ARG, "postop must be 0..5");
+    if (out_f32 != 0 && out_f32 != 1) FAIL(TERNOCL_ERR_INVALID_ARG, "out_f32 must be 0 or 1");
+    if (postop_needs_other(postop) && !Other) FAIL(TERNOCL_ERR_INVALID_ARG, "this postop reads Other: it must be non-null");
+    if (postop_needs_bias(postop) && !Bias) FAIL(TERNOCL_ERR_INVALID_ARG, "this postop reads Bias: it must be non-null");
+    return TERNOCL_OK;
+}
+
+extern "C" {
+
+const char *ternocl_status_string(int status) {
+    switch (status) {
+    case TERNOCL_OK: return "ok";
+    case TERNOCL_ERR_INVALID_ARG: return "invalid argument";
+    case TERNOCL_ERR_UNSUPPORTED_SHAPE: return "unsupported shape";
+    case TERNOCL_ERR_WORKSPACE: return "workspace missing or too small";
+    case TERNOCL_ERR_LAUNCH: return "HIP launch error";
+    default: return "unknown status";
+    }
+}
+
+const char *ternocl_last_error(void) { return g_err; }
+const char *ternocl_version(void) { return "0.1.0"; }
+
+size_t ternocl_int2_gemm_ws_bytes(int M, int N, int K) {
+    (void)M; (void)N; (void)K;
+    return 0;  // no kernel of this build keeps scratch between launches
+}
+
+ternocl_status ternocl_workspace_zero(void *ws, size_t ws_bytes, void *stream) {
+    if (!ws || !ws_bytes) return TERNOCL_OK;
+    return fill_zero_run(ws, ws_bytes, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const uint32_t *B,
+                                               const void *S, void *C, const void *Other,
+                                               const void *Bias, int M, int N, int K, int postop,
+                                               int out_f32, void *ws, size_t ws_bytes,
+                                               const ternocl_gemv_tile *tile, void *stream) {
+    ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
+    if (s != TERNOCL_OK) return s;
+    (void)ws; (void)ws_bytes;
+    const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0};
+    if (t.engine < 0 || t.engine > 2) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0, 1 or 2");
+    if (M <= 16) {
+        if (t.engine == 1) {
+            if (M > 8) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the VALU GEMV takes M <= 8");
+            return int2_gemv_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,
+                                 t.col_lanes, (hipStream_t)stream);
+        }
+        return int2_gemv_mfma_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,
+                                  t.cols_per_lane, t.groups_per_wave, (hipStream_t)stream);
+    }
+    FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "M > 16 (the MFMA GEMM) is not available in this build");
+}
+
+ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
+                                            const void *S, void *C, const void *Other,
+                                            const void *Bias, int M, int N, int K, int postop,
+                                            int out_f32, void *ws, size_t ws_bytes, void *stream) {
+    return ternocl_int2_fp16_upcvt_gemm_ex(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32,
+                                           ws, ws_bytes, nullptr, stream);
+}
+
+ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
+                                    int N, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!B || !S || !W) FAIL(TERNOCL_ERR_INVALID_ARG, "B, S and W must be non-null");
+    if (N < 16 || N % 16 || K < kGS || K % kGS) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 128 == 0");
+    return int2_dequant_run(dtype, B, S, W, K, N, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,
+                                        int K, int N, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!B || !D) FAIL(TERNOCL_ERR_INVALID_ARG, "B and D must be non-null");
+    if (engine != 1 && engine != 2) FAIL(TERNOCL_ERR_INVALID_ARG, "engine must be 1 (VALU) or 2 (MFMA)");
+    if (N < 16 || N % 16 || K < 16 || K % 16) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 16 == 0");
+    if (engine == 2) return int2_mfma_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
+    return int2_gemv_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+// common.hpp -- device helpers shared by the gfx950 kernels: DT (fp16 / bf16)
+// conversions, the fused epilogue and host-side launch plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/ternocl_amd.h"
+
+namespace tcl {
+
+constexpr int kGS = 128;  // scale group size (K rows per scale)
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+
+// ---- DT conversions (round to nearest even), as common/dt16.hpp:18-42 ----
+
+template <bool BF16>
+__device__ __forceinline__ float dt2f(uint32_t h) {
+    if constexpr (BF16) {
+        return __uint_as_float(h << 16);
+    } else {
+        const uint16_t b = (uint16_t)h;
+        _Float16 x;
+        __builtin_memcpy(&x, &b, 2);
+        return (float)x;
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t f2dt(float f) {
+    if constexpr (BF16) {
+        uint32_t u = __float_as_uint(f);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // NaN
+        u += 0x7fffu + ((u >> 16) & 1u);
+        return u >> 16;
+    } else {
+        const _Float16 x = (_Float16)f;  // v_cvt_f16_f32, RTE
+        uint16_t b;
+        __builtin_memcpy(&b, &x, 2);
+        return b;
+    }
+}
+
+// ---- fused epilogue: common/epilogue.clh:22-48, common/epilogue.hpp:82 ----
+// postop 0 none, 1 silu(acc)*other, 2 acc+other, 3 acc+bias, 4 sigmoid,
+// 5 (acc+bias)+other (bias add + residual add, an extension).
+__device__ __forceinline__ float sigmoid_ref(float x) {
+    return x <= -10.0f ? 0.0f : 1.0f / (expf(-x) + 1.0f);
+}
+
+__device__ __forceinline__ float epi_apply(float v, int postop, float other, float bias) {
+    switch (postop) {
+    case 1: return v * sigmoid_ref(v) * other;
+    case 2: return v + other;
+    case 3: return v + bias;
+    case 4: return sigmoid_ref(v);
+    case 5: return (v + bias) + other;
+    default: return v;
+    }
+}
+
+__host__ __device__ constexpr bool postop_needs_other(int p) { return p == 1 || p == 2 || p == 5; }
+__host__ __device__ constexpr bool postop_needs_bias(int p) { return p == 3 || p == 5; }
+
+// Epilogue + store of 4 consecutive outputs (m, n..n+3), n % 4 == 0.
+template <bool BF16>
+__device__ __forceinline__ void epi_store4(void *C, const uint16_t *Other, const void *Bias,
+                                           int postop, int out_f32, int N, int m, int n,
+                                           const float v[4]) {
+    const size_t i = (size_t)m * N + n;
+    float o[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+    if (postop_needs_other(postop)) {
+        const uint2 t = *(const uint2 *)(Other + i);
+        o[0] = dt2f<BF16>(t.x & 0xffffu); o[1] = dt2f<BF16>(t.x >> 16);
+        o[2] = dt2f<BF16>(t.y & 0xffffu); o[3] = dt2f<BF16>(t.y >> 16);
+    }
+    if (postop_needs_bias(postop)) {
+        if (out_f32) {
+            const float4 t = *(const float4 *)((const float *)Bias + n);
+            b[0] = t.x; b[1] = t.y; b[2] = t.z; b[3] = t.w;
+        } else {
+            const uint2 t = *(const uint2 *)((const uint16_t *)Bias + n);
+            b[0] = dt2f<BF16>(t.x & 0xffffu); b[1] = dt2f<BF16>(t.x >> 16);
+            b[2] = dt2f<BF16>(t.y & 0xffffu); b[3] = dt2f<BF16>(t.y >> 16);
+        }
+    }
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = epi_apply(v[c], postop, o[c], b[c]);
+    if (out_f32) {
+        *(float4 *)((float *)C + i) = make_float4(r[0], r[1], r[2], r[3]);
+    } else {
+        uint2 t;
+        t.x = f2dt<BF16>(r[0]) | (f2dt<BF16>(r[1]) << 16);
+        t.y = f2dt<BF16>(r[2]) | (f2dt<BF16>(r[3]) << 16);
+        *(uint2 *)((uint16_t *)C + i) = t;
+    }
+}
+
+// Epilogue + store of one output (m, n).
+template <bool BF16>
+__device__ __forceinline__ void epi_store1(void *C, const uint16_t *Other, const void *Bias,
+                                           int postop, int out_f32, int N, int m, int n, float v) {
+    const size_t i = (size_t)m * N + n;
+    const float o = postop_needs_other(postop) ? dt2f<BF16>(Other[i]) : 0.0f;
+    float b = 0.0f;
+    if (postop_needs_bias(postop))
+        b = out_f32 ? ((const float *)Bias)[n] : dt2f<BF16>(((const uint16_t *)Bias)[n]);
+    const float r = epi_apply(v, postop, o, b);
+    if (out_f32) ((float *)C)[i] = r;
+    else ((uint16_t *)C)[i] = (uint16_t)f2dt<BF16>(r);
+}
+
+}  // namespace tcl
+
+// ---- host side ----------------------------------------------------------
+namespace tcl {
+// Records the HIP error text for ternocl_last_error() and maps it to a status.
+ternocl_status launch_status(hipError_t e);
+ternocl_status check_launch();
+void set_error(const char *msg);
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+}  // namespace tcl

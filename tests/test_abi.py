@@ -1,0 +1,73 @@
+"""The C ABI without a GPU: the header declares exactly the exported symbol
+table, the built library exports every symbol, and host-side argument checks
+return their status codes before any launch (int2_fp16_upcvt/main.cpp:159 is
+the reference's shape check, which exits instead)."""
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ternocl_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return set(re.findall(r"\b(ternocl_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_matches_symbol_table():
+    from ternocl_amd import _abi
+    assert _declared() == set(_abi.SYMBOLS), _declared() ^ set(_abi.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    import ternocl_amd as T
+    path = T.library_path()
+    assert path.exists(), "build the library first (python -m ternocl_amd.build)"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (ternocl_[a-z0-9_]+)", out))
+    missing = _declared() - exported
+    assert not missing, missing
+    T.lib()  # loads and binds every signature
+
+
+def test_header_compiles_as_c():
+    src = f'#include "{HEADER}"\nint main(void){{return TERNOCL_OK;}}\n'
+    r = subprocess.run(["gcc", "-x", "c", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def _call_gemm(L, **kw):
+    a = dict(dtype=0, A=1, B=1, S=1, C=1, Other=None, Bias=None, M=1, N=4096, K=4096,
+             postop=0, out_f32=0, ws=None, ws_bytes=0, stream=None)
+    a.update(kw)
+    return L.ternocl_int2_fp16_upcvt_gemm(*a.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(N=4100), 2), (dict(K=4000), 2), (dict(M=0), 2), (dict(dtype=7), 1),
+    (dict(A=None), 1), (dict(postop=6), 1), (dict(postop=1), 1), (dict(postop=3), 1),
+    (dict(out_f32=2), 1)])
+def test_host_validation(kw, status):
+    import ternocl_amd as T
+    L = T.lib()
+    assert _call_gemm(L, **kw) == status
+    assert L.ternocl_last_error().decode()
+
+
+def test_status_strings():
+    import ternocl_amd as T
+    L = T.lib()
+    assert L.ternocl_status_string(0) == b"ok"
+    assert L.ternocl_version().decode().count(".") == 2
+
+
+def test_ws_bytes_query():
+    import ternocl_amd as T
+    assert T.int2_gemm_ws_bytes(1, 14336, 4096) == 0  # the GEMV keeps no scratch

@@ -1,0 +1,215 @@
+"""GPU parity of the int2 upcvt path (decode GEMV, M <= 8) through the C ABI.
+
+Reference test design followed: int2_fp16_upcvt/validate.sh:8-10 (shape list,
+fp16 + bf16, distinct sets), validate_epilogues.sh:19-36 (POSTOP 0..4 x DT/fp32
+output x shapes), int2_fp16_upcvt/main.cpp:351-353 (every rotating set must
+reproduce set 0 bit for bit).  Golds: the oracle's restatement of
+compute_gold + epilogue_ref (int2_fp16_upcvt/main.cpp:79-98,
+common/epilogue.hpp:98-115).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from ternocl_amd import formats, synth
+from tests.gpu_util import allclose_report, dev_dt, dev_raw, host_f32, host_u16, host_u32, xetla_cmp
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(seed, M, K, N, bf16, ref_dist=False):
+    g = synth.rng(seed)
+    if ref_dist:  # the reference driver's distributions (int2_fp16_upcvt/main.cpp:236, :243)
+        A = formats.f32_to_dt(g.uniform(-5, 5, (M, K)).astype(np.float32), bf16)
+        S = synth.scales(g, K, N, bf16, 0.75, 15.75)
+    else:  # the workload's: A ~ N(0,1), S ~ U[0.005, 0.02]
+        A = synth.activations(g, (M, K), bf16)
+        S = synth.scales(g, K, N, bf16)
+    B = synth.int2_weights(g, K, N)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = (g.standard_normal(N).astype(np.float32) * 0.1)
+    return A, B, S, other, bias_f
+
+
+def _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32, ws=True, tile=None):
+    dA, dB, dS = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16)
+    dO = dev_dt(other, bf16)
+    if out_f32:
+        dBias = torch.from_numpy(bias_f).cuda()
+        dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    else:
+        dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+        dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+    wsb = T.int2_gemm_ws_bytes(M, N, K)
+    dW = None
+    if ws and wsb:
+        dW = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        T.workspace_zero(dW)
+    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, out_f32, ws=dW, tile=tile)
+    torch.cuda.synchronize()
+    return dC, dW
+
+
+def _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32):
+    acc = orc.int2_gold(A, B, S, M, K, N, bf16)
+    bias = bias_f if out_f32 else formats.f32_to_dt(bias_f, bf16)
+    return orc.epilogue(acc, other, bias, postop, out_f32, bf16), acc
+
+
+SHAPES = [(1, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (2, 4096, 14336), (4, 14336, 4096),
+          (8, 4096, 14336), (3, 256, 48), (1, 128, 16), (5, 1024, 272), (7, 384, 2064), (1, 17408, 5120),
+          (16, 4096, 4096), (13, 1024, 272), (11, 640, 48)]
+
+
+@pytest.mark.parametrize("engine", [1, 2])
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", SHAPES)
+def test_gemv_parity(dev, orc, M, K, N, bf16, engine):
+    import torch
+    import ternocl_amd as T
+    if engine == 1 and M > 8:
+        pytest.skip("the VALU GEMV takes M <= 8")
+    print(f"gemv parity M={M} K={K} N={N} bf16={bf16} engine={engine}", flush=True)
+    A, B, S, other, bias_f = _inputs(1000 + M + K + N, M, K, N, bf16)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, False, tile=T.gemv_tile(engine))
+    want, acc = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, False)
+    got = formats.dt_to_f32(host_u16(dC), bf16)
+    bad, dmax = allclose_report(got, formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("M,K,N", [(1, 5120, 4096), (3, 4096, 2048)])
+def test_gemv_epilogues(dev, orc, M, K, N, bf16, postop, out_f32):
+    import torch
+    import ternocl_amd as T
+    print(f"gemv epilogue M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32}", flush=True)
+    A, B, S, other, bias_f = _inputs(7 + postop, M, K, N, bf16)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32)
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32)
+    if out_f32:
+        got, ref = host_f32(dC), want
+    else:
+        got, ref = formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16)
+    bad, dmax = allclose_report(got, ref)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemv_reference_distribution_rule(dev, orc, bf16):
+    """The reference driver's own inputs and pass rule (xetla_buff_cmp)."""
+    import torch
+    import ternocl_amd as T
+    M, K, N = 1, 5120, 4096
+    A, B, S, other, bias_f = _inputs(99, M, K, N, bf16, ref_dist=True)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, False)
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, False)
+    assert xetla_cmp(host_u16(dC), want, bf16) == 0
+
+
+TILES = [(1, 1, 0, 0, 4), (1, 3, 0, 0, 4), (1, 4, 0, 0, 4), (1, 1, 0, 0, 8), (1, 5, 0, 0, 8),
+         (1, 8, 0, 0, 8), (1, 2, 0, 0, 16), (1, 8, 0, 0, 16), (1, 0, 0, 0, 0),
+         (2, 1, 1, 1, 0), (2, 8, 1, 1, 0), (2, 4, 2, 1, 0), (2, 8, 2, 2, 0), (2, 2, 1, 4, 0),
+         (2, 8, 2, 4, 0), (2, 3, 2, 2, 0), (2, 0, 0, 0, 0), (0, 0, 0, 0, 0)]
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_gemv_tiles_deterministic(dev, orc, tile):
+    """Every tile (engine, waves, cols/lane, groups/wave, col_lanes) gives the
+    gold, and repeated calls are bit-identical (the K reduction has a fixed order)."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, bf16 = 2, 3840, 1024, False
+    A, B, S, other, bias_f = _inputs(5, M, K, N, bf16)
+    outs = []
+    for _ in range(3):
+        dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, False, tile=T.gemv_tile(*tile))
+        outs.append(host_u16(dC))
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(outs[0], bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"tile {tile}: {bad} bad (max |d| {dmax})"
+    assert all(np.array_equal(outs[0], o) for o in outs[1:]), "non-deterministic"
+
+
+def test_gemv_plan_too_big_for_lds_is_rejected(dev):
+    import torch
+    import ternocl_amd as T
+    M, K, N = 2, 3840, 1024
+    A = torch.zeros((M, K), dtype=torch.float16, device="cuda")
+    B = torch.zeros((K // 16, N), dtype=torch.int32, device="cuda")
+    S = torch.zeros((K // 128, N), dtype=torch.float16, device="cuda")
+    C = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(A, B, S, C, None, None, M, N, K, tile=T.gemv_tile(1, 16, 0, 0, 4))
+    assert e.value.status == 1
+    with pytest.raises(T.TernoclError):  # M > 8 on the VALU engine
+        T.int2_fp16_upcvt_gemm(A.repeat(5, 1), B, S, C.repeat(5, 1), None, None, 10, N, K,
+                               tile=T.gemv_tile(1))
+
+
+@pytest.mark.parametrize("M,tile", [(1, (1, 2, 0, 0, 16)), (8, (1, 2, 0, 0, 16)), (8, (2, 0, 0, 0, 0)),
+                                    (16, (2, 0, 0, 0, 0)), (3, (2, 2, 1, 1, 0))])
+def test_gemv_multi_window(dev, orc, M, tile):
+    """K long enough for several LDS rounds / windows (double-buffered staging)."""
+    import torch
+    import ternocl_amd as T
+    K, N, bf16 = 40960, 64, True
+    A, B, S, other, bias_f = _inputs(11, M, K, N, bf16)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, False, tile=T.gemv_tile(*tile))
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, False)
+    bad, _ = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_int2_dequant_bit_exact(dev, orc, bf16):
+    """The reference B-operand unpack (dq_word): +0 / +s / s^0x8000, bit for bit."""
+    import torch
+    import ternocl_amd as T
+    K, N = 512, 272
+    g = synth.rng(3)
+    B = synth.int2_weights(g, K, N)
+    S = synth.scales(g, K, N, bf16)
+    dW = torch.empty((K, N), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    T.int2_dequant(dev_raw(B), dev_dt(S, bf16), dW, K, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(dW), orc.int2_dequant(B, S, K, N))
+
+
+@pytest.mark.parametrize("engine", [1, 2])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemv_decode_bit_exact(dev, bf16, engine):
+    """Each GEMV's own in-register unpack, bit for bit against its closed form:
+    dword = DT(BASE + (v+2) * 2^p) for two rows of the word (low / high half),
+    and every half decodes back to the signed weight."""
+    import torch
+    import ternocl_amd as T
+    K, N = 256, 64
+    g = synth.rng(4)
+    B = synth.int2_weights(g, K, N)
+    B[0, :16] = np.arange(16, dtype=np.uint32) * 0x11111111  # every code in every field
+    D = torch.empty(((K // 16) * N * 8,), dtype=torch.int32, device="cuda")
+    T.int2_gemv_decode(dev_raw(B), D, K, N, bf16, engine=engine)
+    torch.cuda.synchronize()
+    got = host_u32(D).reshape(K // 16, N, 8)
+    codes = (B[..., None] >> (2 * np.arange(16, dtype=np.uint32))) & 3  # [K/16, N, 16]
+    x = (codes ^ 2).astype(np.uint32)
+    if engine == 1:  # pair j = rows (j, j+8)
+        rows = list(range(8))
+        shifts = [0, 2, 4, 0, 2, 4, 0, 2] if bf16 else [0, 2, 4, 6, 8, 2, 4, 6]
+    else:  # dword 4h+i = rows (4h+i, 4h+i+8)
+        rows = list(range(8))
+        shifts = ([0, 2, 4, 5] if bf16 else [0, 2, 4, 6]) * 2
+    base = 0x4300 if bf16 else 0x6400
+    for d, (j, p) in enumerate(zip(rows, shifts)):
+        want = (base | (x[..., j] << p)) | ((base | (x[..., j + 8] << p)) << 16)
+        assert np.array_equal(got[..., d], want.astype(np.uint32)), f"dword {d}"
+    sv = formats.unpack_int2(B, K).reshape(K // 16, 16, N).transpose(0, 2, 1)
+    for d, (j, p) in enumerate(zip(rows, shifts)):
+        for half, row in ((0, j), (1, j + 8)):
+            vals = formats.dt_to_f32(((got[..., d] >> (16 * half)) & 0xFFFF).astype(np.uint16), bf16)
+            v = (vals - (128.0 if bf16 else 1024.0)) / 2.0 ** p - 2
+            assert np.array_equal(v.astype(np.int8), sv[..., row])
