@@ -198,7 +198,7 @@ template <int CPL, int GPW> struct Slab {
 // MR: staged activation rows (power of two >= M), CPL: words (columns) per
 // lane, GPW: groups per wave per window.  W = blockDim.x / 64 waves; a window
 // is W * GPW groups.
-__host__ __device__ constexpr int mf_max_waves(int MR) { return MR <= 4 ? 16 : 8; }
+__host__ __device__ constexpr int mf_max_waves(int) { return 8; }  // 16-wave workgroups measured slower
 
 template <int MR, int CPL, int GPW, bool BF16>
 __global__ void __launch_bounds__(64 * mf_max_waves(MR))
@@ -337,16 +337,16 @@ MfPlan mf_plan(int M, int N, int K, int waves, int cpl, int gpw) {
     } else {
         long best = LONG_MIN;
         for (int g : {1, 2, 4, 8, 16}) {
-            if (gpw > 0 && g != gpw) continue;
-            if (MR * g > 16) continue;  // staging registers: MR * GPW / 4 quads per thread
-            // automatic plans stop at 8 waves (16-wave workgroups measured slower)
-            for (int w = 1; w <= (waves > 0 ? mf_max_waves(MR) : 8); ++w) {
+            if (gpw > 0 ? g != gpw : g > 4) continue;  // automatic: <= 4 groups per wave (measured best)
+            if (MR * g > 16) continue;     // staging registers: MR * GPW / 4 quads per thread
+            if (p.cpl * g > 16) continue;  // weight registers: 2 * CPL * GPW words per lane
+            for (int w = 1; w <= 8; ++w) {
                 if (waves > 0 && w != waves) continue;
                 if (mf_lds(MR, w, g, p.cpl, groups) > kMfMaxLds) continue;
                 const int gw = w * g, windows = (groups + gw - 1) / gw;
                 const int idle = windows * gw - groups;
-                // fewest windows, then fewest idle group slots, then more waves
-                const long score = -(long)windows * 1000000 - (long)idle * 1000 + w * 10 - g;
+                // fewest idle group slots, then fewest windows, then more waves
+                const long score = -(long)idle * 100000 - (long)windows * 100 + w;
                 if (score > best) { best = score; bw = w; bg = g; }
             }
         }
@@ -381,7 +381,7 @@ hipError_t mf_launch_g(const MfPlan &p, const void *A, const uint32_t *B, const 
         if constexpr (MR <= 2) return mf_launch_t<MR, CPL, 8, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         return hipErrorInvalidValue;
     default:
-        if constexpr (MR == 1) return mf_launch_t<MR, CPL, 16, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        if constexpr (MR == 1 && CPL == 1) return mf_launch_t<MR, CPL, 16, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         return hipErrorInvalidValue;
     }
 }
@@ -439,12 +439,13 @@ ternocl_status int2_gemv_mfma_run(int dtype, const void *A, const uint32_t *B, c
         set_error("groups_per_wave must be 0 (automatic), 1, 2, 4, 8 or 16");
         return TERNOCL_ERR_INVALID_ARG;
     }
-    if (gpw * mf_mr(M) > 16) {
-        set_error("groups_per_wave * (M rounded up to a power of two) must be <= 16");
+    if (gpw * mf_mr(M) > 16 || gpw * (cpl ? cpl : 1) > 16) {
+        set_error("groups_per_wave * (M rounded up to a power of two) and groups_per_wave * "
+                  "cols_per_lane must be <= 16");
         return TERNOCL_ERR_INVALID_ARG;
     }
     if (waves < 0 || waves > mf_max_waves(mf_mr(M))) {
-        set_error("waves must be 0 (automatic) .. 16 for M <= 4, .. 8 for M = 5..16");
+        set_error("waves must be 0 (automatic) .. 8");
         return TERNOCL_ERR_INVALID_ARG;
     }
     const MfPlan p = mf_plan(M, N, K, waves, cpl, gpw);
