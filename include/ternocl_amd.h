@@ -70,7 +70,8 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint
 /* Decode-GEMV tile, the reference's -DSGM/-DNSG_N/-DLS/-DU knobs for this
  * hardware.  Every field 0 = automatic. */
 typedef struct {
-    int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: MFMA GEMV (M <= 16) */
+    int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: MFMA GEMV (M <= 16);
+                            3: MFMA prefill GEMM (any M, 128 x 128 tiles; the M > 16 engine) */
     int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
     int cols_per_lane;   /* MFMA: adjacent columns per lane, 1 or 2 (16- or 32-column strips) */
     int groups_per_wave; /* MFMA: 128-row groups per wave per LDS window, 1..16 (power of
@@ -78,8 +79,9 @@ typedef struct {
     int col_lanes;       /* VALU: lanes across a strip of 4*col_lanes columns, 4, 8 or 16 */
 } ternocl_gemv_tile;
 
-/* Same as ternocl_int2_fp16_upcvt_gemm with an explicit GEMV tile (NULL = automatic).
- * The tile is ignored when M > 16. */
+/* Same as ternocl_int2_fp16_upcvt_gemm with an explicit tile (NULL = automatic:
+ * the MFMA GEMV for M <= 16, the prefill GEMM above).  When M > 16 the engine
+ * must be 0 or 3. */
 ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const uint32_t *B,
                                                const void *S, void *C, const void *Other,
                                                const void *Bias, int M, int N, int K,
@@ -94,7 +96,8 @@ ternocl_status ternocl_workspace_zero(void *ws, size_t ws_bytes, void *stream);
  * int2_fp16_upcvt.cl:118-150): W[k][n] = +0 / S / S^0x8000 for codes 0 / 1 / 3,
  * W is DT [K, N].  The GEMVs' own in-register decodes are exported for testing
  * too: ternocl_int2_gemv_decode writes, per B word, the 8 packed DT pairs that
- * engine (1 = VALU, 2 = MFMA) builds (layout [K/16][N][8] uint32). */
+ * engine (1 = VALU GEMV, 2 = MFMA GEMV, 3 = prefill GEMM) builds (layout
+ * [K/16][N][8] uint32). */
 ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
                                     int N, void *stream);
 ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,

@@ -22,7 +22,7 @@ from . import _abi
 __all__ = [
     "TernoclError", "lib", "library_path", "FP16", "BF16",
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
-    "int2_gemv_decode", "gemv_tile", "GemvTile", "VALU", "MFMA",
+    "int2_gemv_decode", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
 ]
 
 FP16, BF16 = 0, 1
@@ -105,7 +105,7 @@ def workspace_zero(ws, stream=None) -> None:
 
 
 GemvTile = _abi.GemvTile
-VALU, MFMA = 1, 2
+VALU, MFMA, GEMM = 1, 2, 3  # engines: VALU GEMV, MFMA GEMV, MFMA prefill GEMM
 
 
 def gemv_tile(engine: int = 0, waves: int = 0, cols_per_lane: int = 0, groups_per_wave: int = 0,
@@ -134,6 +134,6 @@ def int2_dequant(B, S, W, K: int, N: int, stream=None) -> None:
 
 
 def int2_gemv_decode(B, D, K: int, N: int, bf16: bool, engine: int = MFMA, stream=None) -> None:
-    """D[word][j] = the packed DT pair j a GEMV engine builds from each B word (test hook)."""
+    """D[word][j] = the packed DT pair j an engine builds from each B word (test hook)."""
     _check(lib().ternocl_int2_gemv_decode(BF16 if bf16 else FP16, engine, _ptr(B), _ptr(D), K, N,
                                           _stream(stream)))

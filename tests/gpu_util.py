@@ -60,3 +60,47 @@ def xetla_cmp(got_bits: np.ndarray, ref_bits: np.ndarray, bf16: bool, abs_tol=No
         rel = np.abs((des - act) / des)
     ok = (d <= abs_tol) | (ulp <= ulp_tol) | (rel <= 1e-3)
     return int((~ok).sum())
+
+
+# ---- int2 upcvt GEMM inputs / launch / gold, shared by the GEMV and GEMM tests ----
+
+def int2_inputs(seed, M, K, N, bf16, ref_dist=False):
+    from ternocl_amd import formats, synth
+    g = synth.rng(seed)
+    if ref_dist:  # the reference driver's distributions (int2_fp16_upcvt/main.cpp:236, :243)
+        A = formats.f32_to_dt(g.uniform(-5, 5, (M, K)).astype(np.float32), bf16)
+        S = synth.scales(g, K, N, bf16, 0.75, 15.75)
+    else:  # the workload's: A ~ N(0,1), S ~ U[0.005, 0.02]
+        A = synth.activations(g, (M, K), bf16)
+        S = synth.scales(g, K, N, bf16)
+    B = synth.int2_weights(g, K, N)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = (g.standard_normal(N).astype(np.float32) * 0.1)
+    return A, B, S, other, bias_f
+
+
+def int2_run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32, ws=True, tile=None):
+    from ternocl_amd import formats
+    dA, dB, dS = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16)
+    dO = dev_dt(other, bf16)
+    if out_f32:
+        dBias = torch.from_numpy(bias_f).cuda()
+        dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    else:
+        dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+        dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+    wsb = T.int2_gemm_ws_bytes(M, N, K)
+    dW = None
+    if ws and wsb:
+        dW = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        T.workspace_zero(dW)
+    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, out_f32, ws=dW, tile=tile)
+    torch.cuda.synchronize()
+    return dC, dW
+
+
+def int2_gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32):
+    from ternocl_amd import formats
+    acc = orc.int2_gold(A, B, S, M, K, N, bf16)
+    bias = bias_f if out_f32 else formats.f32_to_dt(bias_f, bf16)
+    return orc.epilogue(acc, other, bias, postop, out_f32, bf16), acc

@@ -14,47 +14,9 @@ import pytest
 
 from ternocl_amd import formats, synth
 from tests.gpu_util import allclose_report, dev_dt, dev_raw, host_f32, host_u16, host_u32, xetla_cmp
+from tests.gpu_util import int2_gold as _gold, int2_inputs as _inputs, int2_run as _run
 
 pytestmark = pytest.mark.gpu
-
-
-def _inputs(seed, M, K, N, bf16, ref_dist=False):
-    g = synth.rng(seed)
-    if ref_dist:  # the reference driver's distributions (int2_fp16_upcvt/main.cpp:236, :243)
-        A = formats.f32_to_dt(g.uniform(-5, 5, (M, K)).astype(np.float32), bf16)
-        S = synth.scales(g, K, N, bf16, 0.75, 15.75)
-    else:  # the workload's: A ~ N(0,1), S ~ U[0.005, 0.02]
-        A = synth.activations(g, (M, K), bf16)
-        S = synth.scales(g, K, N, bf16)
-    B = synth.int2_weights(g, K, N)
-    other = synth.activations(g, (M, N), bf16)
-    bias_f = (g.standard_normal(N).astype(np.float32) * 0.1)
-    return A, B, S, other, bias_f
-
-
-def _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32, ws=True, tile=None):
-    dA, dB, dS = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16)
-    dO = dev_dt(other, bf16)
-    if out_f32:
-        dBias = torch.from_numpy(bias_f).cuda()
-        dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
-    else:
-        dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
-        dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
-    wsb = T.int2_gemm_ws_bytes(M, N, K)
-    dW = None
-    if ws and wsb:
-        dW = torch.empty(wsb, dtype=torch.uint8, device="cuda")
-        T.workspace_zero(dW)
-    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, out_f32, ws=dW, tile=tile)
-    torch.cuda.synchronize()
-    return dC, dW
-
-
-def _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32):
-    acc = orc.int2_gold(A, B, S, M, K, N, bf16)
-    bias = bias_f if out_f32 else formats.f32_to_dt(bias_f, bf16)
-    return orc.epilogue(acc, other, bias, postop, out_f32, bf16), acc
 
 
 SHAPES = [(1, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (2, 4096, 14336), (4, 14336, 4096),
