@@ -22,8 +22,11 @@
  *                           postop 0..4 x {DT, fp32}; postop 5 (bias + residual)
  *                           is an extension: parity unpinned against the reference.
  *   orc_scale_a/quant_a     bit-identical to the compiled compute_scale_a and the
- *                           lrintf quantization; closed-form checks (RTE ties,
- *                           saturation, FLT_EPSILON floor).
+ *                           lrintf quantization for finite products; closed-form
+ *                           checks (RTE ties, saturation, FLT_EPSILON floor).
+ *                           Infinite / NaN products (fp16 SA = inf) follow the
+ *                           reference device kernel's saturating conversion
+ *                           (closed-form test), not the host's undefined lrintf.
  *   orc_int8_gold           bit-identical to the compiled compute_gold
  *                           (int2_via_int2_x_int8_dpas/main.cpp:94-121).
  *   orc_bitcos_*            pack/decode round trip; slice ranks and decode and
@@ -184,9 +187,18 @@ void orc_quant_a(int bf16, const uint16_t *A, const uint16_t *SA, int8_t *Aq, in
 #pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m)
         for (int k = 0; k < K; ++k) {
-            long v = lrintf(orc_tof(A[(size_t)m * K + k], bf16) *
-                            orc_tof(SA[(size_t)(k / GS) * orc_ldsa(M) + m], bf16));
-            v = v > 127L ? 127L : (v < -128L ? -128L : v);
+            const float p = orc_tof(A[(size_t)m * K + k], bf16) *
+                            orc_tof(SA[(size_t)(k / GS) * orc_ldsa(M) + m], bf16);
+            /* lrintf + clamp to [-128, 127] as main.cpp:101-102 for every finite
+             * product; a product of +-inf (fp16 SA overflows to inf when a
+             * group's absmax is below 127 / 65504) saturates and NaN (0 * inf)
+             * gives 0, as the reference device kernel's convert_char8_sat_rte
+             * (int2_int8_dpas.cl:120) does: lrintf is undefined there. */
+            long v;
+            if (p != p) v = 0;
+            else if (p >= 127.0f) v = 127;
+            else if (p <= -128.0f) v = -128;
+            else v = lrintf(p);
             Aq[(size_t)m * K + k] = (int8_t)v;
         }
 }

@@ -23,6 +23,7 @@ __all__ = [
     "TernoclError", "lib", "library_path", "FP16", "BF16",
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
     "int2_gemv_decode", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
+    "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
 ]
 
 FP16, BF16 = 0, 1
@@ -137,3 +138,30 @@ def int2_gemv_decode(B, D, K: int, N: int, bf16: bool, engine: int = MFMA, strea
     """D[word][j] = the packed DT pair j an engine builds from each B word (test hook)."""
     _check(lib().ternocl_int2_gemv_decode(BF16 if bf16 else FP16, engine, _ptr(B), _ptr(D), K, N,
                                           _stream(stream)))
+
+
+# ---- int2 x int8 (int2_via_int2_x_int8_dpas/int2_int8_dpas.cl) ------------
+
+def ldsa(M: int) -> int:
+    """Row pitch of SA, (M + 31) & ~31 (LDSA of int2_int8_dpas.cl:58)."""
+    return lib().ternocl_ldsa(M)
+
+
+def quant_a(A, SA, Aq, M: int, K: int, stream=None) -> None:
+    """quant_a(A, SA, Aq, M, K) of int2_int8_dpas.cl:105: SA [K/128, ldsa(M)] DT scales
+    and Aq [M, K] int8, bit-exact with the reference's host quantization."""
+    _check(lib().ternocl_quant_a(_dtype_of(A), _ptr(A), _ptr(SA), _ptr(Aq), M, K, _stream(stream)))
+
+
+def int2_int8_gemm(A, Aq, SA, B, SB, C, Other, Bias, M: int, N: int, K: int, postop: int = 0,
+                   out_f32: bool = False, stream=None) -> None:
+    """int2_int8_gemm_mt(A, Aq, SA, B, SB, C, Other, Bias, M, N, K) of int2_int8_dpas.cl:316
+    in upfront mode (A is not read and may be None; the dtype comes from SB)."""
+    _check(lib().ternocl_int2_int8_gemm(_dtype_of(SB), _ptr(A), _ptr(Aq), _ptr(SA), _ptr(B), _ptr(SB),
+                                        _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                        int(bool(out_f32)), _stream(stream)))
+
+
+def int2_s8_decode(B, D, K: int, N: int, stream=None) -> None:
+    """D[word][i] = the s8 x s2 GEMM's B fragment dwords of each word (test hook)."""
+    _check(lib().ternocl_int2_s8_decode(_ptr(B), _ptr(D), K, N, _stream(stream)))

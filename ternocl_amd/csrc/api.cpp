@@ -42,6 +42,12 @@ ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, c
                                   const void *Other, const void *Bias, int M, int N, int K,
                                   int postop, int out_f32, hipStream_t st);
 ternocl_status int2_gemm_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
+// kernels (int2_int8.hip)
+ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st);
+ternocl_status int2_int8_gemm_run(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
+                                  const void *SB, void *C, const void *Other, const void *Bias, int M,
+                                  int N, int K, int postop, int out_f32, hipStream_t st);
+ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (misc.hip)
 ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st);
 
@@ -155,6 +161,35 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
     if (engine == 3) return int2_gemm_decode_run(B, D, K, N, (hipStream_t)stream);
     if (engine == 2) return int2_mfma_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     return int2_gemv_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
+}
+
+int ternocl_ldsa(int M) { return (M + 31) & ~31; }
+
+ternocl_status ternocl_quant_a(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K,
+                               void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!A || !SA || !Aq) FAIL(TERNOCL_ERR_INVALID_ARG, "A, SA and Aq must be non-null");
+    if (M < 1 || K < kGS || K % kGS) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need M >= 1 and K % 128 == 0");
+    return quant_a_run(dtype, A, SA, Aq, M, K, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                      const uint32_t *B, const void *SB, void *C,
+                                      const void *Other, const void *Bias, int M, int N, int K,
+                                      int postop, int out_f32, void *stream) {
+    (void)A;  // the in-GEMM quantization mode is not built: Aq is required
+    if (!Aq) FAIL(TERNOCL_ERR_INVALID_ARG, "Aq must be non-null (quantize A with ternocl_quant_a)");
+    ternocl_status s = check_gemm_common(dtype, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32);
+    if (s != TERNOCL_OK) return s;
+    return int2_int8_gemm_run(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
+                              (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_s8_decode(const uint32_t *B, uint32_t *D, int K, int N, void *stream) {
+    if (!B || !D) FAIL(TERNOCL_ERR_INVALID_ARG, "B and D must be non-null");
+    if (N < 16 || N % 16 || K < 16 || K % 16) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 16 == 0");
+    return int2_s8_decode_run(B, D, K, N, (hipStream_t)stream);
 }
 
 }  // extern "C"

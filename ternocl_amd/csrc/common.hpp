@@ -114,6 +114,22 @@ __device__ __forceinline__ void epi_store1(void *C, const uint16_t *Other, const
     else ((uint16_t *)C)[i] = (uint16_t)f2dt<BF16>(r);
 }
 
+// Workgroup -> (m tile, n tile) of a GEMM grid of mt x nt tiles.  Workgroups
+// are dealt to the 8 XCDs round-robin (x, x+8, x+16, ... run on XCD x); those
+// take all M tiles of column strip x, then of strip x+8, ... (when the strip
+// count is a multiple of 8), so a strip's weights are fetched into one XCD's
+// L2 once.
+__device__ __forceinline__ void xcd_tile_of(int id, int mt, int nt, int &tm, int &tn) {
+    if (nt % 8 == 0) {
+        const int x = id & 7, r = id >> 3;
+        tm = r % mt;
+        tn = (r / mt) * 8 + x;
+    } else {
+        tm = id % mt;
+        tn = id / mt;
+    }
+}
+
 }  // namespace tcl
 
 // ---- host side ----------------------------------------------------------

@@ -204,20 +204,6 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint
     }
 }
 
-// Workgroup -> (m tile, n tile): with 8 XCDs served round-robin, workgroups
-// x, x+8, x+16, ... run on XCD x; they take all M tiles of column strip x,
-// then of strip x+8, ... (when the strip count is a multiple of 8).
-__device__ __forceinline__ void tile_of(int id, int mt, int nt, int &tm, int &tn) {
-    if (nt % 8 == 0) {
-        const int x = id & 7, r = id >> 3;
-        tm = r % mt;
-        tn = (r / mt) * 8 + x;
-    } else {
-        tm = id % mt;
-        tn = id / mt;
-    }
-}
-
 template <bool BF16>
 __global__ void __launch_bounds__(256)
 k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
@@ -226,7 +212,7 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BM * A_PITCH];  // 68 KiB
     const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     int tm, tn;
-    tile_of(blockIdx.x, mt, nt, tm, tn);
+    xcd_tile_of(blockIdx.x, mt, nt, tm, tn);
     const ARows ar{A + (size_t)tm * BM * K, nullptr, 1};
     const int mrows = min(BM, M - tm * BM);
     gemm_tile<BF16>(ar, mrows, B, S, C, Other, Bias, tm * BM, N, K, tn * BN, postop, out_f32, lds);

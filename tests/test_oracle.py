@@ -159,6 +159,21 @@ def test_quant_rte_and_saturation(orc):
     assert q2[0, 0] == 127 and q2[0, 7] == -128
 
 
+def test_quant_overflowing_fp16_scale_saturates(orc):
+    """fp16 group with absmax < 127/65504: SA = inf, so a * SA is +-inf (saturate
+    to 127 / -128) or NaN for a = 0 (-> 0), the device kernel's
+    convert_char8_sat_rte semantics (int2_int8_dpas.cl:120)."""
+    M, K = 1, 128
+    A = np.zeros((M, K), np.float32)
+    A[0, :3] = [1e-3, -1e-3, 0.0]
+    Ah = formats.f32_to_dt(A, False)
+    SA = orc.scale_a(Ah, M, K, False)
+    assert SA[0, 0] == 0x7C00  # +inf
+    q = orc.quant_a(Ah, SA, M, K, False)
+    assert list(q[0, :3]) == [127, -128, 0]
+    assert (q[0, 3:] == 0).all()
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_int8_gold_vs_float64(orc, bf16):
     M, K, N = 4, 384, 32
