@@ -135,6 +135,47 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
  * of the word (the k order the GEMM uses for both operands). */
 ternocl_status ternocl_int2_s8_decode(const uint32_t *B, uint32_t *D, int K, int N, void *stream);
 
+/* ---- BITCOS (presence bitmap + compacted signs) GEMV --------------------
+ * Replaces bitcos_fp16_upcvt_gemv / _gemm_mt (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:179-181,
+ * :303-305):  C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(k,n))).
+ * B: the BITCOS buffer of common/bitcos.hpp, uint32 words
+ *   bitmap [K/32][N] | offsets [N] | per-column sign streams | 4 pad words
+ * (bit c of bitmap word (kp, n) = row 32kp+c of column n is non-zero; a sign
+ * bit of 1 = -1, in k order per column).  SR: slice ranks [ls-1][N] for ls K
+ * slices (common/bitcos.hpp:81-94; ternocl_bitcos_slice_ranks computes them
+ * on the device), may be NULL when ls == 1.  The kernel splits K into exactly
+ * ls slices.  Constraints: N % 16 == 0, K % 128 == 0, 1 <= ls <= 16,
+ * K % (64 * ls) == 0.  M <= 4 per pass (larger M runs ceil(M/4) passes over
+ * the weights). */
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
+                                              const void *S, const uint32_t *SR, int ls, void *C,
+                                              const void *Other, const void *Bias, int M, int N,
+                                              int K, int postop, int out_f32, void *stream);
+/* Slice ranks of a BITCOS buffer for ls slices: SR[(s-1)*N + n] = non-zeros of
+ * column n in bitmap words kp < s * ceil(K/ls) / 32 (common/bitcos.hpp:81-94). */
+ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K, int N, int ls,
+                                          void *stream);
+/* A slice count for ternocl_bitcos_fp16_upcvt_gemm at this shape (the largest
+ * ls <= 16 with K % (64 * ls) == 0 that keeps >= 6 sixty-four-row chunks per slice). */
+int ternocl_bitcos_pick_ls(int M, int N, int K);
+/* Bit-exact test hook of the BITCOS decode: W[k][n] = 0 / S / S ^ 0x8000 for
+ * code 0 / +1 / -1 (the B operand the reference builds, bitcos_fp16_upcvt.cl:153-175),
+ * W DT [K, N]. */
+ternocl_status ternocl_bitcos_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
+                                      int N, void *stream);
+
+/* ---- Hadamard input transform -------------------------------------------
+ * Replaces hadamard_fwht(x, signs, y, K, use_signs) (hadamard/hadamard_fwht.cl:62-64)
+ * with -DHB as an argument and the row count explicit:
+ *   y = DT(SCALE * H_HB(s .* x)) per HB-wide block along K of x DT [rows, K],
+ * fp32 butterflies in the reference's stage order (bit-identical), SCALE =
+ * 1/sqrt(HB).  signs: int8 [K] (+1 / -1 per in-row position), read when
+ * use_signs != 0.  HB: a power of two in [256, 4096].  K % HB may be non-zero
+ * when it is a power of two: that tail is transformed as one block of its own
+ * size (the reference leaves it unwritten). */
+ternocl_status ternocl_hadamard_fwht(int dtype, const void *x, const int8_t *signs, void *y,
+                                     int rows, int K, int HB, int use_signs, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

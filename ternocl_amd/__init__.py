@@ -24,6 +24,8 @@ __all__ = [
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
     "int2_gemv_decode", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
     "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
+    "bitcos_fp16_upcvt_gemm", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
+    "hadamard_fwht",
 ]
 
 FP16, BF16 = 0, 1
@@ -165,3 +167,36 @@ def int2_int8_gemm(A, Aq, SA, B, SB, C, Other, Bias, M: int, N: int, K: int, pos
 def int2_s8_decode(B, D, K: int, N: int, stream=None) -> None:
     """D[word][i] = the s8 x s2 GEMM's B fragment dwords of each word (test hook)."""
     _check(lib().ternocl_int2_s8_decode(_ptr(B), _ptr(D), K, N, _stream(stream)))
+
+
+# ---- BITCOS (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl) ------------------------
+
+def bitcos_fp16_upcvt_gemm(A, B, S, SR, C, Other, Bias, M: int, N: int, K: int, ls: int = 1,
+                           postop: int = 0, out_f32: bool = False, stream=None) -> None:
+    """bitcos_fp16_upcvt_gemv(A, B, S, SR, C, Other, Bias, M, N, K) of
+    bitcos_fp16_upcvt.cl:179 with LS = ls K slices (SR computed for that ls)."""
+    _check(lib().ternocl_bitcos_fp16_upcvt_gemm(_dtype_of(A), _ptr(A), _ptr(B), _ptr(S), _ptr(SR), ls,
+                                                _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                                int(bool(out_f32)), _stream(stream)))
+
+
+def bitcos_slice_ranks(B, SR, K: int, N: int, ls: int, stream=None) -> None:
+    """SR [ls-1, N] slice ranks of a BITCOS buffer (common/bitcos.hpp:81-94), on the device."""
+    _check(lib().ternocl_bitcos_slice_ranks(_ptr(B), _ptr(SR), K, N, ls, _stream(stream)))
+
+
+def bitcos_pick_ls(M: int, N: int, K: int) -> int:
+    return lib().ternocl_bitcos_pick_ls(M, N, K)
+
+
+def bitcos_dequant(B, S, W, K: int, N: int, stream=None) -> None:
+    """W = the DT B operand of the BITCOS kernels (0 / S / S^0x8000), test hook."""
+    _check(lib().ternocl_bitcos_dequant(_dtype_of(W), _ptr(B), _ptr(S), _ptr(W), K, N, _stream(stream)))
+
+
+# ---- Hadamard (hadamard/hadamard_fwht.cl) ------------------------------------
+
+def hadamard_fwht(x, signs, y, rows: int, K: int, HB: int, use_signs: bool = True, stream=None) -> None:
+    """hadamard_fwht(x, signs, y, K, use_signs) of hadamard_fwht.cl:63 with -DHB=HB over rows rows."""
+    _check(lib().ternocl_hadamard_fwht(_dtype_of(x), _ptr(x), _ptr(signs), _ptr(y), rows, K, HB,
+                                       int(bool(use_signs)), _stream(stream)))

@@ -34,6 +34,11 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_quant_a": (I, [I, P, P, P, I, I, P]),
     "ternocl_int2_int8_gemm": (I, [I, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "ternocl_int2_s8_decode": (I, [P, P, I, I, P]),
+    "ternocl_bitcos_fp16_upcvt_gemm": (I, [I, P, P, P, P, I, P, P, P, I, I, I, I, I, P]),
+    "ternocl_bitcos_slice_ranks": (I, [P, P, I, I, I, P]),
+    "ternocl_bitcos_pick_ls": (I, [I, I, I]),
+    "ternocl_bitcos_dequant": (I, [I, P, P, P, I, I, P]),
+    "ternocl_hadamard_fwht": (I, [I, P, P, P, I, I, I, I, P]),
 }
 
 

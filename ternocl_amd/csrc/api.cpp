@@ -3,6 +3,7 @@
 // allocates device memory or synchronises the stream.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 
@@ -48,6 +49,18 @@ ternocl_status int2_int8_gemm_run(int dtype, const int8_t *Aq, const void *SA, c
                                   const void *SB, void *C, const void *Other, const void *Bias, int M,
                                   int N, int K, int postop, int out_f32, hipStream_t st);
 ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
+// kernels (bitcos.hip)
+int bitcos_max_ls();
+ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, const void *S,
+                               const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias,
+                               int M, int N, int K, int postop, int out_f32, hipStream_t st);
+ternocl_status bitcos_slice_ranks_run(const uint32_t *Bc, uint32_t *SR, int N, int K, int ls,
+                                      hipStream_t st);
+ternocl_status bitcos_dequant_run(int dtype, const uint32_t *Bc, const void *S, void *W, int N, int K,
+                                  hipStream_t st);
+// kernels (hadamard.hip)
+ternocl_status fwht_run(int dtype, const void *x, const int8_t *signs, void *y, int rows, int K,
+                        int HB, int use_signs, float scale_full, float scale_tail, hipStream_t st);
 // kernels (misc.hip)
 ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st);
 
@@ -190,6 +203,61 @@ ternocl_status ternocl_int2_s8_decode(const uint32_t *B, uint32_t *D, int K, int
     if (!B || !D) FAIL(TERNOCL_ERR_INVALID_ARG, "B and D must be non-null");
     if (N < 16 || N % 16 || K < 16 || K % 16) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 16 == 0");
     return int2_s8_decode_run(B, D, K, N, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
+                                              const void *S, const uint32_t *SR, int ls, void *C,
+                                              const void *Other, const void *Bias, int M, int N,
+                                              int K, int postop, int out_f32, void *stream) {
+    ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
+    if (s != TERNOCL_OK) return s;
+    if (ls < 1 || ls > bitcos_max_ls()) FAIL(TERNOCL_ERR_INVALID_ARG, "ls must be 1..16");
+    if (K % (64 * ls)) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "BITCOS needs K % (64 * ls) == 0");
+    if (ls > 1 && !SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR (slice ranks for ls slices) must be non-null when ls > 1");
+    return bitcos_gemv_run(dtype, A, B, S, SR, ls, C, Other, Bias, M, N, K, postop, out_f32,
+                           (hipStream_t)stream);
+}
+
+ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K, int N, int ls,
+                                          void *stream) {
+    if (!B) FAIL(TERNOCL_ERR_INVALID_ARG, "B must be non-null");
+    if (ls < 1 || ls > bitcos_max_ls()) FAIL(TERNOCL_ERR_INVALID_ARG, "ls must be 1..16");
+    if (N < 16 || N % 16 || K < 64 || K % (64 * ls)) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % (64 * ls) == 0");
+    if (ls == 1) return TERNOCL_OK;
+    if (!SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR must be non-null");
+    return bitcos_slice_ranks_run(B, SR, N, K, ls, (hipStream_t)stream);
+}
+
+int ternocl_bitcos_pick_ls(int M, int N, int K) {
+    (void)M; (void)N;
+    int best = 1;
+    for (int ls = 1; ls <= bitcos_max_ls(); ++ls)
+        if (K % (64 * ls) == 0 && K / (64 * ls) >= 6) best = ls;
+    return best;
+}
+
+ternocl_status ternocl_bitcos_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
+                                      int N, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!B || !S || !W) FAIL(TERNOCL_ERR_INVALID_ARG, "B, S and W must be non-null");
+    if (N < 16 || N % 16 || K < kGS || K % kGS) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 128 == 0");
+    return bitcos_dequant_run(dtype, B, S, W, N, K, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_hadamard_fwht(int dtype, const void *x, const int8_t *signs, void *y,
+                                     int rows, int K, int HB, int use_signs, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!x || !y) FAIL(TERNOCL_ERR_INVALID_ARG, "x and y must be non-null");
+    if (use_signs && !signs) FAIL(TERNOCL_ERR_INVALID_ARG, "use_signs needs a signs vector");
+    if (HB < 256 || HB > 4096 || (HB & (HB - 1))) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "HB must be a power of two in [256, 4096]");
+    if (rows < 1 || K < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "rows and K must be positive");
+    const int tail = K % HB;
+    if (tail & (tail - 1)) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "K % HB must be 0 or a power of two");
+    const float full = (float)(1.0 / std::sqrt((double)HB));
+    const float part = tail ? (float)(1.0 / std::sqrt((double)tail)) : full;
+    return fwht_run(dtype, x, signs, y, rows, K, HB, use_signs ? 1 : 0, full, part, (hipStream_t)stream);
 }
 
 }  // extern "C"

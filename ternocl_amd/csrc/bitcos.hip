@@ -1,0 +1,280 @@
+// bitcos.hip -- BITCOS (presence bitmap + compacted signs) ternary GEMV on
+// gfx950, replacing bitcos_fp16_upcvt_gemv (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:177-277),
+// plus the slice-rank precompute (common/bitcos.hpp:81-94) and a bit-exact
+// decode hook.
+//
+//   C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(k,n))),  code in {-1, 0, +1}
+//
+// B is one uint32 buffer: bitmap [K/32][N] (bit c of word (kp, n) = row
+// 32kp+c of column n is non-zero) | offsets [N] (first sign word of column n) |
+// per-column sign streams (one bit per non-zero in k order, 1 = -1) | pad.
+// SR [ls-1][N]: non-zeros of column n above each slice start s*K/ls.
+//
+// Work split: lane = output column (64 columns per wave, every bitmap load is
+// 256 contiguous bytes), wave s of a workgroup = K slice s (it enters the
+// column's sign stream at SR[s-1]); the slices reduce through LDS in slice
+// order (deterministic).  Per 64-row chunk a lane loads the column's two
+// bitmap words and three sign words (the chunk consumes at most 64 sign bits
+// from the column's rank onwards); loads run two chunks (bitmap) and one chunk
+// (signs, whose address needs the rank, i.e. the previous bitmap words) ahead.
+// Decode per 32-row word: the word's sign window is funnel-shifted out of the
+// three sign words (v_alignbit); each 4-row nibble m and the next four window
+// bits s index a 256-entry LDS table of four DT codes +1 / -1 / 0 (a 4-bit
+// pdep), and the window advances by popcount(m) (v_bfe at a running offset,
+// v_bcnt with accumulate).  MACs: v_dot2_f32_{f16,bf16} of the code pairs with
+// activation pairs that are uniform across the wave (scalar loads), one fp32
+// partial per 128-row group, then acc += partial * S as the reference's host
+// gold (bitcos_fp16_upcvt/main.cpp:64-86).
+#include "common.hpp"
+
+namespace tcl {
+namespace {
+
+constexpr int kBcMaxLs = 16;  // slices (waves) per workgroup
+
+template <bool BF16> __host__ __device__ constexpr uint32_t bc_pos() { return BF16 ? 0x3F80u : 0x3C00u; }
+template <bool BF16> __host__ __device__ constexpr uint32_t bc_neg() { return BF16 ? 0xBF80u : 0xBC00u; }
+
+// Table entry (m, s): row i of the nibble is 0 if bit i of m is clear, else
+// -1 if sign bit popcount(m & ((1 << i) - 1)) of s is set, else +1
+// (bitcos_fp16_upcvt.cl:108-124).  .x = rows 0, 1; .y = rows 2, 3.
+template <bool BF16>
+__device__ __forceinline__ uint2 bc_lut_entry(int idx) {
+    const uint32_t m = (uint32_t)idx >> 4, s = (uint32_t)idx & 15u;
+    uint32_t c[4], r = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t p = (m >> i) & 1u;
+        c[i] = p ? (((s >> r) & 1u) ? bc_neg<BF16>() : bc_pos<BF16>()) : 0u;
+        r += p;
+    }
+    return make_uint2(c[0] | (c[1] << 16), c[2] | (c[3] << 16));
+}
+
+template <bool BF16>
+__device__ __forceinline__ void bc_build_lut(uint2 *lut) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) lut[i] = bc_lut_entry<BF16>(i);
+    __syncthreads();
+}
+
+// 32-bit sign window at stream bit r from three consecutive words q[0..2]
+// starting at word base (r / 32 - base is 0 or 1).
+__device__ __forceinline__ uint32_t bc_window(const uint32_t q[3], uint32_t base, uint32_t r) {
+    const bool up = (r >> 5) != base;
+    const uint32_t lo = up ? q[1] : q[0], hi = up ? q[2] : q[1];
+    return __builtin_amdgcn_alignbit(hi, lo, r & 31u);
+}
+
+// The 8 nibble lookups of one bitmap word with window sw.
+__device__ __forceinline__ void bc_decode_word(const uint2 *lut, uint32_t bm, uint32_t sw, uint2 e[8]) {
+    uint32_t p = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t m4 = (bm >> (4 * i)) & 15u;
+        const uint32_t s4 = (sw >> p) & 15u;
+        p = __builtin_popcount(m4) + p;
+        e[i] = lut[(m4 << 4) | s4];
+    }
+}
+
+template <int MR, bool BF16>
+__global__ void __launch_bounds__(64 * kBcMaxLs)
+k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
+              const uint16_t *__restrict__ S, const uint32_t *__restrict__ SR, void *__restrict__ C,
+              const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int m0, int N,
+              int K, int ls, int postop, int out_f32) {
+    __shared__ uint2 lut[256];
+    __shared__ float red[kBcMaxLs - 1][MR][64];
+    bc_build_lut<BF16>(lut);
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 64 + lane;
+    const int nc = n < N ? n : N - 1;
+    const size_t bw = (size_t)(K >> 5) * N;
+    const uint32_t *__restrict__ sg = Bc + bw + N + Bc[bw + nc];
+    const int slice = K / ls;
+    const int k0 = wave * slice;
+    const int chunks = slice >> 6;  // 64-row chunks (K % (64 * ls) == 0)
+    uint32_t R = wave ? SR[(size_t)(wave - 1) * N + nc] : 0u;
+
+    // activation rows m0 .. m0 + MR - 1 as packed pairs (rows past M repeat M - 1)
+    const uint32_t *__restrict__ ar[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) ar[r] = (const uint32_t *)(A + (size_t)min(m0 + r, M - 1) * K);
+
+    auto bm_load = [&](int c, uint32_t b[2]) {
+        const int cc = c < chunks ? c : chunks - 1;
+        const size_t kp = (size_t)((k0 >> 5) + 2 * cc);
+        b[0] = Bc[kp * N + nc];
+        b[1] = Bc[(kp + 1) * N + nc];
+    };
+    auto sg_load = [&](uint32_t r, uint32_t q[3]) {
+        const uint32_t w = r >> 5;
+        q[0] = sg[w];
+        q[1] = sg[w + 1];
+        q[2] = sg[w + 2];
+    };
+
+    float acc[MR], part[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = part[r] = 0.0f;
+
+    uint32_t bmA[2], bmB[2], qA[3];
+    bm_load(0, bmA);
+    bm_load(1, bmB);
+    sg_load(R, qA);
+    for (int c = 0; c < chunks; ++c) {
+        const uint32_t b0 = bmA[0], b1 = bmA[1];
+        uint32_t q[3] = {qA[0], qA[1], qA[2]};
+        const uint32_t r0 = R, r1 = __builtin_popcount(b0) + r0;
+        R = __builtin_popcount(b1) + r1;
+        // next chunk's signs (its rank is known now) and the bitmap two chunks ahead
+        sg_load(R, qA);
+        bmA[0] = bmB[0]; bmA[1] = bmB[1];
+        bm_load(c + 2, bmB);
+
+        const int k = k0 + 64 * c;
+        const uint32_t base = r0 >> 5;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint2 e[8];
+            bc_decode_word(lut, h ? b1 : b0, bc_window(q, base, h ? r1 : r0), e);
+            const int kd = (k + 32 * h) >> 1;  // first activation pair of the word
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                float pr = part[r];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    pr = dot2<BF16>(e[i].x, ar[r][kd + 2 * i], pr);
+                    pr = dot2<BF16>(e[i].y, ar[r][kd + 2 * i + 1], pr);
+                }
+                part[r] = pr;
+            }
+        }
+        // group end (or slice end mid-group): apply the group's scale
+        if (((k + 64) & (kGS - 1)) == 0 || c + 1 == chunks) {
+            const float s = dt2f<BF16>(S[(size_t)(k >> 7) * N + nc]);
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                acc[r] += part[r] * s;
+                part[r] = 0.0f;
+            }
+        }
+    }
+
+    // reduce the slices in slice order
+    if (ls > 1) {
+        if (wave > 0)
+#pragma unroll
+            for (int r = 0; r < MR; ++r) red[wave - 1][r][lane] = acc[r];
+        __syncthreads();
+        if (wave > 0) return;
+        for (int j = 0; j < ls - 1; ++j)
+#pragma unroll
+            for (int r = 0; r < MR; ++r) acc[r] += red[j][r][lane];
+    }
+    if (n >= N) return;
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+        if (m0 + r < M) epi_store1<BF16>(C, Other, Bias, postop, out_f32, N, m0 + r, n, acc[r]);
+}
+
+// SR[(s-1)*N + n] = non-zeros of column n in bitmap words kp < s * ceil(K/ls) / 32
+__global__ void k_bitcos_slice_ranks(const uint32_t *__restrict__ Bc, uint32_t *__restrict__ SR, int N,
+                                     int K, int ls) {
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    const int slice_k = (K + ls - 1) / ls;
+    uint32_t s = 0;
+    int kp = 0;
+    for (int sl = 1; sl < ls; ++sl) {
+        for (; kp < sl * slice_k / 32; ++kp) s += __builtin_popcount(Bc[(size_t)kp * N + n]);
+        SR[(size_t)(sl - 1) * N + n] = s;
+    }
+}
+
+// Test hook: W[k][n] = 0 / S / S ^ 0x8000 for code 0 / +1 / -1, through the
+// GEMV's decode (sign windows, nibble table) -- one thread per column.
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+k_bitcos_dequant(const uint32_t *__restrict__ Bc, const uint16_t *__restrict__ S, uint16_t *__restrict__ W,
+                 int N, int K) {
+    __shared__ uint2 lut[256];
+    bc_build_lut<BF16>(lut);
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    const size_t bw = (size_t)(K >> 5) * N;
+    const uint32_t *sg = Bc + bw + N + Bc[bw + n];
+    uint32_t R = 0;
+    for (int kp = 0; kp < K / 32; ++kp) {
+        const uint32_t bm = Bc[(size_t)kp * N + n];
+        const uint32_t q[3] = {sg[R >> 5], sg[(R >> 5) + 1], sg[(R >> 5) + 2]};
+        uint2 e[8];
+        bc_decode_word(lut, bm, bc_window(q, R >> 5, R), e);
+        R += __builtin_popcount(bm);
+        const uint32_t s = S[(size_t)(kp >> 2) * N + n];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t cw[4] = {e[i].x & 0xffffu, e[i].x >> 16, e[i].y & 0xffffu, e[i].y >> 16};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                W[(size_t)(32 * kp + 4 * i + j) * N + n] = (uint16_t)(cw[j] ? (s ^ (cw[j] & 0x8000u)) : 0u);
+        }
+    }
+}
+
+template <int MR, bool BF16>
+void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
+               const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
+               int out_f32, hipStream_t st) {
+    hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16>), dim3((N + 63) / 64), dim3(64 * ls), 0, st,
+                       (const uint16_t *)A, Bc, (const uint16_t *)S, SR, C, (const uint16_t *)Other, Bias,
+                       M, m0, N, K, ls, postop, out_f32);
+}
+
+template <bool BF16>
+void bc_launch_rows(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
+                    const void *Other, const void *Bias, int M, int N, int K, int ls, int postop,
+                    int out_f32, hipStream_t st) {
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        const int rows = M - m0;
+        if (rows == 1) bc_launch<1, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, st);
+        else if (rows == 2) bc_launch<2, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, st);
+        else bc_launch<4, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, st);
+    }
+}
+
+}  // namespace
+
+int bitcos_max_ls() { return kBcMaxLs; }
+
+ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, const void *S,
+                               const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias,
+                               int M, int N, int K, int postop, int out_f32, hipStream_t st) {
+    if (dtype == TERNOCL_BF16)
+        bc_launch_rows<true>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, st);
+    else
+        bc_launch_rows<false>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, st);
+    return check_launch();
+}
+
+ternocl_status bitcos_slice_ranks_run(const uint32_t *Bc, uint32_t *SR, int N, int K, int ls,
+                                      hipStream_t st) {
+    hipLaunchKernelGGL(k_bitcos_slice_ranks, dim3((N + 255) / 256), dim3(256), 0, st, Bc, SR, N, K, ls);
+    return check_launch();
+}
+
+ternocl_status bitcos_dequant_run(int dtype, const uint32_t *Bc, const void *S, void *W, int N, int K,
+                                  hipStream_t st) {
+    const dim3 grid((N + 255) / 256), block(256);
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL(k_bitcos_dequant<true>, grid, block, 0, st, Bc, (const uint16_t *)S,
+                           (uint16_t *)W, N, K);
+    else
+        hipLaunchKernelGGL(k_bitcos_dequant<false>, grid, block, 0, st, Bc, (const uint16_t *)S,
+                           (uint16_t *)W, N, K);
+    return check_launch();
+}
+
+}  // namespace tcl

@@ -37,10 +37,30 @@ __device__ __forceinline__ uint32_t f2dt(float f) {
         u += 0x7fffu + ((u >> 16) & 1u);
         return u >> 16;
     } else {
+        // Materialise the fp32 value first: otherwise a product feeding the
+        // conversion fuses into v_fma_mixlo_f16, which rounds once straight to
+        // fp16 instead of fp32 then fp16 as the reference's DT stores do.
+        asm volatile("" : "+v"(f));
         const _Float16 x = (_Float16)f;  // v_cvt_f16_f32, RTE
         uint16_t b;
         __builtin_memcpy(&b, &x, 2);
         return b;
+    }
+}
+
+// c + w.lo * a.lo + w.hi * a.hi on packed DT pairs (v_dot2_f32_{f16,bf16})
+template <bool BF16>
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t a, float c) {
+    if constexpr (BF16) {
+        bf162_t x, y;
+        __builtin_memcpy(&x, &w, 4);
+        __builtin_memcpy(&y, &a, 4);
+        return __builtin_amdgcn_fdot2_f32_bf16(x, y, c, false);
+    } else {
+        half2_t x, y;
+        __builtin_memcpy(&x, &w, 4);
+        __builtin_memcpy(&y, &a, 4);
+        return __builtin_amdgcn_fdot2(x, y, c, false);
     }
 }
 

@@ -28,21 +28,6 @@
 namespace tcl {
 namespace {
 
-template <bool BF16>
-__device__ __forceinline__ float dot2(uint32_t w, uint32_t a, float c) {
-    if constexpr (BF16) {
-        bf162_t x, y;
-        __builtin_memcpy(&x, &w, 4);
-        __builtin_memcpy(&y, &a, 4);
-        return __builtin_amdgcn_fdot2_f32_bf16(x, y, c, false);
-    } else {
-        half2_t x, y;
-        __builtin_memcpy(&x, &w, 4);
-        __builtin_memcpy(&y, &a, 4);
-        return __builtin_amdgcn_fdot2(x, y, c, false);
-    }
-}
-
 // LDS layout of one round buffer: for each row m and round-local group q,
 // 64 packed activation pairs plus 4 dwords of padding (keeps the k-slots of a
 // wave, which read different groups, on different banks); then beta[m][q].

@@ -1,0 +1,220 @@
+"""GPU parity of the BITCOS GEMV, its slice ranks and decode, and the Hadamard
+transform, through the C ABI.
+
+Reference test design followed: bitcos_fp16_upcvt/validate.sh (shape list,
+fp16 + bf16, zero densities, LS choices) and zsweep.sh (z sweep); the host
+gold compute_gold (bitcos_fp16_upcvt/main.cpp:64-86) restated by the oracle;
+the slice ranks of common/bitcos.hpp:81-94.  The reference has no Hadamard
+test: the transform is checked bit for bit against the oracle's restatement of
+hadamard_fwht.cl, which the CPU suite pins to the Sylvester matrix.
+Bars: decode, slice ranks and FWHT bit-exact; C within 1e-3 + 1e-2 |ref|.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from ternocl_amd import formats, synth
+from tests.gpu_util import allclose_report, dev_dt, dev_raw, host_u16, host_u32
+
+pytestmark = pytest.mark.gpu
+
+
+# ---- Hadamard ------------------------------------------------------------------
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("HB", [256, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("rows,K,use_signs", [(1, 4096, True), (3, 8192, False), (2, 5376, True)])
+def test_fwht_bit_exact(dev, orc, HB, bf16, rows, K, use_signs):
+    import torch
+    import ternocl_amd as T
+    tail = K % HB
+    if tail & (tail - 1):
+        pytest.skip("K % HB is not a power of two for this pair")
+    print(f"fwht HB={HB} rows={rows} K={K} signs={use_signs} bf16={bf16}", flush=True)
+    g = synth.rng(HB + K + rows)
+    x = synth.activations(g, (rows, K), bf16)
+    s = (g.integers(0, 2, K, dtype=np.int8) * 2 - 1).astype(np.int8)
+    dy = torch.zeros((rows, K), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    T.hadamard_fwht(dev_dt(x, bf16), dev_raw(s), dy, rows, K, HB, use_signs)
+    torch.cuda.synchronize()
+    want = orc.fwht(x, s, rows, K, HB, use_signs, bf16)
+    assert np.array_equal(host_u16(dy), want)
+
+
+def test_fwht_rejects_bad_shapes(dev):
+    import torch
+    import ternocl_amd as T
+    x = torch.zeros(1000, dtype=torch.float16, device="cuda")
+    with pytest.raises(T.TernoclError):
+        T.hadamard_fwht(x, None, x, 1, 1000, 512, False)  # tail 488 is not a power of two
+    with pytest.raises(T.TernoclError):
+        T.hadamard_fwht(x, None, x, 1, 1024, 100, False)  # HB not a power of two
+    with pytest.raises(T.TernoclError):
+        T.hadamard_fwht(x, None, x, 1, 1024, 512, True)  # signs missing
+
+
+# ---- BITCOS ----------------------------------------------------------------------
+
+def _bitcos_case(seed, M, K, N, z, bf16):
+    g = synth.rng(seed)
+    A = synth.activations(g, (M, K), bf16)
+    codes = synth.ternary_codes(g, K, N, z)
+    S = synth.scales(g, K, N, bf16)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = g.standard_normal(N).astype(np.float32) * np.float32(0.1)
+    return A, codes, S, other, bias_f
+
+
+def _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32):
+    dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(buf), dev_dt(S, bf16), dev_dt(other, bf16)
+    dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    if out_f32:
+        dBias = torch.from_numpy(bias_f).cuda()
+        dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    else:
+        dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+        dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+    T.bitcos_fp16_upcvt_gemm(dA, dB, dS, dSR if ls > 1 else None, dC, dO, dBias, M, N, K, ls, postop, out_f32)
+    torch.cuda.synchronize()
+    return dC
+
+
+def _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, postop, out_f32):
+    acc = orc.bitcos_gold(A, buf, S, M, K, N, bf16)
+    bias = bias_f if out_f32 else formats.f32_to_dt(bias_f, bf16)
+    return orc.epilogue(acc, other, bias, postop, out_f32, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("z", [0.0, 0.3, 0.5, 0.7, 1.0])
+def test_bitcos_dequant_bit_exact(dev, orc, z, bf16):
+    import torch
+    import ternocl_amd as T
+    K, N = 1024, 96
+    A, codes, S, _, _ = _bitcos_case(int(z * 10) + 1, 1, K, N, z, bf16)
+    buf = formats.bitcos_pack(codes)
+    dW = torch.zeros((K, N), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    T.bitcos_dequant(dev_raw(buf), dev_dt(S, bf16), dW, K, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(dW), orc.bitcos_dequant(buf, S, K, N))
+
+
+@pytest.mark.parametrize("ls", [2, 3, 4, 7, 16])
+def test_bitcos_slice_ranks(dev, orc, ls):
+    import torch
+    import ternocl_amd as T
+    K, N = 21504, 80  # divisible by 64 * ls for every ls tested
+    _, codes, _, _, _ = _bitcos_case(ls, 1, K, N, 0.4, False)
+    buf = formats.bitcos_pack(codes)
+    dSR = torch.zeros((ls - 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dev_raw(buf), dSR, K, N, ls)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u32(dSR), orc.bitcos_slice_ranks(buf, K, N, ls))
+
+
+SHAPES = [(1, 256, 16, 1), (1, 1024, 272, 4), (2, 4096, 1040, 8), (3, 2048, 528, 2),
+          (4, 5376, 2048, 7), (5, 1536, 336, 6), (8, 640, 64, 5), (1, 5376, 21504, 14)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ls", SHAPES)
+@pytest.mark.parametrize("z", [0.3, 0.7])
+def test_bitcos_gemv_parity(dev, orc, M, K, N, ls, z, bf16):
+    import torch
+    import ternocl_amd as T
+    print(f"bitcos gemv M={M} K={K} N={N} ls={ls} z={z} bf16={bf16}", flush=True)
+    A, codes, S, other, bias_f = _bitcos_case(4000 + M + K + N + ls, M, K, N, z, bf16)
+    buf = formats.bitcos_pack(codes)
+    dC = _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False)
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 0, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("z", [0.0, 1.0])
+def test_bitcos_gemv_extreme_density(dev, orc, z):
+    """All weights non-zero (every sign bit consumed) and all zero (empty sign streams)."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, ls, bf16 = 1, 2048, 144, 4, False
+    A, codes, S, other, bias_f = _bitcos_case(9, M, K, N, z, bf16)
+    buf = formats.bitcos_pack(codes)
+    dC = _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, True)
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 0, True)
+    bad, dmax = allclose_report(dC.cpu().numpy(), want)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_bitcos_gemv_epilogues(dev, orc, bf16, postop, out_f32):
+    import torch
+    import ternocl_amd as T
+    M, K, N, ls = 2, 1024, 528, 4
+    A, codes, S, other, bias_f = _bitcos_case(60 + postop, M, K, N, 0.5, bf16)
+    buf = formats.bitcos_pack(codes)
+    dC = _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32)
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, postop, out_f32)
+    got = dC.cpu().numpy() if out_f32 else formats.dt_to_f32(host_u16(dC), bf16)
+    ref = want if out_f32 else formats.dt_to_f32(want, bf16)
+    bad, dmax = allclose_report(got, ref)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+def test_bitcos_ls_invariance_and_determinism(dev, orc):
+    """Every slice count gives the reference result; repeated calls are bit-identical."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, bf16 = 1, 5376, 512, False
+    A, codes, S, other, bias_f = _bitcos_case(21, M, K, N, 0.5, bf16)
+    buf = formats.bitcos_pack(codes)
+    want = formats.dt_to_f32(_bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 0, False), bf16)
+    for ls in (1, 2, 3, 4, 6, 7, 12, 14):
+        out = host_u16(_bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False))
+        bad, dmax = allclose_report(formats.dt_to_f32(out, bf16), want)
+        assert bad == 0, f"ls={ls}: {bad} bad (max |d| {dmax})"
+        again = host_u16(_bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False))
+        assert np.array_equal(out, again)
+
+
+def test_bitcos_hadamard_pipeline(dev, orc):
+    """The decode-step workload: sign flip + FWHT (HB 512) on the activation, then the
+    BITCOS GEMV on the transformed activation (K = 5376: a 256-element tail block)."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, ls, bf16, HB = 1, 5376, 1024, 7, False, 512
+    g = synth.rng(99)
+    x = synth.activations(g, (M, K), bf16)
+    sgn = (g.integers(0, 2, K, dtype=np.int8) * 2 - 1).astype(np.int8)
+    codes = synth.ternary_codes(g, K, N, 0.5)
+    S = synth.scales(g, K, N, bf16)
+    buf = formats.bitcos_pack(codes)
+    dx, dy = dev_dt(x, bf16), torch.zeros((M, K), dtype=torch.float16, device="cuda")
+    T.hadamard_fwht(dx, dev_raw(sgn), dy, M, K, HB, True)
+    dB, dS = dev_raw(buf), dev_dt(S, bf16)
+    dSR = torch.zeros((ls - 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    dC = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    T.bitcos_fp16_upcvt_gemm(dy, dB, dS, dSR, dC, None, None, M, N, K, ls)
+    torch.cuda.synchronize()
+    y = orc.fwht(x, sgn, M, K, HB, True, bf16)
+    assert np.array_equal(host_u16(dy), y)
+    want = formats.dt_to_f32(orc.epilogue(orc.bitcos_gold(y, buf, S, M, K, N, bf16), None, None, 0, False, bf16), bf16)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), want)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+def test_bitcos_rejects_bad_ls(dev):
+    import torch
+    import ternocl_amd as T
+    A = torch.zeros((1, 1024), dtype=torch.float16, device="cuda")
+    B = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    S = torch.zeros((8, 16), dtype=torch.float16, device="cuda")
+    C = torch.zeros((1, 16), dtype=torch.float16, device="cuda")
+    with pytest.raises(T.TernoclError):
+        T.bitcos_fp16_upcvt_gemm(A, B, S, None, C, None, None, 1, 16, 1024, ls=3)  # 1024 % 192
+    with pytest.raises(T.TernoclError):
+        T.bitcos_fp16_upcvt_gemm(A, B, S, None, C, None, None, 1, 16, 1024, ls=2)  # SR missing
