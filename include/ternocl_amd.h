@@ -176,6 +176,49 @@ ternocl_status ternocl_bitcos_dequant(int dtype, const uint32_t *B, const void *
 ternocl_status ternocl_hadamard_fwht(int dtype, const void *x, const int8_t *signs, void *y,
                                      int rows, int K, int HB, int use_signs, void *stream);
 
+/* ---- int2 MoE prefill ----------------------------------------------------
+ * Replaces the kernels of int2_moe/int2_moe_prefill.cl and the layer sequence
+ * of int2_moe/prefill.cpp:268-279.  Assignments g = t * topk + j (token t,
+ * slot j); ids int [G] expert of each assignment; RW DT [G] its gate weight.
+ * Expert weights: B_all uint32 [E][K/16][N], S_all DT [E][K/128][N].
+ *
+ * Route (int2_moe_prefill.cl:29-61): meta int [2E+2] = row offsets [0..E] of
+ * each expert in the expert-sorted order, then row-tile offsets [E+1..2E+1]
+ * (tiles of ternocl_moe_tile_rows() rows); perm int [G] sorted row -> g;
+ * inv int [G] = perm^-1.  Rows of an expert are in assignment order (stable,
+ * deterministic).  An id outside [0, E) drops its assignment (inv = -1).
+ * 1 <= E <= 512. */
+int ternocl_moe_tile_rows(void);
+ternocl_status ternocl_int2_moe_route(const int *ids, int *meta, int *perm, int *inv, int G, int E,
+                                      void *stream);
+/* Gather (int2_moe_prefill.cl:63-70): Xs[p] = X[perm[p] / topk], rows of K DT. */
+ternocl_status ternocl_int2_moe_gather(int dtype, const void *X, const int *perm, void *Xs, int G,
+                                       int K, int topk, void *stream);
+/* Grouped GEMM (int2_moe_prefill.cl:72-141): for every sorted row p of expert e,
+ *   C[p, n] = ct(epi(sum_g S_e[g,n] * sum_{k in g} A(p)[k] * code_e(k, n)))
+ * A(p) = A_all[perm[p] / topk] when perm is non-NULL (the gather fused into
+ * the GEMM's A loads), else A_all[p].  C and Other are [G, N] in sorted order;
+ * postop 0, 1, 2 or 4 (no bias), out_f32 as ternocl_int2_fp16_upcvt_gemm. */
+ternocl_status ternocl_int2_moe_gemm(int dtype, const int *meta, const void *A_all, const int *perm,
+                                     int topk, const uint32_t *B_all, const void *S_all, void *C_all,
+                                     const void *Other_all, int E, int G, int N, int K, int postop,
+                                     int out_f32, void *stream);
+/* Combine (int2_moe_prefill.cl:143-156): O[t, n] = DT(sum_{j < topk} RW[g] * Y[inv[g], n]),
+ * j in order, fp32; Y fp32 [G, N] (sorted rows), O DT [T, N]. */
+ternocl_status ternocl_int2_moe_combine(int dtype, const float *Y, const int *inv, const void *RW,
+                                        void *O, int T, int topk, int N, void *stream);
+/* One whole MoE layer: route, up = X x B_up (POSTOP 0), Hs = silu(X x B_gate) * up
+ * (POSTOP 1), Y = Hs x B_down (fp32), combine.  X DT [T, H]; gate / up
+ * weights [E][H/16][I] / [E][H/128][I]; down [E][I/16][H] / [E][I/128][H];
+ * O DT [T, H].  ws: device scratch of ternocl_int2_moe_prefill_ws_bytes()
+ * bytes (meta, perm, inv, U, Hs, Y). */
+size_t ternocl_int2_moe_prefill_ws_bytes(int T, int E, int topk, int H, int I);
+ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids, const void *RW,
+                                        int T, int E, int topk, int H, int I, const uint32_t *Bg,
+                                        const void *Sg, const uint32_t *Bu, const void *Su,
+                                        const uint32_t *Bd, const void *Sd, void *O, void *ws,
+                                        size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

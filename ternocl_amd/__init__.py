@@ -26,6 +26,8 @@ __all__ = [
     "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
     "bitcos_fp16_upcvt_gemm", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
+    "moe_tile_rows", "int2_moe_route", "int2_moe_gather", "int2_moe_gemm", "int2_moe_combine",
+    "int2_moe_prefill_ws_bytes", "int2_moe_prefill",
 ]
 
 FP16, BF16 = 0, 1
@@ -200,3 +202,48 @@ def hadamard_fwht(x, signs, y, rows: int, K: int, HB: int, use_signs: bool = Tru
     """hadamard_fwht(x, signs, y, K, use_signs) of hadamard_fwht.cl:63 with -DHB=HB over rows rows."""
     _check(lib().ternocl_hadamard_fwht(_dtype_of(x), _ptr(x), _ptr(signs), _ptr(y), rows, K, HB,
                                        int(bool(use_signs)), _stream(stream)))
+
+
+# ---- int2 MoE prefill (int2_moe/int2_moe_prefill.cl) ---------------------------
+
+def moe_tile_rows() -> int:
+    """Rows per tile of meta's row-tile offsets."""
+    return lib().ternocl_moe_tile_rows()
+
+
+def int2_moe_route(ids, meta, perm, inv, G: int, E: int, stream=None) -> None:
+    """int2_moe_route(ids, meta, perm, inv, G) of int2_moe_prefill.cl:30 (stable order)."""
+    _check(lib().ternocl_int2_moe_route(_ptr(ids), _ptr(meta), _ptr(perm), _ptr(inv), G, E, _stream(stream)))
+
+
+def int2_moe_gather(X, perm, Xs, G: int, K: int, topk: int, stream=None) -> None:
+    """int2_moe_gather(X, perm, Xs, K) of int2_moe_prefill.cl:64."""
+    _check(lib().ternocl_int2_moe_gather(_dtype_of(X), _ptr(X), _ptr(perm), _ptr(Xs), G, K, topk,
+                                         _stream(stream)))
+
+
+def int2_moe_gemm(meta, A_all, perm, topk: int, B_all, S_all, C_all, Other_all, E: int, G: int, N: int,
+                  K: int, postop: int = 0, out_f32: bool = False, stream=None) -> None:
+    """int2_moe_gemm_mt(meta, A_all, B_all, S_all, C_all, Other_all, N, K) of
+    int2_moe_prefill.cl:75; A rows through perm / topk when perm is given."""
+    _check(lib().ternocl_int2_moe_gemm(_dtype_of(A_all), _ptr(meta), _ptr(A_all), _ptr(perm), topk,
+                                       _ptr(B_all), _ptr(S_all), _ptr(C_all), _ptr(Other_all), E, G, N, K,
+                                       postop, int(bool(out_f32)), _stream(stream)))
+
+
+def int2_moe_combine(Y, inv, RW, O, T: int, topk: int, N: int, stream=None) -> None:
+    """int2_moe_combine(Y, inv, RW, O, N) of int2_moe_prefill.cl:144."""
+    _check(lib().ternocl_int2_moe_combine(_dtype_of(O), _ptr(Y), _ptr(inv), _ptr(RW), _ptr(O), T, topk, N,
+                                          _stream(stream)))
+
+
+def int2_moe_prefill_ws_bytes(T: int, E: int, topk: int, H: int, I: int) -> int:
+    return lib().ternocl_int2_moe_prefill_ws_bytes(T, E, topk, H, I)
+
+
+def int2_moe_prefill(X, ids, RW, T: int, E: int, topk: int, H: int, I: int, Bg, Sg, Bu, Su, Bd, Sd, O,
+                     ws, stream=None) -> None:
+    """One MoE layer: route, up, gate (silu * up), down, combine (int2_moe/prefill.cpp:268-279)."""
+    _check(lib().ternocl_int2_moe_prefill(_dtype_of(X), _ptr(X), _ptr(ids), _ptr(RW), T, E, topk, H, I,
+                                          _ptr(Bg), _ptr(Sg), _ptr(Bu), _ptr(Su), _ptr(Bd), _ptr(Sd), _ptr(O),
+                                          _ptr(ws), _nbytes(ws), _stream(stream)))

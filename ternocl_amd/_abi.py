@@ -39,6 +39,13 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_bitcos_pick_ls": (I, [I, I, I]),
     "ternocl_bitcos_dequant": (I, [I, P, P, P, I, I, P]),
     "ternocl_hadamard_fwht": (I, [I, P, P, P, I, I, I, I, P]),
+    "ternocl_moe_tile_rows": (I, []),
+    "ternocl_int2_moe_route": (I, [P, P, P, P, I, I, P]),
+    "ternocl_int2_moe_gather": (I, [I, P, P, P, I, I, I, P]),
+    "ternocl_int2_moe_gemm": (I, [I, P, P, P, I, P, P, P, P, I, I, I, I, I, I, P]),
+    "ternocl_int2_moe_combine": (I, [I, P, P, P, P, I, I, I, P]),
+    "ternocl_int2_moe_prefill_ws_bytes": (Z, [I, I, I, I, I]),
+    "ternocl_int2_moe_prefill": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
 }
 
 

@@ -61,6 +61,24 @@ ternocl_status bitcos_dequant_run(int dtype, const uint32_t *Bc, const void *S, 
 // kernels (hadamard.hip)
 ternocl_status fwht_run(int dtype, const void *x, const int8_t *signs, void *y, int rows, int K,
                         int HB, int use_signs, float scale_full, float scale_tail, hipStream_t st);
+// kernels (moe.hip, int2_gemm_mfma.hip)
+int moe_tile_rows();
+size_t moe_route_lds(int E);
+ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st);
+ternocl_status moe_gather_run(const void *X, const int *perm, void *Xs, int G, int K, int topk, hipStream_t st);
+ternocl_status moe_combine_run(int dtype, const float *Y, const int *inv, const void *RW, void *O, int T,
+                               int topk, int N, hipStream_t st);
+ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
+                            const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
+                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st);
+struct MoeWs {
+    size_t meta, perm, inv, u, h, y, total;
+};
+MoeWs moe_ws_layout(int T, int E, int topk, int H, int I);
+ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                               int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                               const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                               void *O, void *ws, hipStream_t st);
 // kernels (misc.hip)
 ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st);
 
@@ -258,6 +276,70 @@ ternocl_status ternocl_hadamard_fwht(int dtype, const void *x, const int8_t *sig
     const float full = (float)(1.0 / std::sqrt((double)HB));
     const float part = tail ? (float)(1.0 / std::sqrt((double)tail)) : full;
     return fwht_run(dtype, x, signs, y, rows, K, HB, use_signs ? 1 : 0, full, part, (hipStream_t)stream);
+}
+
+constexpr int kMoeMaxExperts = 512;  // route LDS: 18 ints per expert (36 KiB)
+
+int ternocl_moe_tile_rows(void) { return moe_tile_rows(); }
+
+ternocl_status ternocl_int2_moe_route(const int *ids, int *meta, int *perm, int *inv, int G, int E,
+                                      void *stream) {
+    if (!ids || !meta || !perm || !inv) FAIL(TERNOCL_ERR_INVALID_ARG, "ids, meta, perm and inv must be non-null");
+    if (G < 1 || E < 1 || E > kMoeMaxExperts) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need G >= 1 and 1 <= E <= 512");
+    return moe_route_run(ids, meta, perm, inv, G, E, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_moe_gather(int dtype, const void *X, const int *perm, void *Xs, int G,
+                                       int K, int topk, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!X || !perm || !Xs) FAIL(TERNOCL_ERR_INVALID_ARG, "X, perm and Xs must be non-null");
+    if (G < 1 || K < 1 || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need G, K, topk >= 1");
+    return moe_gather_run(X, perm, Xs, G, K, topk, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_moe_gemm(int dtype, const int *meta, const void *A_all, const int *perm,
+                                     int topk, const uint32_t *B_all, const void *S_all, void *C_all,
+                                     const void *Other_all, int E, int G, int N, int K, int postop,
+                                     int out_f32, void *stream) {
+    ternocl_status s = check_gemm_common(dtype, A_all, B_all, S_all, C_all, Other_all, nullptr, G, N, K,
+                                         postop == 3 || postop == 5 ? 0 : postop, out_f32);
+    if (s != TERNOCL_OK) return s;
+    if (!meta) FAIL(TERNOCL_ERR_INVALID_ARG, "meta must be non-null");
+    if (postop == 3 || postop == 5) FAIL(TERNOCL_ERR_INVALID_ARG, "the MoE GEMM has no bias: postop 0, 1, 2 or 4");
+    if (E < 1 || E > kMoeMaxExperts || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need 1 <= E <= 512 and topk >= 1");
+    return moe_gemm_run(dtype, meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop,
+                        out_f32, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_moe_combine(int dtype, const float *Y, const int *inv, const void *RW,
+                                        void *O, int T, int topk, int N, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!Y || !inv || !RW || !O) FAIL(TERNOCL_ERR_INVALID_ARG, "Y, inv, RW and O must be non-null");
+    if (T < 1 || topk < 1 || N < 4 || N % 4) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need T, topk >= 1 and N % 4 == 0");
+    return moe_combine_run(dtype, Y, inv, RW, O, T, topk, N, (hipStream_t)stream);
+}
+
+size_t ternocl_int2_moe_prefill_ws_bytes(int T, int E, int topk, int H, int I) {
+    if (T < 1 || E < 1 || topk < 1 || H < 1 || I < 1) return 0;
+    return moe_ws_layout(T, E, topk, H, I).total;
+}
+
+ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids, const void *RW,
+                                        int T, int E, int topk, int H, int I, const uint32_t *Bg,
+                                        const void *Sg, const uint32_t *Bu, const void *Su,
+                                        const uint32_t *Bd, const void *Sd, void *O, void *ws,
+                                        size_t ws_bytes, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!X || !ids || !RW || !Bg || !Sg || !Bu || !Su || !Bd || !Sd || !O)
+        FAIL(TERNOCL_ERR_INVALID_ARG, "X, ids, RW, the six weight tensors and O must be non-null");
+    if (T < 1 || E < 1 || E > kMoeMaxExperts || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need T, topk >= 1 and 1 <= E <= 512");
+    if (H % 128 || I % 128) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "H and I must be multiples of 128");
+    if (!ws || ws_bytes < moe_ws_layout(T, E, topk, H, I).total)
+        FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_prefill_ws_bytes() bytes");
+    return moe_prefill_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -218,6 +218,38 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     gemm_tile<BF16>(ar, mrows, B, S, C, Other, Bias, tm * BM, N, K, tn * BN, postop, out_f32, lds);
 }
 
+// Grouped GEMM of the MoE prefill (int2_moe/int2_moe_prefill.cl:72-141): the
+// rows of each expert e are meta[e] .. meta[e+1]-1 of the expert-sorted order,
+// cut into 128-row tiles numbered from meta[E+1+e]; workgroup (tile, column
+// block) finds its expert by binary search over the tile offsets.  A rows come
+// from A_all[perm[p] / topk] when perm is given (the gather fused into the
+// A-tile load), else from A_all[p].  Expert e's weights: B_all + e*(K/16)*N,
+// S_all + e*(K/128)*N; C and Other are indexed by the sorted row p.
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all,
+                const int *__restrict__ perm, int topk, const uint32_t *__restrict__ B_all,
+                const uint16_t *__restrict__ S_all, void *__restrict__ C_all,
+                const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
+                int ntn) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BM * A_PITCH];
+    const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
+    if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {  // the last expert whose first tile is <= tile
+        const int mid = (lo + hi + 1) >> 1;
+        if (meta[E + 1 + mid] <= tile) lo = mid;
+        else hi = mid - 1;
+    }
+    const int e = lo, row0 = meta[e];
+    const int m0 = (tile - meta[E + 1 + e]) * BM;
+    const int mrows = min(BM, meta[e + 1] - row0 - m0);
+    const ARows ar = perm ? ARows{A_all, perm + row0 + m0, topk}
+                          : ARows{A_all + (size_t)(row0 + m0) * K, nullptr, 1};
+    gemm_tile<BF16>(ar, mrows, B_all + (size_t)e * (K / 16) * N, S_all + (size_t)e * (K / kGS) * N, C_all,
+                    Other_all, nullptr, row0 + m0, N, K, tn * BN, postop, out_f32, lds);
+}
+
 // Test hook: the B fragments the GEMM builds, D[word][0..3] = half 0,
 // D[word][4..7] = half 1 (the same bits for fp16 and bf16).
 __global__ void k_int2_gemm_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, int words) {
@@ -232,6 +264,25 @@ __global__ void k_int2_gemm_decode(const uint32_t *__restrict__ B, uint32_t *__r
 }
 
 }  // namespace
+
+int moe_tile_rows() { return BM; }
+
+ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
+                            const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
+                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st) {
+    const int ntn = (N + BN - 1) / BN;
+    const int max_tiles = (G + BM - 1) / BM + E;  // each expert's ragged tail adds at most one tile
+    const dim3 grid((unsigned)(max_tiles * ntn)), block(256);
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL(k_int2_moe_gemm<true>, grid, block, 0, st, meta, (const uint16_t *)A_all, perm, topk,
+                           B_all, (const uint16_t *)S_all, C_all, (const uint16_t *)Other_all, E, N, K, postop,
+                           out_f32, ntn);
+    else
+        hipLaunchKernelGGL(k_int2_moe_gemm<false>, grid, block, 0, st, meta, (const uint16_t *)A_all, perm, topk,
+                           B_all, (const uint16_t *)S_all, C_all, (const uint16_t *)Other_all, E, N, K, postop,
+                           out_f32, ntn);
+    return check_launch();
+}
 
 ternocl_status int2_gemm_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st) {
     const int words = K / 16 * N;

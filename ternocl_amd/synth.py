@@ -8,7 +8,9 @@ gives the same bits regardless of thread count.  Distributions:
   reference drivers do (int2_fp16_upcvt/main.cpp:238-242: low bit = r1,
   high bit = r1 & r2, per 2-bit field) -> codes {0, 1, 3};
 * per-128-group scales ~ U[0.005, 0.02];
-* BITCOS weights at zero density z, non-zeros +/-1 equiprobable.
+* BITCOS weights at zero density z, non-zeros +/-1 equiprobable;
+* MoE routing: each token picks topk distinct experts uniformly at random; its
+  gate weights are the softmax of topk logits ~N(0, 1) (fp32, then DT).
 """
 from __future__ import annotations
 
@@ -50,3 +52,12 @@ def ternary_codes(g: np.random.Generator, K: int, N: int, z: float) -> np.ndarra
 def bitcos_weights(g: np.random.Generator, K: int, N: int, z: float):
     codes = ternary_codes(g, K, N, z)
     return bitcos_pack(codes), codes
+
+
+def moe_routing(g: np.random.Generator, T: int, E: int, topk: int, bf16: bool):
+    """ids int32 [T*topk] (distinct experts per token, uniform) and RW DT [T*topk]."""
+    ids = np.argsort(g.random((T, E), dtype=np.float32), axis=1)[:, :topk].astype(np.int32)
+    logits = g.standard_normal((T, topk), dtype=np.float32)
+    w = np.exp(logits - logits.max(axis=1, keepdims=True))
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids.reshape(-1), f32_to_dt(w.reshape(-1), bf16)
