@@ -1,23 +1,32 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X ternary GEMV (the int2 decode path), one JSON line.
+"""Benchmark of the MI355X ternary GEMV/GEMM library, one JSON line.
 
-Workload (the decode GEMV sweep): int2 upcvt GEMV, bf16 activations ~N(0,1),
-ternary weights p(-1,0,+1) = (.25,.5,.25) packed 2 bits/weight, per-128-group
-bf16 scales ~U[.005,.02], fused bias add (bias ~N(0,0.1)) + residual add
-(residual ~N(0,1)), shapes (K=4096, N=14336) and (K=14336, N=4096), M = 1.
-A step = one GEMV per shape.  Every call reads its own weight set out of a
-rotation of distinct sets totalling > 2 GiB per shape (the reference's
-cache-defeat rule, int2_fp16_upcvt/main.cpp:218-228), so weights stream from
-HBM, not from the 256 MB Infinity Cache.
+Headline workload (the decode GEMV sweep, M = 1): int2 upcvt GEMV, bf16
+activations ~N(0,1), ternary weights p(-1,0,+1) = (.25,.5,.25) packed 2
+bits/weight, per-128-group bf16 scales ~U[.005,.02], fused bias add (bias
+~N(0,0.1)) + residual add (residual ~N(0,1)), shapes (K=4096, N=14336) and
+(K=14336, N=4096).  A step = one GEMV per shape.  Every call reads its own
+weight set out of a rotation of distinct sets totalling > 2 GiB per shape (the
+reference's cache-defeat rule, int2_fp16_upcvt/main.cpp:218-228), so weights
+stream from HBM, not from the 256 MB Infinity Cache.
+
+The same line reports the metric's prefill half and the other workloads,
+each timed the same way (> 2 GiB rotation, HIP-graph replays between events):
+  prefill  int2 x int8 prefill M=1024 K=4096 N=14336 fp16, quant_a pre-kernel
+           + s8 x s2 GEMM (TOPS, fraction of the 5.0 POPS int8 peak)
+  c1       int2 GEMV M=1 K=N=4096 fp16, no epilogue
+  c4       FWHT (HB 512, sign flip) + BITCOS GEMV M=1 K=5376 N=21504, z = .3/.5/.7
+  c5       int2 MoE prefill layer T=2048 E=64 top-8 H=2048 I=1408 bf16
+           (TFLOPS, fraction of the 2.5 PFLOPS bf16 peak)
 
 Timing: the W warm-up steps and then exactly K timed steps are captured in HIP
-graphs (so host launch overhead stays off the GPU timeline) and replayed on one
-stream between HIP events, after a device synchronize; the per-shape launch
-duration comes from a graph of that shape's launches alone.  Bytes follow the
-reference byte model (int2_fp16_upcvt/main.cpp:331-333): A + B + S + C + Other
-+ Bias.  Also reported: M = 2, 4, 8 of the sweep, the VALU engine, and the
-reference's own host gold (compiled from its sources into oracle/_ref) timed on
-this machine's CPU cores as the cpu_baseline.
+graphs (host launch overhead stays off the GPU timeline) and replayed on one
+stream between HIP events, after a device synchronize; per-kernel durations
+come from graphs of that kernel's launches alone.  Bytes follow the reference
+byte models (int2_fp16_upcvt/main.cpp:331-333, bitcos_fp16_upcvt/main.cpp:289-293),
+ops 2*M*N*K (int2_moe/prefill.cpp:350 for the MoE layer).  The CPU baseline is
+the reference's own host gold (compiled from its sources into oracle/_ref)
+timed on this machine's CPU cores.
 """
 from __future__ import annotations
 
@@ -35,6 +44,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA, 2.5 PFLOPS
+METRIC = "GEMV weight-stream GB/s (%HBM peak) at M=1; prefill TOPS (%MFMA peak) at M=1024"
 SHAPES = [(4096, 14336), (14336, 4096)]
 WEIGHT_ROTATION_BYTES = 2 * 2**30
 POSTOP_BIAS_RESIDUAL = 5
@@ -164,6 +176,200 @@ def cpu_baseline(sample_s: float):
                       f"M=1 K={K} N={N} bf16 in {el:.1f} s ({per * 1e3:.2f} ms/call), OpenMP over outputs"}
 
 
+def rotation(torch, tensors, set_bytes):
+    """Copies of the device tensors making > 2 GiB of distinct weight sets."""
+    sets = max(1, math.ceil(WEIGHT_ROTATION_BYTES / set_bytes))
+    return sets, [[t.clone() for t in tensors] for _ in range(sets)]
+
+
+def graph_time_us(torch, fn, n):
+    """Average duration of one fn() call from a HIP graph of n calls (warm replay first)."""
+    g, s = graph_of(torch, fn, n)
+    time_graph(torch, g, s)
+    return time_graph(torch, g, s) / n * 1e6
+
+
+def dev16(torch, a, bf16):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(
+        torch.bfloat16 if bf16 else torch.float16)
+
+
+def dev32(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).cuda()
+
+
+def bench_c1(torch, T, synth, formats, orc):
+    """int2 GEMV M=1 K=N=4096 fp16, no epilogue."""
+    M, K, N, bf16 = 1, 4096, 4096, False
+    g = synth.rng(11)
+    A, B, S = synth.activations(g, (M, K), bf16), synth.int2_weights(g, K, N), synth.scales(g, K, N, bf16)
+    dA = dev16(torch, A, bf16)
+    sets, W = rotation(torch, [dev32(torch, B), dev16(torch, S, bf16)], B.nbytes + S.nbytes)
+    dC = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    it = [0]
+
+    def call():
+        b, sc = W[it[0] % sets]
+        it[0] += 1
+        T.int2_fp16_upcvt_gemm(dA, b, sc, dC, None, None, M, N, K)
+    call()
+    torch.cuda.synchronize()
+    got = formats.dt_to_f32(dC.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    want = formats.dt_to_f32(orc.epilogue(orc.int2_gold(A, B, S, M, K, N, bf16), None, None, 0, False, bf16), bf16)
+    bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
+    us = graph_time_us(torch, call, 400)
+    nbytes = M * K * 2 + K * N / 4 + M * N * 2 + (K // 128) * N * 2
+    return {"workload": "int2 GEMV M=1 K=4096 N=4096 fp16, no epilogue", "us": round(us, 3),
+            "GB/s": round(nbytes / us / 1e3, 1), "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "bytes": int(nbytes), "weight_sets": sets, "parity_bad": bad}
+
+
+def bench_c3(torch, T, synth, formats, orc):
+    """int2 x int8 prefill M=1024 K=4096 N=14336 fp16: quant_a + s8 x s2 GEMM."""
+    M, K, N, bf16 = 1024, 4096, 14336, False
+    g = synth.rng(33)
+    A, B, SB = synth.activations(g, (M, K), bf16), synth.int2_weights(g, K, N), synth.scales(g, K, N, bf16)
+    dA = dev16(torch, A, bf16)
+    sets, W = rotation(torch, [dev32(torch, B), dev16(torch, SB, bf16)], B.nbytes + SB.nbytes)
+    dSA = torch.empty((K // 128, T.ldsa(M)), dtype=torch.float16, device="cuda")
+    dAq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    dC = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    it = [0]
+
+    def call():
+        b, sb = W[it[0] % sets]
+        it[0] += 1
+        T.quant_a(dA, dSA, dAq, M, K)
+        T.int2_int8_gemm(None, dAq, dSA, b, sb, dC, None, None, M, N, K)
+
+    def quant():
+        T.quant_a(dA, dSA, dAq, M, K)
+
+    def gemm():
+        b, sb = W[it[0] % sets]
+        it[0] += 1
+        T.int2_int8_gemm(None, dAq, dSA, b, sb, dC, None, None, M, N, K)
+
+    def upcvt():
+        b, sb = W[it[0] % sets]
+        it[0] += 1
+        T.int2_fp16_upcvt_gemm(dA, b, sb, dC, None, None, M, N, K)
+    call()
+    torch.cuda.synchronize()
+    rows = 8  # parity on the first rows (quantization and dots are per row)
+    SA = orc.scale_a(A[:rows], rows, K, bf16)
+    want = formats.dt_to_f32(orc.epilogue(orc.int8_gold(A[:rows], B, SA, SB, rows, K, N, bf16), None, None, 0,
+                                          False, bf16), bf16)
+    got = formats.dt_to_f32(dC[:rows].contiguous().view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
+    Aq_ok = bool(np.array_equal(dAq[:rows].cpu().numpy(), orc.quant_a(A[:rows], SA, rows, K, bf16)))
+    us = graph_time_us(torch, call, 40)
+    q_us = graph_time_us(torch, quant, 40)
+    g_us = graph_time_us(torch, gemm, 40)
+    u_us = graph_time_us(torch, upcvt, 20)
+    ops = 2.0 * M * N * K
+    tops = ops / us / 1e6
+    return {"workload": "int2_via_int2_x_int8 prefill M=1024 K=4096 N=14336 fp16, quant_a + s8 x s2 GEMM",
+            "value": round(tops, 1), "unit": "TOPS", "us": round(us, 2), "mfma_frac": round(tops / I8_PEAK_TOPS, 4),
+            "peak": I8_PEAK_TOPS, "quant_us": round(q_us, 2), "gemm_us": round(g_us, 2),
+            "gemm_TOPS": round(ops / g_us / 1e6, 1), "weight_sets": sets,
+            "parity_bad": bad, "parity_rows": rows, "quant_bit_exact": Aq_ok,
+            "upcvt_fp16_gemm": {"us": round(u_us, 2), "TFLOPS": round(ops / u_us / 1e6, 1),
+                                "mfma_frac": round(ops / u_us / 1e6 / BF16_PEAK_TFLOPS, 4)}}
+
+
+def bench_c4(torch, T, synth, formats, orc):
+    """FWHT (HB 512) + BITCOS GEMV M=1 K=5376 N=21504 fp16 at z = .3 / .5 / .7."""
+    M, K, N, HB, bf16 = 1, 5376, 21504, 512, False
+    out = {"workload": "sign flip + FWHT HB=512, then BITCOS GEMV M=1 K=5376 N=21504 fp16"}
+    for z in (0.3, 0.5, 0.7):
+        g = synth.rng(44 + int(10 * z))
+        x = synth.activations(g, (M, K), bf16)
+        buf, _ = synth.bitcos_weights(g, K, N, z)
+        S = synth.scales(g, K, N, bf16)
+        sgn = (g.integers(0, 2, K, dtype=np.int8) * 2 - 1).astype(np.int8)
+        ls = T.bitcos_pick_ls(M, N, K)
+        dx, ds = dev16(torch, x, bf16), torch.from_numpy(sgn).cuda()
+        dy = torch.empty_like(dx)
+        dB = dev32(torch, buf)
+        dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+        T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+        sets, W = rotation(torch, [dB, dev16(torch, S, bf16), dSR], buf.nbytes + S.nbytes)
+        dC = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        it = [0]
+
+        def fwht():
+            T.hadamard_fwht(dx, ds, dy, M, K, HB, True)
+
+        def gemv():
+            b, sc, sr = W[it[0] % sets]
+            it[0] += 1
+            T.bitcos_fp16_upcvt_gemm(dy, b, sc, sr, dC, None, None, M, N, K, ls)
+
+        def call():
+            fwht()
+            gemv()
+        call()
+        torch.cuda.synchronize()
+        y = orc.fwht(x, sgn, M, K, HB, True, bf16)
+        fwht_ok = bool(np.array_equal(dy.view(torch.int16).cpu().numpy().view(np.uint16), y))
+        want = formats.dt_to_f32(orc.epilogue(orc.bitcos_gold(y, buf, S, M, K, N, bf16), None, None, 0, False,
+                                              bf16), bf16)
+        got = formats.dt_to_f32(dC.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+        bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
+        us = graph_time_us(torch, call, 200)
+        g_us = graph_time_us(torch, gemv, 200)
+        f_us = graph_time_us(torch, fwht, 200)
+        nbytes = M * K * 2 + buf.nbytes + S.nbytes + M * N * 2  # bitcos_fp16_upcvt/main.cpp:289-291
+        out[f"z{z}"] = {"us": round(us, 2), "gemv_us": round(g_us, 2), "fwht_us": round(f_us, 2),
+                        "gemv_GB/s": round(nbytes / g_us / 1e3, 1),
+                        "gemv_hbm_frac": round(nbytes / g_us / 1e3 / HBM_PEAK_GBS, 4),
+                        "pipeline_GB/s": round((nbytes + 2 * M * K * 2 + K) / us / 1e3, 1),
+                        "bytes": int(nbytes), "ls": ls, "weight_sets": sets, "parity_bad": bad,
+                        "fwht_bit_exact": fwht_ok}
+        del W, dB, dSR
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_c5(torch, T, synth, formats, orc):
+    """int2 MoE prefill layer: T=2048 E=64 top-8, H=2048 I=1408, bf16, uniform routing."""
+    Tk, E, topk, H, I, bf16 = 2048, 64, 8, 2048, 1408, True
+    g = synth.rng(55)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+
+    def experts(K, N):
+        return (np.stack([synth.int2_weights(g, K, N) for _ in range(E)]),
+                np.stack([synth.scales(g, K, N, bf16) for _ in range(E)]))
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = experts(H, I), experts(H, I), experts(I, H)
+    layer_bytes = sum(a.nbytes for a in (Bg, Sg, Bu, Su, Bd, Sd))
+    sets, W = rotation(torch, [dev32(torch, Bg), dev16(torch, Sg, bf16), dev32(torch, Bu), dev16(torch, Su, bf16),
+                               dev32(torch, Bd), dev16(torch, Sd, bf16)], layer_bytes)
+    dX, dRW = dev16(torch, X, bf16), dev16(torch, RW, bf16)
+    dids = torch.from_numpy(ids).cuda()
+    dO = torch.empty((Tk, H), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(T.int2_moe_prefill_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def call():
+        bg, sg, bu, su, bd, sd = W[it[0] % sets]
+        it[0] += 1
+        T.int2_moe_prefill(dX, dids, dRW, Tk, E, topk, H, I, bg, sg, bu, su, bd, sd, dO, ws)
+    call()
+    torch.cuda.synchronize()
+    got = formats.dt_to_f32(dO.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    ref = orc.moe_ref_tokens(X, ids, RW, 0, 4, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16)
+    rel = float(np.abs(got[:4] - ref).max() / np.abs(ref).max())
+    us = graph_time_us(torch, call, 10)
+    flops = 2.0 * Tk * topk * (2.0 * H * I + I * H)  # int2_moe/prefill.cpp:350
+    tf = flops / us / 1e6
+    return {"workload": "int2 MoE prefill layer T=2048 E=64 top-8 H=2048 I=1408 bf16 (route, up, gate, down, combine)",
+            "value": round(tf, 1), "unit": "TFLOPS", "us": round(us, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+            "peak": BF16_PEAK_TFLOPS, "layers_rotated": sets, "layer_weight_bytes": int(layer_bytes),
+            "check_rel_err_4_tokens": rel, "check_pass": rel < 1e-2}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -171,7 +377,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-sample-s", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-sweep", action="store_true", help="skip the M = 2, 4, 8 sweep")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the M = 2, 4, 8 sweep and the VALU engine")
+    ap.add_argument("--only-headline", action="store_true", help="skip the prefill, C1, C4 and C5 workloads")
     ap.add_argument("--probe", type=int, default=0, metavar="N",
                     help="counter-collection mode for rocprofv3 --pmc: N eager launches per shape plus "
                          "a 64 MiB device copy (the calibration kernel of known size); prints one line")
@@ -260,13 +467,23 @@ def main():
             torch.cuda.empty_cache()
         extra["valu_engine_m1"] = valu
 
+    if not args.only_headline:
+        extra["prefill"] = bench_c3(torch, T, synth, formats, orc)
+        torch.cuda.empty_cache()
+        extra["c1"] = bench_c1(torch, T, synth, formats, orc)
+        torch.cuda.empty_cache()
+        extra["c4"] = bench_c4(torch, T, synth, formats, orc)
+        torch.cuda.empty_cache()
+        extra["c5"] = bench_c5(torch, T, synth, formats, orc)
+        torch.cuda.empty_cache()
+
     traffic = None
     tf = ROOT / "profiles" / "int2_gemv_m1_bf16_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_step")
 
     line = {
-        "metric": "GEMV weight-stream GB/s (%HBM peak) at M=1",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
