@@ -97,7 +97,8 @@ ternocl_status ternocl_workspace_zero(void *ws, size_t ws_bytes, void *stream);
  * W is DT [K, N].  The GEMVs' own in-register decodes are exported for testing
  * too: ternocl_int2_gemv_decode writes, per B word, the 8 packed DT pairs that
  * engine (1 = VALU GEMV, 2 = MFMA GEMV, 3 = prefill GEMM) builds (layout
- * [K/16][N][8] uint32). */
+ * [K/16][N][8] uint32); the prefill GEMM folds the group scale into its
+ * fragments, and the hook builds them at unit scale (DT 1.0). */
 ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
                                     int N, void *stream);
 ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,

@@ -42,7 +42,7 @@ ternocl_status int2_mfma_decode_run(int dtype, const uint32_t *B, uint32_t *D, i
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
                                   int postop, int out_f32, hipStream_t st);
-ternocl_status int2_gemm_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
+ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (int2_int8.hip)
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st);
 ternocl_status int2_int8_gemm_run(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
@@ -189,7 +189,7 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
     if (!B || !D) FAIL(TERNOCL_ERR_INVALID_ARG, "B and D must be non-null");
     if (engine < 1 || engine > 3) FAIL(TERNOCL_ERR_INVALID_ARG, "engine must be 1 (VALU), 2 (MFMA GEMV) or 3 (GEMM)");
     if (N < 16 || N % 16 || K < 16 || K % 16) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 16 == 0");
-    if (engine == 3) return int2_gemm_decode_run(B, D, K, N, (hipStream_t)stream);
+    if (engine == 3) return int2_gemm_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     if (engine == 2) return int2_mfma_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     return int2_gemv_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
 }

@@ -3,24 +3,27 @@
 // (int2_fp16_upcvt/int2_fp16_upcvt.cl:292-395), and the tile engine of the MoE
 // prefill (int2_moe/int2_moe_prefill.cl:72-141).
 //
-//   C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(B[k,n])))
+//   C[m,n] = ct(epi(sum_k A[m,k] * w(k,n))),  w(k,n) = code(k,n) * S[k/128, n]
 //
-// Tiling: a workgroup of 4 waves computes a 128 x 128 tile of C; each wave a
-// 64 x 64 quarter as 4 x 4 v_mfma_f32_16x16x32_{f16,bf16} tiles.  K advances
-// one 128-row scale group at a time (4 MFMA k-steps of 32).
+// Tiling: a workgroup of 4 waves (2 x 2) computes a BM x BN tile of C, each
+// wave a (16 NMB) x (16 NCB) block as NMB x NCB v_mfma_f32_16x16x32_{f16,bf16}
+// tiles whose fp32 accumulators stay in registers (AGPRs for the large tiles)
+// over all of K.  K advances in LDS stages of 64 (two MFMA k-steps of 32).
 //   * A (DT, row-major) goes global -> registers -> LDS once per workgroup and
-//     group, each 16-element chunk stored in the order 0,8,1,9,...,7,15, so the
+//     stage, each 16-element chunk stored in the order 0,8,1,9,...,7,15, so the
 //     MFMA A fragment of lane (row, q) -- pairs (4h+i, 4h+i+8) of one chunk --
-//     is one 16-byte LDS read;
-//   * B is never expanded in memory: each wave loads the packed words of its 64
-//     columns (L2-resident across the M tiles) and decodes the MFMA B fragment
-//     in registers: for the pair of rows (j, j+8) of a word,
-//     (w << (14 - 2j)) & 0xC000C000 is exactly +-2.0 / 0 in fp16 and in bf16
-//     (the code's low bit lands on the exponent LSB, its high bit on the sign),
-//     two VALU ops per pair, no tables;
-//   * each group accumulates in its own fp32 MFMA accumulators (the chain for
-//     k-step 0 starts from zero), then one FMA per output element applies the
-//     group scale: acc += acc_g * (S[g,n] / 2);
+//     is one 16-byte LDS read (row pitch 72 elements: conflict-free);
+//   * B is never expanded in memory: each wave loads the packed words of its
+//     columns (L2-resident across the M tiles) and builds the MFMA B fragment
+//     in registers with the group scale folded in, as the reference's
+//     dequantising decode does (int2_fp16_upcvt.cl:118-150), so the MFMA chains
+//     run over all of K with no per-group rescale:
+//       fp16: (w << (14 - 2j)) & 0xC000C000 is exactly +-2.0 / 0 for the rows
+//             (j, j+8) of a word; one v_pk_mul_f16 by (s, s) gives +-2s exactly
+//             and the accumulators are halved once at the end;
+//       bf16: v_perm_b32 through per-column byte tables {0, s, 0, -s} (low and
+//             high bytes) indexed by the codes: selector = ((w >> 2j) &
+//             0x30003) * 0x101 + 0x04000400, one v_mad_u32_u24;
 //   * workgroup -> tile mapping keeps the M tiles of one column strip on one
 //     XCD, so a strip's packed weights are fetched into that XCD's L2 once.
 #include "common.hpp"
@@ -32,8 +35,9 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf168_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int BK = 64;           // K per LDS stage
 constexpr int A_PITCH = BK + 8;  // DT elements per LDS row (16 bytes of padding)
+constexpr int kMoeNMB = 4;       // MoE tiles: 128 rows (experts hold a few hundred rows each)
 
 template <bool BF16>
 __device__ __forceinline__ f32x4_t mfma16(const uint32_t a[4], const uint32_t b[4], f32x4_t c) {
@@ -50,12 +54,43 @@ __device__ __forceinline__ f32x4_t mfma16(const uint32_t a[4], const uint32_t b[
     }
 }
 
-// B fragment of half h of word w: dword i = rows (4h+i, 4h+i+8) as +-2.0 / 0.
-__device__ __forceinline__ void pm2_fragment(uint32_t w, int h, uint32_t b[4]) {
+// Per-column scale operand of the decode: fp16 (s, s) packed; bf16 the byte
+// tables lo = {0, s.lo, 0, s.lo}, hi = {0, s.hi, 0, s.hi ^ 0x80}.
+template <bool BF16> struct ScaleOp;
+template <> struct ScaleOp<false> {
+    uint32_t s2;
+    __device__ __forceinline__ void set(uint32_t s) { s2 = s | (s << 16); }
+};
+template <> struct ScaleOp<true> {
+    uint32_t lo, hi;
+    __device__ __forceinline__ void set(uint32_t s) {
+        const uint32_t l = s & 0xffu, h = (s >> 8) & 0xffu;
+        lo = (l << 8) | (l << 24);
+        hi = (h << 8) | ((h ^ 0x80u) << 24);
+    }
+};
+
+// B fragment of half h of word w with the scale folded in: dword i = rows
+// (4h+i, 4h+i+8) of the word as (w(j), w(j+8)); fp16 values are 2x the weight.
+__device__ __forceinline__ void frag(uint32_t w, int h, const ScaleOp<false> &sc, uint32_t b[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int j = 4 * h + i;
-        b[i] = (w << (14 - 2 * j)) & 0xC000C000u;
+        const uint32_t t = (w << (14 - 2 * j)) & 0xC000C000u;  // +-2.0 / +-0 per half
+        half2_t x, y;
+        __builtin_memcpy(&x, &t, 4);
+        __builtin_memcpy(&y, &sc.s2, 4);
+        const half2_t r = x * y;  // v_pk_mul_f16: exact
+        __builtin_memcpy(&b[i], &r, 4);
+    }
+}
+__device__ __forceinline__ void frag(uint32_t w, int h, const ScaleOp<true> &sc, uint32_t b[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int j = 4 * h + i;
+        const uint32_t x = (w >> (2 * j)) & 0x00030003u;  // codes of rows j (byte 0), j+8 (byte 2)
+        const uint32_t sel = __umul24(x, 0x101u) + 0x04000400u;  // v_mad_u32_u24
+        b[i] = __builtin_amdgcn_perm(sc.hi, sc.lo, sel);
     }
 }
 
@@ -80,159 +115,198 @@ struct ARows {
     }
 };
 
-// One 128 x 128 output tile of rows [m0, m0 + mrows) (mrows <= 128 valid) and
-// columns [n0, n0 + 128) (N % 16 == 0; columns >= N masked).
-template <bool BF16>
+template <int NMB, int NCB> struct TileCfg {
+    static constexpr int BM = 32 * NMB, BN = 32 * NCB;
+    static constexpr int ACH = BM / 64;  // 16-element A chunks per thread per stage
+    static constexpr size_t lds_elems = 2 * (size_t)BM * A_PITCH;
+};
+
+// One BM x BN output tile of rows [0, mrows) of ar (mrows <= BM) and columns
+// [n0, n0 + BN) (columns >= N masked); C row r is crow0 + r.
+template <int NMB, int NCB, bool BF16>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint32_t *__restrict__ B,
                                           const uint16_t *__restrict__ S, void *__restrict__ C,
                                           const uint16_t *__restrict__ Other, const void *__restrict__ Bias,
-                                          int ldc_rows_base, int N, int K, int n0, int postop,
-                                          int out_f32, uint16_t *lds) {
+                                          int crow0, int N, int K, int n0, int postop, int out_f32,
+                                          uint16_t *lds) {
+    using Cfg = TileCfg<NMB, NCB>;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c16 = lane & 15, q = lane >> 4;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // this wave's quarter
-    const int groups = K / kGS;
+    const int c16 = lane & 15, q = lane >> 4, h = q & 1;
+    const int wm = (wave >> 1) * 16 * NMB, wn = (wave & 1) * 16 * NCB;
+    const int stages = K / BK;
 
-    // A staging: thread tid owns rows (tid >> 3) + 32 * u (u = 0..3) and the
-    // 16-element chunk (tid & 7) of the group: 4 x 32 bytes per group.
-    const int arow0 = tid >> 3, achunk = tid & 7;
-    uint4 av[4][2];
-    auto a_load = [&](int g) {
+    // A staging: chunk id = tid + 256u -> row id >> 2, 16-element chunk id & 3
+    const uint16_t *arow[Cfg::ACH];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int r = arow0 + 32 * u;
-            const int rc = r < mrows ? r : mrows - 1;
-            const uint4 *p = (const uint4 *)(ar.row(rc, K) + (size_t)g * kGS + 16 * achunk);
+    for (int u = 0; u < Cfg::ACH; ++u) {
+        const int id = tid + 256 * u, r = id >> 2;
+        arow[u] = ar.row(r < mrows ? r : mrows - 1, K) + 16 * (id & 3);
+    }
+    uint4 av[Cfg::ACH][2];
+    auto a_load = [&](int st) {
+#pragma unroll
+        for (int u = 0; u < Cfg::ACH; ++u) {
+            const uint4 *p = (const uint4 *)(arow[u] + st * BK);
             av[u][0] = p[0];
             av[u][1] = p[1];
-            if (r >= mrows) av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
         }
     };
+    // Rows past mrows are zeroed here, not at the load: touching the loaded
+    // registers right after the loads would make the wave wait for them.
     auto a_store = [&](uint16_t *buf) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t v[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
-                                   av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
+        for (int u = 0; u < Cfg::ACH; ++u) {
+            const int id = tid + 256 * u;
+            const bool live = (id >> 2) < mrows;
+            const uint4 a0 = live ? av[u][0] : make_uint4(0, 0, 0, 0);
+            const uint4 a1 = live ? av[u][1] : make_uint4(0, 0, 0, 0);
+            const uint32_t v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             uint32_t o[8];
             chunk_interleave(v, o);
-            uint4 *d = (uint4 *)(buf + (size_t)(arow0 + 32 * u) * A_PITCH + 16 * achunk);
+            uint4 *d = (uint4 *)(buf + (size_t)(id >> 2) * A_PITCH + 16 * (id & 3));
             d[0] = make_uint4(o[0], o[1], o[2], o[3]);
             d[1] = make_uint4(o[4], o[5], o[6], o[7]);
         }
     };
 
-    // B words of this wave for group g: column block cb, k-step ks -> word
-    // (kp = 8g + 2ks + q/2, column n0 + wn + 16cb + c16); half q % 2.
-    uint32_t bw[4][4];
-    uint32_t sc[4];
-    auto b_load = [&](int g) {
+    // B words of this wave for stage st: block cb, k-step ks -> word
+    // kp = 4 st + 2 ks + q / 2 of column n0 + wn + 16 cb + c16, half q % 2
+    const uint32_t *bcol[NCB];
+    const uint16_t *scol[NCB];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            int n = n0 + wn + 16 * cb + c16;
-            n = n < N ? n : N - 1;
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int n = n0 + wn + 16 * cb + c16;
+        const int nc = n < N ? n : N - 1;
+        bcol[cb] = B + (size_t)(q >> 1) * N + nc;
+        scol[cb] = S + nc;
+    }
+    uint32_t bw[NCB][2], sraw[NCB];
+    auto b_load = [&](int st) {
+        const size_t r0 = (size_t)st * 4 * N;  // uniform
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) bw[cb][ks] = B[((size_t)g * 8 + 2 * ks + (q >> 1)) * N + n];
-            sc[cb] = S[(size_t)g * N + n];
-        }
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) bw[cb][ks] = bcol[cb][r0 + (size_t)(2 * ks) * N];
+    };
+    auto s_load = [&](int g) {
+        const size_t r0 = (size_t)g * N;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) sraw[cb] = scol[cb][r0];
     };
 
-    f32x4_t acc[4][4];
+    f32x4_t acc[NMB][NCB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int cb = 0; cb < NCB; ++cb) acc[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    ScaleOp<BF16> sop[NCB];
     a_load(0);
     b_load(0);
+    s_load(0);
     a_store(lds);
-    for (int g = 0; g < groups; ++g) {
-        __syncthreads();  // A tile g staged, tile g-1 consumed
-        const uint16_t *abuf = lds + (size_t)(g & 1) * BM * A_PITCH;
-        uint32_t bwc[4][4], scc[4];
+    for (int st = 0; st < stages; ++st) {
+        __syncthreads();  // stage st staged; stage st - 1 consumed
+        const uint16_t *abuf = lds + (size_t)(st & 1) * Cfg::BM * A_PITCH;
+        uint32_t bwc[NCB][2];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            scc[cb] = sc[cb];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) bwc[cb][ks] = bw[cb][ks];
+        for (int cb = 0; cb < NCB; ++cb) {
+            bwc[cb][0] = bw[cb][0];
+            bwc[cb][1] = bw[cb][1];
         }
-        const bool more = g + 1 < groups;
-        if (more) {  // next group's loads in flight during this group's MFMAs
-            a_load(g + 1);
-            b_load(g + 1);
+        if ((st & 1) == 0) {  // a new 128-row scale group
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) sop[cb].set(sraw[cb]);
         }
-        f32x4_t accg[4][4];
+        const bool more = st + 1 < stages;
+        if (more) {  // next stage's loads in flight during this stage's MFMAs
+            a_load(st + 1);
+            b_load(st + 1);
+            if (st & 1) s_load((st + 1) >> 1);
+        }
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            uint32_t af[4][4];
+        for (int ks = 0; ks < 2; ++ks) {
+            uint32_t af[NMB][4];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
+            for (int mb = 0; mb < NMB; ++mb) {
                 const uint4 v = *(const uint4 *)(abuf + (size_t)(wm + 16 * mb + c16) * A_PITCH +
-                                                 (2 * ks + (q >> 1)) * 16 + 8 * (q & 1));
+                                                 (2 * ks + (q >> 1)) * 16 + 8 * h);
                 af[mb][0] = v.x; af[mb][1] = v.y; af[mb][2] = v.z; af[mb][3] = v.w;
             }
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
+            for (int cb = 0; cb < NCB; ++cb) {
                 uint32_t bf[4];
-                pm2_fragment(bwc[cb][ks], q & 1, bf);
+                frag(bwc[cb][ks], h, sop[cb], bf);
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
-                    accg[mb][cb] = mfma16<BF16>(af[mb], bf, ks == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : accg[mb][cb]);
+                for (int mb = 0; mb < NMB; ++mb) acc[mb][cb] = mfma16<BF16>(af[mb], bf, acc[mb][cb]);
             }
         }
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            const float s = 0.5f * dt2f<BF16>(scc[cb]);
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) acc[mb][cb] = accg[mb][cb] * s + acc[mb][cb];
-        }
-        if (more) a_store(lds + (size_t)((g + 1) & 1) * BM * A_PITCH);
+        if (more) a_store(lds + (size_t)((st + 1) & 1) * Cfg::BM * A_PITCH);
     }
 
-    // lane holds rows wm + 16mb + 4q + i of column wn + 16cb + c16
+    // Epilogue through LDS, one 16-column block at a time: lane (c16, q) holds
+    // rows 16mb + 4q + i of column 16cb + c16; it writes them to its wave's
+    // [16 NMB][kEpPitch] fp32 block, then reads back 4 adjacent columns of one
+    // row for epi_store4.  (Reading the accumulators only in fully unrolled
+    // loops also keeps the array in registers.)
+    const float fix = BF16 ? 1.0f : 0.5f;  // fp16 fragments carry 2x the weight
+    constexpr int kEpPitch = 20;           // floats per row: 16 + 4 (16-byte aligned rows)
+    float *ct = (float *)lds + (size_t)wave * 16 * NMB * kEpPitch;
+    __syncthreads();  // the A buffers are free
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-        const int n = n0 + wn + 16 * cb + c16;
-        if (n >= N) continue;
+    for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int mb = 0; mb < NMB; ++mb) {
+            const f32x4_t v = acc[mb][cb] * fix;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = wm + 16 * mb + 4 * q + i;
-                if (r < mrows)
-                    epi_store1<BF16>(C, Other, Bias, postop, out_f32, N, ldc_rows_base + r, n, acc[mb][cb][i]);
-            }
+            for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * kEpPitch + c16] = v[i];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
+        for (int pass = 0; pass < NMB; ++pass) {
+            const int r = wm + 16 * pass + (lane >> 2);
+            const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * kEpPitch + 4 * (lane & 3));
+            const float v4[4] = {t.x, t.y, t.z, t.w};
+            if (r < mrows && n < N) epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, crow0 + r, n, v4);
+        }
+        __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
     }
 }
 
-template <bool BF16>
+template <int NMB, int NCB, bool BF16>
 __global__ void __launch_bounds__(256)
 k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
             const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BM * A_PITCH];  // 68 KiB
-    const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+    using Cfg = TileCfg<NMB, NCB>;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
+    const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
     int tm, tn;
     xcd_tile_of(blockIdx.x, mt, nt, tm, tn);
-    const ARows ar{A + (size_t)tm * BM * K, nullptr, 1};
-    const int mrows = min(BM, M - tm * BM);
-    gemm_tile<BF16>(ar, mrows, B, S, C, Other, Bias, tm * BM, N, K, tn * BN, postop, out_f32, lds);
+    const ARows ar{A + (size_t)tm * Cfg::BM * K, nullptr, 1};
+    const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
+    gemm_tile<NMB, NCB, BF16>(ar, mrows, B, S, C, Other, Bias, tm * Cfg::BM, N, K, tn * Cfg::BN, postop,
+                              out_f32, lds);
 }
 
 // Grouped GEMM of the MoE prefill (int2_moe/int2_moe_prefill.cl:72-141): the
 // rows of each expert e are meta[e] .. meta[e+1]-1 of the expert-sorted order,
-// cut into 128-row tiles numbered from meta[E+1+e]; workgroup (tile, column
-// block) finds its expert by binary search over the tile offsets.  A rows come
-// from A_all[perm[p] / topk] when perm is given (the gather fused into the
-// A-tile load), else from A_all[p].  Expert e's weights: B_all + e*(K/16)*N,
-// S_all + e*(K/128)*N; C and Other are indexed by the sorted row p.
-template <bool BF16>
+// cut into tiles of moe_tile_rows() rows numbered from meta[E+1+e]; workgroup
+// (tile, column block) finds its expert by binary search over the tile
+// offsets.  A rows come from A_all[perm[p] / topk] when perm is given (the
+// gather fused into the A-tile load), else from A_all[p].  Expert e's weights:
+// B_all + e*(K/16)*N, S_all + e*(K/128)*N; C and Other are indexed by the
+// sorted row p.
+template <int NCB, bool BF16>
 __global__ void __launch_bounds__(256)
 k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all,
                 const int *__restrict__ perm, int topk, const uint32_t *__restrict__ B_all,
                 const uint16_t *__restrict__ S_all, void *__restrict__ C_all,
                 const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
                 int ntn) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BM * A_PITCH];
+    using Cfg = TileCfg<kMoeNMB, NCB>;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
     if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
     int lo = 0, hi = E - 1;
@@ -242,65 +316,121 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
         else hi = mid - 1;
     }
     const int e = lo, row0 = meta[e];
-    const int m0 = (tile - meta[E + 1 + e]) * BM;
-    const int mrows = min(BM, meta[e + 1] - row0 - m0);
+    const int m0 = (tile - meta[E + 1 + e]) * Cfg::BM;
+    const int mrows = min(Cfg::BM, meta[e + 1] - row0 - m0);
     const ARows ar = perm ? ARows{A_all, perm + row0 + m0, topk}
                           : ARows{A_all + (size_t)(row0 + m0) * K, nullptr, 1};
-    gemm_tile<BF16>(ar, mrows, B_all + (size_t)e * (K / 16) * N, S_all + (size_t)e * (K / kGS) * N, C_all,
-                    Other_all, nullptr, row0 + m0, N, K, tn * BN, postop, out_f32, lds);
+    gemm_tile<kMoeNMB, NCB, BF16>(ar, mrows, B_all + (size_t)e * (K / 16) * N, S_all + (size_t)e * (K / kGS) * N,
+                                  C_all, Other_all, nullptr, row0 + m0, N, K, tn * Cfg::BN, postop, out_f32, lds);
 }
 
-// Test hook: the B fragments the GEMM builds, D[word][0..3] = half 0,
-// D[word][4..7] = half 1 (the same bits for fp16 and bf16).
+// Test hook: the B fragments the GEMM builds at unit scale (DT 1.0),
+// D[word][0..3] = half 0, D[word][4..7] = half 1.
+template <bool BF16>
 __global__ void k_int2_gemm_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, int words) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= words) return;
+    ScaleOp<BF16> one;
+    one.set(BF16 ? 0x3F80u : 0x3C00u);
     uint32_t b[8];
-    pm2_fragment(B[i], 0, b);
-    pm2_fragment(B[i], 1, b + 4);
+    frag(B[i], 0, one, b);
+    frag(B[i], 1, one, b + 4);
     uint4 *d = (uint4 *)(D + (size_t)i * 8);
     d[0] = make_uint4(b[0], b[1], b[2], b[3]);
     d[1] = make_uint4(b[4], b[5], b[6], b[7]);
 }
 
+// ---- host side: tile choice ----------------------------------------------------
+
+struct GemmPlan {
+    int nmb, ncb;
+};
+
+// Fewest idle MFMA slots over the machine (ragged tiles and the last partial
+// round of workgroups over the 256 CUs), weighted by the relative MAC rate of
+// each tile size (larger tiles decode fewer B words and read less A per MAC).
+GemmPlan gemm_plan(int M, int N) {
+    static const GemmPlan cands[] = {{8, 8}, {8, 4}, {4, 8}, {4, 4}};
+    static const double eff[] = {1.0, 0.88, 0.88, 0.75};
+    GemmPlan best = cands[3];
+    double best_t = 1e300;
+    for (int c = 0; c < 4; ++c) {
+        const int BM = 32 * cands[c].nmb, BN = 32 * cands[c].ncb;
+        const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+        const long rounds = (tiles + 255) / 256;
+        const double t = (double)rounds * BM * BN / eff[c];
+        if (t < best_t * 0.999) {
+            best_t = t;
+            best = cands[c];
+        }
+    }
+    return best;
+}
+
+template <int NMB, int NCB, bool BF16>
+void gemm_launch(const void *A, const uint32_t *B, const void *S, void *C, const void *Other, const void *Bias,
+                 int M, int N, int K, int postop, int out_f32, hipStream_t st) {
+    using Cfg = TileCfg<NMB, NCB>;
+    const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
+    hipLaunchKernelGGL((k_int2_gemm<NMB, NCB, BF16>), dim3(mt * nt), dim3(256), 0, st, (const uint16_t *)A, B,
+                       (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
+}
+
+template <bool BF16>
+void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const void *S, void *C,
+                   const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
+                   hipStream_t st) {
+    if (p.nmb == 8 && p.ncb == 8) gemm_launch<8, 8, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.nmb == 8) gemm_launch<8, 4, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.ncb == 8) gemm_launch<4, 8, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else gemm_launch<4, 4, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+}
+
+template <int NCB, bool BF16>
+void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, const uint32_t *B_all,
+                const void *S_all, void *C_all, const void *Other_all, int E, int G, int N, int K, int postop,
+                int out_f32, hipStream_t st) {
+    using Cfg = TileCfg<kMoeNMB, NCB>;
+    const int ntn = (N + Cfg::BN - 1) / Cfg::BN;
+    const int max_tiles = (G + Cfg::BM - 1) / Cfg::BM + E;  // each expert's ragged tail adds at most one tile
+    hipLaunchKernelGGL((k_int2_moe_gemm<NCB, BF16>), dim3((unsigned)(max_tiles * ntn)), dim3(256), 0, st, meta,
+                       (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
+                       (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn);
+}
+
 }  // namespace
 
-int moe_tile_rows() { return BM; }
+int moe_tile_rows() { return TileCfg<kMoeNMB, 4>::BM; }
 
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
                             int E, int G, int N, int K, int postop, int out_f32, hipStream_t st) {
-    const int ntn = (N + BN - 1) / BN;
-    const int max_tiles = (G + BM - 1) / BM + E;  // each expert's ragged tail adds at most one tile
-    const dim3 grid((unsigned)(max_tiles * ntn)), block(256);
-    if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL(k_int2_moe_gemm<true>, grid, block, 0, st, meta, (const uint16_t *)A_all, perm, topk,
-                           B_all, (const uint16_t *)S_all, C_all, (const uint16_t *)Other_all, E, N, K, postop,
-                           out_f32, ntn);
-    else
-        hipLaunchKernelGGL(k_int2_moe_gemm<false>, grid, block, 0, st, meta, (const uint16_t *)A_all, perm, topk,
-                           B_all, (const uint16_t *)S_all, C_all, (const uint16_t *)Other_all, E, N, K, postop,
-                           out_f32, ntn);
+    const bool wide = N % 256 == 0;  // 256-column tiles when they divide N, else 128
+    if (dtype == TERNOCL_BF16) {
+        if (wide) moe_launch<8, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else moe_launch<4, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+    } else {
+        if (wide) moe_launch<8, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else moe_launch<4, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+    }
     return check_launch();
 }
 
-ternocl_status int2_gemm_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st) {
+ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st) {
     const int words = K / 16 * N;
-    hipLaunchKernelGGL(k_int2_gemm_decode, dim3((words + 255) / 256), dim3(256), 0, st, B, D, words);
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL(k_int2_gemm_decode<true>, dim3((words + 255) / 256), dim3(256), 0, st, B, D, words);
+    else
+        hipLaunchKernelGGL(k_int2_gemm_decode<false>, dim3((words + 255) / 256), dim3(256), 0, st, B, D, words);
     return check_launch();
 }
 
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
                                   int postop, int out_f32, hipStream_t st) {
-    const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
-    const dim3 grid(mt * nt), block(256);
-    if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL(k_int2_gemm<true>, grid, block, 0, st, (const uint16_t *)A, B,
-                           (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
-    else
-        hipLaunchKernelGGL(k_int2_gemm<false>, grid, block, 0, st, (const uint16_t *)A, B,
-                           (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
+    const GemmPlan p = gemm_plan(M, N);
+    if (dtype == TERNOCL_BF16) gemm_dispatch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else gemm_dispatch<false>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     return check_launch();
 }
 

@@ -142,7 +142,6 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
             const int r = arow0 + 32 * u;
             const int rc = r < mrows ? r : mrows - 1;
             av[u] = *(const uint4 *)(Aq + (size_t)(m0 + rc) * K + (size_t)g * kGS + 16 * achunk);
-            if (r >= mrows) av[u] = make_uint4(0, 0, 0, 0);
         }
     };
     uint32_t sa_raw = 0;
@@ -152,7 +151,9 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
     auto a_store = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint32_t d[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
+            // rows past mrows are zeroed here, not at the load (that would wait for it)
+            const uint4 a = arow0 + 32 * u < mrows ? av[u] : make_uint4(0, 0, 0, 0);
+            const uint32_t d[4] = {a.x, a.y, a.z, a.w};
             uint32_t o[4];
             transpose4x4(d, o);
             *(uint4 *)(&lds_a[buf][(arow0 + 32 * u) * QA_PITCH + 16 * achunk]) = make_uint4(o[0], o[1], o[2], o[3]);

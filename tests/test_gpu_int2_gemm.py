@@ -107,26 +107,27 @@ def test_gemm_explicit_gemv_engine_rejected_above_16(dev):
         assert e.value.status == 2
 
 
-def test_gemm_decode_bit_exact(dev):
-    """The GEMM's in-register B fragment: dword 4h+i of a word holds rows
-    (4h+i, 4h+i+8) as code << 14 in each half, i.e. exactly 2x the signed
-    weight (+-2.0 / 0) in fp16 and in bf16."""
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemm_decode_bit_exact(dev, bf16):
+    """The GEMM's in-register B fragment at unit scale: dword 4h+i of a word
+    holds rows (4h+i, 4h+i+8).  fp16: code << 14 in each half times 1.0, i.e.
+    exactly 2x the signed weight (+-2.0 / +-0); bf16: the byte-table decode,
+    +1.0 / -1.0 / +0 (code 2 reads as 0, as the reference's select decode)."""
     import torch
     import ternocl_amd as T
     K, N = 256, 64
     g = synth.rng(8)
-    B = synth.int2_weights(g, K, N)
+    B = g.integers(0, 2**32, size=(K // 16, N), dtype=np.uint32)  # all four codes
     D = torch.empty(((K // 16) * N * 8,), dtype=torch.int32, device="cuda")
-    T.int2_gemv_decode(dev_raw(B), D, K, N, False, engine=T.GEMM)
+    T.int2_gemv_decode(dev_raw(B), D, K, N, bf16, engine=T.GEMM)
     torch.cuda.synchronize()
     got = host_u32(D).reshape(K // 16, N, 8)
     codes = ((B[..., None] >> (2 * np.arange(16, dtype=np.uint32))) & 3).astype(np.uint32)
-    sv = formats.unpack_int2(B, K).reshape(K // 16, 16, N).transpose(0, 2, 1)
+    if bf16:
+        lut = np.array([0x0000, 0x3F80, 0x0000, 0xBF80], np.uint32)
+    else:
+        lut = np.array([0x0000, 0x4000, 0x8000, 0xC000], np.uint32)
     for d in range(8):
         j = d  # dword 4h+i covers row j = 4h+i (low half) and j + 8 (high half)
-        want = (codes[..., j] << 14) | (codes[..., j + 8] << 30)
+        want = lut[codes[..., j]] | (lut[codes[..., j + 8]] << 16)
         assert np.array_equal(got[..., d], want.astype(np.uint32)), f"dword {d}"
-        for half, row in ((0, j), (1, j + 8)):
-            bits = ((got[..., d] >> (16 * half)) & 0xFFFF).astype(np.uint16)
-            for bf16 in (False, True):
-                assert np.array_equal(formats.dt_to_f32(bits, bf16), 2.0 * sv[..., row])
