@@ -73,7 +73,7 @@ typedef struct {
     int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: MFMA GEMV (M <= 16);
                             3: MFMA prefill GEMM (any M, 128 x 128 tiles; the M > 16 engine) */
     int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
-    int cols_per_lane;   /* MFMA: adjacent columns per lane, 1 or 2 (16- or 32-column strips) */
+    int cols_per_lane;   /* MFMA: adjacent columns per lane, 1, 2 or 4 (16-, 32- or 64-column strips) */
     int groups_per_wave; /* MFMA: 128-row groups per wave per LDS window, 1..16 (power of
                             two, times M rounded up to a power of two <= 16) */
     int col_lanes;       /* VALU: lanes across a strip of 4*col_lanes columns, 4, 8 or 16 */
