@@ -134,6 +134,13 @@ __device__ __forceinline__ void epi_store1(void *C, const uint16_t *Other, const
     else ((uint16_t *)C)[i] = (uint16_t)f2dt<BF16>(r);
 }
 
+// Raw buffer resource over [p, p + bytes).  A buffer load whose VGPR offset
+// (plus its immediate offset) reaches `bytes` returns 0 instead of touching
+// memory; the SGPR offset is not range-checked.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // Workgroup -> (m tile, n tile) of a GEMM grid of mt x nt tiles.  Workgroups
 // are dealt to the 8 XCDs round-robin (x, x+8, x+16, ... run on XCD x); those
 // take all M tiles of column strip x, then of strip x+8, ... (when the strip

@@ -86,7 +86,6 @@ k_quant_a(const uint16_t *__restrict__ A, uint16_t *__restrict__ SA, int8_t *__r
 
 // ---- s8 x s2 GEMM ------------------------------------------------------------
 
-constexpr int QBM = 128, QBN = 128;
 constexpr int QA_PITCH = 144;  // bytes per LDS row of the A tile (128 + 16: conflict-free b128 reads)
 constexpr uint32_t kCodeLut = 0xFFFE0100u;  // int8 of code 0, 1, 2, 3
 
@@ -112,141 +111,197 @@ __device__ __forceinline__ i32x4_t decode_s2(uint32_t w) {
     return r;
 }
 
-template <bool BF16>
-__global__ void __launch_bounds__(256)
+// Tile shape: WVM x WVN waves, each owning MB x CB blocks of 16 x 16 outputs.
+template <int MB_, int CB_, int WVM_, int WVN_> struct QTile {
+    static constexpr int MB = MB_, CB = CB_, WVM = WVM_, WVN = WVN_;
+    static constexpr int THREADS = 64 * WVM * WVN;
+    static constexpr int BM = 16 * MB * WVM, BN = 16 * CB * WVN;
+    static constexpr int A_PER_THREAD = BM * 8 / THREADS;  // 16-byte A chunks per thread and group
+    static_assert(BM * 8 % THREADS == 0, "A chunks must divide evenly");
+    static_assert(BM <= THREADS, "one thread per tile row computes 1 / SA");
+    static constexpr int EP_PITCH = 20;  // epilogue floats per row: 16 + 4 (16-byte aligned rows)
+    static constexpr int STAGE_BYTES = 2 * BM * QA_PITCH + 2 * BM * 4;
+    static constexpr int EPI_BYTES = (THREADS / 64) * 16 * MB * EP_PITCH * 4;
+    static constexpr int LDS_BYTES = STAGE_BYTES > EPI_BYTES ? STAGE_BYTES : EPI_BYTES;
+};
+
+// This wave's packed B words and raw scale bits of one group.
+template <int CB> struct QBSlab {
+    uint32_t w[CB][2], sb[CB];
+};
+
+template <class TC, bool BF16>
+__global__ void __launch_bounds__(TC::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
                  const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB,
                  void *__restrict__ C, const uint16_t *__restrict__ Other,
                  const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][QBM * QA_PITCH];
-    __shared__ float lds_inv[2][QBM];
+    constexpr int MB = TC::MB, CB = TC::CB, BM = TC::BM, BN = TC::BN, AP = TC::A_PER_THREAD;
+    // LDS: two A tiles [BM][QA_PITCH] and two 1 / SA vectors [BM] while K runs,
+    // then the epilogue's per-wave transposition blocks
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TC::LDS_BYTES];
+    uint8_t (*lds_a)[BM * QA_PITCH] = (uint8_t (*)[BM * QA_PITCH])lds;
+    float (*lds_inv)[BM] = (float (*)[BM])(lds + 2 * BM * QA_PITCH);
 
-    const int mt = (M + QBM - 1) / QBM, nt = (N + QBN - 1) / QBN;
+    const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     int tm, tn;
     xcd_tile_of(blockIdx.x, mt, nt, tm, tn);
-    const int m0 = tm * QBM, n0 = tn * QBN;
-    const int mrows = min(QBM, M - m0);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int mrows = min(BM, M - m0);
     const int groups = K / kGS;
     const int lda = ldsa_of(M);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c16 = lane & 15, q = lane >> 4;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int wm = (wave / TC::WVN) * (16 * MB), wn = (wave % TC::WVN) * (16 * CB);
 
-    // A staging: thread tid owns the 16-byte chunk (tid & 7) of rows (tid >> 3) + 32u
+    // All operand loads are buffer loads whose per-lane offsets are set up
+    // once: per group only scalar offsets (A, SA) or one add per pointer (B,
+    // SB) change.  Loads are unconditional -- a load under a branch would be
+    // waited for at the branch's end -- and those of the group after the last
+    // read in-range memory or return 0.
+    //
+    // A staging: thread tid owns the 16-byte chunk (tid & 7) of rows
+    // (tid >> 3) + (THREADS / 8) u; rows past mrows lie past the buffer's end
+    // and load as 0.
+    constexpr int RSTEP = TC::THREADS / 8;
     const int arow0 = tid >> 3, achunk = tid & 7;
-    uint4 av[4];
-    auto a_load = [&](int g) {
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(Aq + (size_t)m0 * K, (uint32_t)((size_t)mrows * K));
+    uint32_t va[AP];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int r = arow0 + 32 * u;
-            const int rc = r < mrows ? r : mrows - 1;
-            av[u] = *(const uint4 *)(Aq + (size_t)(m0 + rc) * K + (size_t)g * kGS + 16 * achunk);
+    for (int u = 0; u < AP; ++u) va[u] = (uint32_t)((arow0 + RSTEP * u) * K + 16 * achunk);
+    uint4 av[AP];
+    auto a_load = [&](int g) {
+        const int gc = g < groups ? g : groups - 1;
+#pragma unroll
+        for (int u = 0; u < AP; ++u) {
+            const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u], gc * kGS, 0);
+            av[u] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
         }
     };
+    // 1 / SA of the tile's rows (thread tid < BM: row tid)
+    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - m0) * 2));
+    const uint32_t vsa = (uint32_t)(tid < BM ? tid : 0) * 2;
     uint32_t sa_raw = 0;
     auto sa_load = [&](int g) {
-        if (tid < QBM) sa_raw = SA[(size_t)g * lda + m0 + (tid < mrows ? tid : mrows - 1)];
+        const int gc = g < groups ? g : groups - 1;
+        sa_raw = __builtin_amdgcn_raw_buffer_load_b16(rSA, vsa, gc * lda * 2, 0);
     };
     auto a_store = [&](int buf) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            // rows past mrows are zeroed here, not at the load (that would wait for it)
-            const uint4 a = arow0 + 32 * u < mrows ? av[u] : make_uint4(0, 0, 0, 0);
-            const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+        for (int u = 0; u < AP; ++u) {
+            const uint32_t d[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
             uint32_t o[4];
             transpose4x4(d, o);
-            *(uint4 *)(&lds_a[buf][(arow0 + 32 * u) * QA_PITCH + 16 * achunk]) = make_uint4(o[0], o[1], o[2], o[3]);
+            *(uint4 *)(&lds_a[buf][(arow0 + RSTEP * u) * QA_PITCH + 16 * achunk]) = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        if (tid < QBM) {
+        if (tid < BM) {
             const float sa = dt2f<BF16>(sa_raw);
             lds_inv[buf][tid] = (tid < mrows && sa != 0.0f) ? 1.0f / sa : 0.0f;
         }
     };
-
     // B words of this wave for group g: block cb, k-step ks -> word kp = 8g + 4ks + q
-    uint32_t bw[4][2], sbr[4];
-    auto b_load = [&](int g) {
+    // of column n0 + wn + 16 cb + c16.  The offsets advance by a group per load
+    // (vb0, vb1, vsb), so a 16-column block past N (when N % BN != 0) reads the
+    // next row's words -- in range, and only feeding outputs that are not
+    // stored -- or, in the last row, 0.
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rSB = buf_rsrc(SB + n0, (uint32_t)(((size_t)groups * N - n0) * 2));
+    uint32_t vb0 = (uint32_t)((q * N + wn + c16) * 4), vb1 = vb0 + (uint32_t)(16 * N);
+    uint32_t vsb = (uint32_t)((wn + c16) * 2);
+    auto b_load = [&](QBSlab<CB> &sl) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            int n = n0 + wn + 16 * cb + c16;
-            n = n < N ? n : N - 1;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) bw[cb][ks] = B[((size_t)g * 8 + 4 * ks + q) * N + n];
-            sbr[cb] = SB[(size_t)g * N + n];
+        for (int cb = 0; cb < CB; ++cb) {
+            sl.w[cb][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb0 + 64 * cb, 0, 0);
+            sl.w[cb][1] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb1 + 64 * cb, 0, 0);
+            sl.sb[cb] = __builtin_amdgcn_raw_buffer_load_b16(rSB, vsb + 32 * cb, 0, 0);
         }
+        vb0 += (uint32_t)(32 * N);
+        vb1 += (uint32_t)(32 * N);
+        vsb += (uint32_t)(2 * N);
     };
 
-    f32x4_t acc[4][4];
+    f32x4_t acc[MB][CB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int cb = 0; cb < CB; ++cb) acc[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    a_load(0);
-    sa_load(0);
-    b_load(0);
-    a_store(0);
-    for (int g = 0; g < groups; ++g) {
+    // One group: issue the next group's loads, then the MFMAs of this group
+    // one 16-row block at a time, each block's int32 dots folded into the
+    // fp32 accumulators right away: acc += float(dot) * (SB * (1 / SA)).
+    auto group = [&](int g, const QBSlab<CB> &cur, QBSlab<CB> &nxt) __attribute__((always_inline)) {
         __syncthreads();  // tile g staged; tile g - 1 consumed
         const int buf = g & 1;
-        uint32_t bwc[4][2], sbc[4];
+        a_load(g + 1);
+        sa_load(g + 1);
+        b_load(nxt);
+        i32x4_t bf[CB][2];
+        float sbf[CB];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            sbc[cb] = sbr[cb];
-            bwc[cb][0] = bw[cb][0];
-            bwc[cb][1] = bw[cb][1];
+        for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) bf[cb][ks] = decode_s2(cur.w[cb][ks]);
+            sbf[cb] = dt2f<BF16>(cur.sb[cb]);
         }
-        const bool more = g + 1 < groups;
-        if (more) {  // next group's loads in flight during this group's MFMAs
-            a_load(g + 1);
-            sa_load(g + 1);
-            b_load(g + 1);
-        }
-        i32x4_t dot[4][4];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            i32x4_t af[4];
+        for (int mb = 0; mb < MB; ++mb) {
+            i32x4_t af[2];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
+            for (int ks = 0; ks < 2; ++ks) {
                 const uint4 v = *(const uint4 *)(&lds_a[buf][(wm + 16 * mb + c16) * QA_PITCH + (4 * ks + q) * 16]);
-                af[mb] = i32x4_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                af[ks] = i32x4_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const i32x4_t bf = decode_s2(bwc[cb][ks]);
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
-                    dot[mb][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        af[mb], bf, ks == 0 ? i32x4_t{0, 0, 0, 0} : dot[mb][cb], 0, 0, 0);
-            }
-        }
-        // fold the group into the fp32 accumulators: acc += float(dot) * (SB * (1 / SA))
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
             const f32x4_t inv = *(const f32x4_t *)(&lds_inv[buf][wm + 16 * mb + 4 * q]);
+            i32x4_t dot[CB];
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const float sb = dt2f<BF16>(sbc[cb]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[mb][cb][i] += (float)dot[mb][cb][i] * (sb * inv[i]);
+            for (int cb = 0; cb < CB; ++cb) {
+                dot[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0], bf[cb][0], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+                dot[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[1], bf[cb][1], dot[cb], 0, 0, 0);
             }
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mb][cb][i] += (float)dot[cb][i] * (sbf[cb] * inv[i]);
         }
-        if (more) a_store(buf ^ 1);
+        a_store(buf ^ 1);  // after the last group: harmless, never read
+    };
+
+    QBSlab<CB> cur;
+    a_load(0);
+    sa_load(0);
+    b_load(cur);
+    a_store(0);
+    for (int g = 0; g < groups; ++g) {
+        QBSlab<CB> nxt;
+        group(g, cur, nxt);
+        cur = nxt;
     }
 
-    // lane holds rows wm + 16mb + 4q + i of column wn + 16cb + c16
+    // Epilogue through LDS, one 16-column block at a time: lane (c16, q) holds
+    // rows wm + 16mb + 4q + i of column wn + 16cb + c16; it writes them to its
+    // wave's [16 MB][EP_PITCH] fp32 block, then reads back 4 adjacent columns of
+    // one row for epi_store4.  (Reading the accumulators only in fully unrolled
+    // loops with small bodies keeps the array in registers.)
+    constexpr int EP = TC::EP_PITCH;
+    float *ct = (float *)lds + (size_t)wave * 16 * MB * EP;
+    __syncthreads();  // the A tiles are free
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-        const int n = n0 + wn + 16 * cb + c16;
-        if (n >= N) continue;
+    for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = wm + 16 * mb + 4 * q + i;
-                if (r < mrows) epi_store1<BF16>(C, Other, Bias, postop, out_f32, N, m0 + r, n, acc[mb][cb][i]);
-            }
+            for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * EP + c16] = acc[mb][cb][i];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
+        for (int pass = 0; pass < MB; ++pass) {
+            const int r = wm + 16 * pass + (lane >> 2);
+            const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * EP + 4 * (lane & 3));
+            const float v4[4] = {t.x, t.y, t.z, t.w};
+            if (r < mrows && n < N) epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, m0 + r, n, v4);
+        }
+        __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
     }
 }
 
@@ -272,18 +327,32 @@ ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M
     return check_launch();
 }
 
+template <class TC>
+static hipError_t int8_gemm_launch(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
+                                   const void *SB, void *C, const void *Other, const void *Bias, int M,
+                                   int N, int K, int postop, int out_f32, hipStream_t st) {
+    const int mt = (M + TC::BM - 1) / TC::BM, nt = (N + TC::BN - 1) / TC::BN;
+    const dim3 grid(mt * nt), block(TC::THREADS);
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL((k_int2_int8_gemm<TC, true>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
+                           (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
+    else
+        hipLaunchKernelGGL((k_int2_int8_gemm<TC, false>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
+                           (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
+    return hipGetLastError();
+}
+
 ternocl_status int2_int8_gemm_run(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
                                   const void *SB, void *C, const void *Other, const void *Bias, int M,
                                   int N, int K, int postop, int out_f32, hipStream_t st) {
-    const int mt = (M + QBM - 1) / QBM, nt = (N + QBN - 1) / QBN;
-    const dim3 grid(mt * nt), block(256);
-    if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL(k_int2_int8_gemm<true>, grid, block, 0, st, Aq, (const uint16_t *)SA, B,
-                           (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
-    else
-        hipLaunchKernelGGL(k_int2_int8_gemm<false>, grid, block, 0, st, Aq, (const uint16_t *)SA, B,
-                           (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
-    return check_launch();
+    // 128 x 128 tiles, 2 x 2 waves of 64 x 64: 213 VGPRs, two waves per SIMD
+    // (a 128-row wave tile's 128 fp32 accumulators do not fit beside the rest)
+    typedef QTile<4, 4, 2, 2> Tile;
+    if ((size_t)M * K >= (1u << 31) || (size_t)(K / 16) * N * 4 >= (1u << 31)) {
+        set_error("int2_int8_gemm: M*K and K*N/4 must be below 2^31 bytes");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    return launch_status(int8_gemm_launch<Tile>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st));
 }
 
 ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st) {
