@@ -118,7 +118,7 @@ template <int MB_, int CB_, int WVM_, int WVN_> struct QTile {
     static constexpr int BM = 16 * MB * WVM, BN = 16 * CB * WVN;
     static constexpr int A_PER_THREAD = BM * 8 / THREADS;  // 16-byte A chunks per thread and group
     static_assert(BM * 8 % THREADS == 0, "A chunks must divide evenly");
-    static_assert(BM <= THREADS, "one thread per tile row computes 1 / SA");
+    static_assert(THREADS % BM == 0 && (BM & (BM - 1)) == 0, "threads cover the tile rows evenly (1 / SA)");
     static constexpr int EP_PITCH = 20;  // epilogue floats per row: 16 + 4 (16-byte aligned rows)
     static constexpr int STAGE_BYTES = 2 * BM * QA_PITCH + 2 * BM * 4;
     static constexpr int EPI_BYTES = (THREADS / 64) * 16 * MB * EP_PITCH * 4;
@@ -181,7 +181,10 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
     };
     // 1 / SA of the tile's rows (thread tid < BM: row tid)
     const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - m0) * 2));
-    const uint32_t vsa = (uint32_t)(tid < BM ? tid : 0) * 2;
+    // threads t and t + BM (when THREADS = 2 BM) load and write the same row's
+    // value, so the store below needs no branch
+    const int srow = tid & (BM - 1);
+    const uint32_t vsa = (uint32_t)srow * 2;
     uint32_t sa_raw = 0;
     auto sa_load = [&](int g) {
         const int gc = g < groups ? g : groups - 1;
@@ -195,10 +198,8 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
             transpose4x4(d, o);
             *(uint4 *)(&lds_a[buf][(arow0 + RSTEP * u) * QA_PITCH + 16 * achunk]) = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        if (tid < BM) {
-            const float sa = dt2f<BF16>(sa_raw);
-            lds_inv[buf][tid] = (tid < mrows && sa != 0.0f) ? 1.0f / sa : 0.0f;
-        }
+        const float sa = dt2f<BF16>(sa_raw);
+        lds_inv[buf][srow] = (srow < mrows && sa != 0.0f) ? 1.0f / sa : 0.0f;
     };
     // B words of this wave for group g: block cb, k-step ks -> word kp = 8g + 4ks + q
     // of column n0 + wn + 16 cb + c16.  The offsets advance by a group per load
@@ -244,25 +245,48 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
             for (int ks = 0; ks < 2; ++ks) bf[cb][ks] = decode_s2(cur.w[cb][ks]);
             sbf[cb] = dt2f<BF16>(cur.sb[cb]);
         }
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            i32x4_t af[2];
+        // Software pipeline over the 16-row blocks: the two MFMAs of (mb, cb)
+        // are issued next to the fold of (mb - 1, cb), pinned in that order by
+        // scheduling barriers, so the matrix core and the VALU work side by
+        // side within the wave instead of in two long phases.
+        auto a_frag = [&](int mb, i32x4_t af[2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const uint4 v = *(const uint4 *)(&lds_a[buf][(wm + 16 * mb + c16) * QA_PITCH + (4 * ks + q) * 16]);
                 af[ks] = i32x4_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
-            const f32x4_t inv = *(const f32x4_t *)(&lds_inv[buf][wm + 16 * mb + 4 * q]);
-            i32x4_t dot[CB];
+        };
+        auto inv_of = [&](int mb) __attribute__((always_inline)) {
+            return *(const f32x4_t *)(&lds_inv[buf][wm + 16 * mb + 4 * q]);
+        };
+        i32x4_t dp[CB], dc[CB];
+        {
+            i32x4_t af[2];
+            a_frag(0, af);
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) {
-                dot[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0], bf[cb][0], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
-                dot[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[1], bf[cb][1], dot[cb], 0, 0, 0);
+                dp[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0], bf[cb][0], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+                dp[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[1], bf[cb][1], dp[cb], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int mb = 1; mb <= MB; ++mb) {
+            i32x4_t af[2];
+            if (mb < MB) a_frag(mb, af);
+            const f32x4_t inv = inv_of(mb - 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                if (mb < MB) {
+                    dc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0], bf[cb][0], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+                    dc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[1], bf[cb][1], dc[cb], 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mb - 1][cb][i] += (float)dp[cb][i] * (sbf[cb] * inv[i]);
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[mb][cb][i] += (float)dot[cb][i] * (sbf[cb] * inv[i]);
+            for (int cb = 0; cb < CB; ++cb) dp[cb] = dc[cb];
         }
         a_store(buf ^ 1);  // after the last group: harmless, never read
     };
