@@ -104,28 +104,33 @@ ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S,
 ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,
                                         int K, int N, void *stream);
 
-/* ---- int2 x int8 prefill (upfront quantization) -----------------------
+/* ---- int2 x int8 prefill ---------------------------------------------------
  * Replaces quant_a (int2_via_int2_x_int8_dpas/int2_int8_dpas.cl:105-106):
  *   SA[g, m] = DT(127 / max(absmax_{k in group g} |A[m, k]|, FLT_EPSILON))
  *   Aq[m, k] = sat_int8(round_to_nearest_even(A[m, k] * SA[k / 128, m]))
  * bit-exact with the reference's host quantization
  * (int2_via_int2_x_int8_dpas/main.cpp:82-103).  A: DT [M, K];
  * SA: DT [K/128, ternocl_ldsa(M)] (row pitch (M + 31) & ~31; the pad columns
- * are not written); Aq: int8 [M, K].  Constraints: K % 128 == 0, M >= 1. */
+ * are not written); Aq: int8 [M, K], or NULL to write SA only (the reference
+ * built without WRITE_Q, :119).  Constraints: K % 128 == 0, M >= 1. */
 int ternocl_ldsa(int M);
 ternocl_status ternocl_quant_a(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K,
                                void *stream);
 
 /* Replaces int2_int8_gemv / int2_int8_gemm_mt (int2_int8_dpas.cl:213-215,
- * :316-318) in their upfront-quantization mode (QMODE 0):
+ * :316-318) in both quantization modes:
  *   C[m,n] = ct(epi(sum_g float(sum_{k in g} Aq[m,k] * v(B[k,n])) * (SB[g,n] * (1/SA[g,m]))))
  * v = the 2-bit two's-complement value of the code (code 2 reads as -2, as
  * the reference's DPAS and host gold do).  The int32 group dot products are
  * exact; the fp32 rescale follows the host gold's order
- * (int2_via_int2_x_int8_dpas/main.cpp:113-116).  A (the DT activations the
- * reference's in-GEMM quantization mode reads) is not read and may be NULL;
- * Aq and SA come from ternocl_quant_a.  SB: DT [K/128, N]; B, C, Other, Bias,
- * postop and out_f32 as ternocl_int2_fp16_upcvt_gemm.  Any M >= 1. */
+ * (int2_via_int2_x_int8_dpas/main.cpp:113-116).  Aq non-NULL: upfront mode
+ * (QMODE 0), Aq and SA from ternocl_quant_a, A not read (may be NULL).
+ * Aq NULL: in-GEMM mode (QMODE 1, :21-27, :61-99): the DT activations A are
+ * quantized tile by tile with SA from ternocl_quant_a; the int8 values equal
+ * quant_a's for every finite input, so both modes give identical C.
+ * SB: DT [K/128, N]; B, C, Other, Bias, postop and out_f32 as
+ * ternocl_int2_fp16_upcvt_gemm.  Any M >= 1; the A operand (M*K elements of
+ * Aq or A) and B must each be below 2^31 bytes. */
 ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                       const uint32_t *B, const void *SB, void *C,
                                       const void *Other, const void *Bias, int M, int N, int K,

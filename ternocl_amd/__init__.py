@@ -153,14 +153,17 @@ def ldsa(M: int) -> int:
 
 def quant_a(A, SA, Aq, M: int, K: int, stream=None) -> None:
     """quant_a(A, SA, Aq, M, K) of int2_int8_dpas.cl:105: SA [K/128, ldsa(M)] DT scales
-    and Aq [M, K] int8, bit-exact with the reference's host quantization."""
+    and Aq [M, K] int8, bit-exact with the reference's host quantization.  Aq=None writes
+    SA only (the reference built without WRITE_Q, for the in-GEMM quantization mode)."""
     _check(lib().ternocl_quant_a(_dtype_of(A), _ptr(A), _ptr(SA), _ptr(Aq), M, K, _stream(stream)))
 
 
 def int2_int8_gemm(A, Aq, SA, B, SB, C, Other, Bias, M: int, N: int, K: int, postop: int = 0,
                    out_f32: bool = False, stream=None) -> None:
-    """int2_int8_gemm_mt(A, Aq, SA, B, SB, C, Other, Bias, M, N, K) of int2_int8_dpas.cl:316
-    in upfront mode (A is not read and may be None; the dtype comes from SB)."""
+    """int2_int8_gemm_mt(A, Aq, SA, B, SB, C, Other, Bias, M, N, K) of int2_int8_dpas.cl:316.
+    With Aq given: upfront quantization (QMODE 0; A is not read and may be None).  With
+    Aq=None: A's tiles are quantized while staged (QMODE 1), bit-identical q.  The dtype
+    comes from SB."""
     _check(lib().ternocl_int2_int8_gemm(_dtype_of(SB), _ptr(A), _ptr(Aq), _ptr(SA), _ptr(B), _ptr(SB),
                                         _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
                                         int(bool(out_f32)), _stream(stream)))

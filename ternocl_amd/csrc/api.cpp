@@ -45,9 +45,10 @@ ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, c
 ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (int2_int8.hip)
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st);
-ternocl_status int2_int8_gemm_run(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
-                                  const void *SB, void *C, const void *Other, const void *Bias, int M,
-                                  int N, int K, int postop, int out_f32, hipStream_t st);
+ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                  const uint32_t *B, const void *SB, void *C, const void *Other,
+                                  const void *Bias, int M, int N, int K, int postop, int out_f32,
+                                  hipStream_t st);
 ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (bitcos.hip)
 int bitcos_max_ls();
@@ -200,7 +201,7 @@ ternocl_status ternocl_quant_a(int dtype, const void *A, void *SA, int8_t *Aq, i
                                void *stream) {
     ternocl_status s = check_dtype(dtype);
     if (s != TERNOCL_OK) return s;
-    if (!A || !SA || !Aq) FAIL(TERNOCL_ERR_INVALID_ARG, "A, SA and Aq must be non-null");
+    if (!A || !SA) FAIL(TERNOCL_ERR_INVALID_ARG, "A and SA must be non-null");
     if (M < 1 || K < kGS || K % kGS) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need M >= 1 and K % 128 == 0");
     return quant_a_run(dtype, A, SA, Aq, M, K, (hipStream_t)stream);
 }
@@ -209,11 +210,10 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
                                       const uint32_t *B, const void *SB, void *C,
                                       const void *Other, const void *Bias, int M, int N, int K,
                                       int postop, int out_f32, void *stream) {
-    (void)A;  // the in-GEMM quantization mode is not built: Aq is required
-    if (!Aq) FAIL(TERNOCL_ERR_INVALID_ARG, "Aq must be non-null (quantize A with ternocl_quant_a)");
+    if (!Aq && !A) FAIL(TERNOCL_ERR_INVALID_ARG, "Aq (upfront quantization) or A (in-GEMM quantization) must be non-null");
     ternocl_status s = check_gemm_common(dtype, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
-    return int2_int8_gemm_run(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
+    return int2_int8_gemm_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
                               (hipStream_t)stream);
 }
 

@@ -1,7 +1,8 @@
 // int2_int8.hip -- the int2 x int8 prefill path on gfx950: the activation
 // quantization pre-kernel and the s8 x s2 GEMM, replacing quant_a and
 // int2_int8_{gemv,gemm_mt} of int2_via_int2_x_int8_dpas/int2_int8_dpas.cl
-// (:101-123, :210-281, :313-385) in its upfront-quantization mode (QMODE 0).
+// (:101-123, :210-281, :313-385) in both of its quantization modes (QMODE 0:
+// upfront, the GEMM reads int8 Aq; QMODE 1: the GEMM quantizes DT A tiles).
 //
 //   SA[g, m] = DT(127 / max(absmax_{k in g} |A[m, k]|, FLT_EPSILON))
 //   Aq[m, k] = sat_int8(rte(A[m, k] * SA[k/128, m]))
@@ -17,20 +18,24 @@
 //
 // The GEMM: a workgroup of 4 waves computes a 128 x 128 tile of C, each wave a
 // 64 x 64 quarter as 4 x 4 v_mfma_i32_16x16x64_i8 tiles; K advances one
-// 128-row scale group at a time (two MFMA k-steps of 64).
+// 128-row scale group at a time (two MFMA k-steps of 64).  Two workgroups share
+// a CU (183 VGPRs: two waves per SIMD).
 //   * B stays packed in HBM / L2: lane (c, q) of a wave loads, per k-step and
 //     16-column block, the word of k rows 16*(4*ks+q) .. +15 of its column and
 //     turns it into the 16 int8 of its MFMA B fragment with v_perm_b32 through
 //     the byte table {0x00, 0x01, 0xFE, 0xFF} indexed by the code:
 //     dword i = codes of rows i, i+4, i+8, i+12 (selector (w >> 2i) & 0x03030303);
-//   * Aq goes global -> registers -> LDS once per workgroup and group, each
-//     16-byte chunk 4x4 byte-transposed on the way so that its dword i holds
-//     rows i, i+4, i+8, i+12 too (the same k order as B: the int32 dot is exact
+//   * A goes global -> registers -> LDS once per workgroup and group, each
+//     16-byte chunk of int8 4x4 byte-transposed on the way (QMODE 1: quantized
+//     and packed straight into that order) so that its dword i holds rows i,
+//     i+4, i+8, i+12 too (the same k order as B: the int32 dot is exact
 //     whatever the order, as long as A and B agree);
 //   * 1 / SA[g, m] of the tile's 128 rows is computed once per group into LDS;
-//   * each group's dot products start from zero in int32 accumulators and are
-//     folded into fp32 accumulators with acc += float(dot) * (SB * inv), the
-//     order of the reference's host gold (int2_via_int2_x_int8_dpas/main.cpp:113-116).
+//   * each 16-row block's dot products start from zero in int32 accumulators
+//     and are folded into fp32 accumulators with acc += float(dot) * (SB * inv),
+//     the order of the reference's host gold (int2_via_int2_x_int8_dpas/main.cpp:113-116);
+//     the fold of block mb runs between the MFMAs of block mb + 1;
+//   * all loads are buffer loads with offsets computed once per kernel.
 #include "common.hpp"
 
 #include <cfloat>
@@ -81,7 +86,7 @@ k_quant_a(const uint16_t *__restrict__ A, uint16_t *__restrict__ SA, int8_t *__r
         const float r = p == p ? fminf(fmaxf(__builtin_rintf(p), -128.0f), 127.0f) : 0.0f;
         q[i >> 2] |= ((uint32_t)(int)r & 0xffu) << (8 * (i & 3));
     }
-    *(uint2 *)(Aq + (size_t)m * K + 8 * (size_t)c) = make_uint2(q[0], q[1]);
+    if (Aq) *(uint2 *)(Aq + (size_t)m * K + 8 * (size_t)c) = make_uint2(q[0], q[1]);
 }
 
 // ---- s8 x s2 GEMM ------------------------------------------------------------
@@ -130,9 +135,21 @@ template <int CB> struct QBSlab {
     uint32_t w[CB][2], sb[CB];
 };
 
-template <class TC, bool BF16>
+// In-GEMM quantization (the reference's QMODE 1, int2_int8_dpas.cl:61-68 and
+// quant8x32 :70-99): the int8 of a DT activation is the low byte of
+// fma(a, sa, 1.5 * 2^23), which rounds a * sa (exact in fp32) to the nearest
+// even integer; |a * sa| <= 127.06 by the construction of sa, so it equals
+// quant_a's saturating conversion for every finite input.
+template <bool BF16>
+__device__ __forceinline__ uint32_t q8_bits(uint32_t h, float sa) {
+    return __float_as_uint(__builtin_fmaf(dt2f<BF16>(h), sa, 12582912.0f));
+}
+
+// QA = false: A tiles come from Aq (int8, written by quant_a: the reference's
+// QMODE 0).  QA = true: from the DT activations A, quantized while staged.
+template <class TC, bool BF16, bool QA>
 __global__ void __launch_bounds__(TC::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
+k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
                  const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB,
                  void *__restrict__ C, const uint16_t *__restrict__ Other,
                  const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
@@ -164,23 +181,41 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
     // A staging: thread tid owns the 16-byte chunk (tid & 7) of rows
     // (tid >> 3) + (THREADS / 8) u; rows past mrows lie past the buffer's end
     // and load as 0.
+    // (QA: the chunk is 16 DT activations, 32 bytes.)
     constexpr int RSTEP = TC::THREADS / 8;
+    constexpr int ES = QA ? 2 : 1;  // bytes per staged A element in memory
     const int arow0 = tid >> 3, achunk = tid & 7;
-    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(Aq + (size_t)m0 * K, (uint32_t)((size_t)mrows * K));
+    const __amdgpu_buffer_rsrc_t rA =
+        buf_rsrc((const uint8_t *)Asrc + (size_t)m0 * K * ES, (uint32_t)((size_t)mrows * K * ES));
     uint32_t va[AP];
 #pragma unroll
-    for (int u = 0; u < AP; ++u) va[u] = (uint32_t)((arow0 + RSTEP * u) * K + 16 * achunk);
-    uint4 av[AP];
+    for (int u = 0; u < AP; ++u) va[u] = (uint32_t)(((arow0 + RSTEP * u) * K + 16 * achunk) * ES);
+    uint4 av[AP][ES];
     auto a_load = [&](int g) {
         const int gc = g < groups ? g : groups - 1;
 #pragma unroll
-        for (int u = 0; u < AP; ++u) {
-            const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u], gc * kGS, 0);
-            av[u] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
-        }
+        for (int u = 0; u < AP; ++u)
+#pragma unroll
+            for (int e = 0; e < ES; ++e) {
+                const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u] + 16 * e, gc * kGS * ES, 0);
+                av[u][e] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
+            }
     };
     // 1 / SA of the tile's rows (thread tid < BM: row tid)
     const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - m0) * 2));
+    // QA: SA of the rows this thread stages (row clamped below mrows)
+    uint32_t vsq[QA ? AP : 1], sq_raw[QA ? AP : 1];
+    if constexpr (QA) {
+#pragma unroll
+        for (int u = 0; u < AP; ++u) vsq[u] = (uint32_t)min(arow0 + RSTEP * u, mrows - 1) * 2;
+    }
+    auto sq_load = [&](int g) {
+        if constexpr (QA) {
+            const int gc = g < groups ? g : groups - 1;
+#pragma unroll
+            for (int u = 0; u < AP; ++u) sq_raw[u] = __builtin_amdgcn_raw_buffer_load_b16(rSA, vsq[u], gc * lda * 2, 0);
+        }
+    };
     // threads t and t + BM (when THREADS = 2 BM) load and write the same row's
     // value, so the store below needs no branch
     const int srow = tid & (BM - 1);
@@ -193,9 +228,27 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
     auto a_store = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < AP; ++u) {
-            const uint32_t d[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
             uint32_t o[4];
-            transpose4x4(d, o);
+            if constexpr (QA) {
+                // quantize the 16 activations; dword i gathers the int8 of
+                // k = i, i + 4, i + 8, i + 12 (the transposed order)
+                const float sa = dt2f<BF16>(sq_raw[u]);
+                const uint32_t h[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
+                                       av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
+                uint32_t qb[16];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    qb[2 * j] = q8_bits<BF16>(h[j] & 0xffffu, sa);
+                    qb[2 * j + 1] = q8_bits<BF16>(h[j] >> 16, sa);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[i] = __builtin_amdgcn_perm(qb[4 + i], qb[i], 0x0c0c0400u) |
+                           __builtin_amdgcn_perm(qb[12 + i], qb[8 + i], 0x04000c0cu);
+            } else {
+                const uint32_t d[4] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w};
+                transpose4x4(d, o);
+            }
             *(uint4 *)(&lds_a[buf][(arow0 + RSTEP * u) * QA_PITCH + 16 * achunk]) = make_uint4(o[0], o[1], o[2], o[3]);
         }
         const float sa = dt2f<BF16>(sa_raw);
@@ -236,6 +289,7 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
         const int buf = g & 1;
         a_load(g + 1);
         sa_load(g + 1);
+        sq_load(g + 1);
         b_load(nxt);
         i32x4_t bf[CB][2];
         float sbf[CB];
@@ -294,6 +348,7 @@ k_int2_int8_gemm(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
     QBSlab<CB> cur;
     a_load(0);
     sa_load(0);
+    sq_load(0);
     b_load(cur);
     a_store(0);
     for (int g = 0; g < groups; ++g) {
@@ -351,32 +406,37 @@ ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M
     return check_launch();
 }
 
-template <class TC>
-static hipError_t int8_gemm_launch(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
+template <class TC, bool QA>
+static hipError_t int8_gemm_launch(int dtype, const void *Asrc, const void *SA, const uint32_t *B,
                                    const void *SB, void *C, const void *Other, const void *Bias, int M,
                                    int N, int K, int postop, int out_f32, hipStream_t st) {
     const int mt = (M + TC::BM - 1) / TC::BM, nt = (N + TC::BN - 1) / TC::BN;
     const dim3 grid(mt * nt), block(TC::THREADS);
     if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL((k_int2_int8_gemm<TC, true>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
+        hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, QA>), grid, block, 0, st, Asrc, (const uint16_t *)SA, B,
                            (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
     else
-        hipLaunchKernelGGL((k_int2_int8_gemm<TC, false>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
+        hipLaunchKernelGGL((k_int2_int8_gemm<TC, false, QA>), grid, block, 0, st, Asrc, (const uint16_t *)SA, B,
                            (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
     return hipGetLastError();
 }
 
-ternocl_status int2_int8_gemm_run(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
-                                  const void *SB, void *C, const void *Other, const void *Bias, int M,
-                                  int N, int K, int postop, int out_f32, hipStream_t st) {
-    // 128 x 128 tiles, 2 x 2 waves of 64 x 64: 213 VGPRs, two waves per SIMD
-    // (a 128-row wave tile's 128 fp32 accumulators do not fit beside the rest)
+ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                  const uint32_t *B, const void *SB, void *C, const void *Other,
+                                  const void *Bias, int M, int N, int K, int postop, int out_f32,
+                                  hipStream_t st) {
+    // 128 x 128 tiles, 2 x 2 waves of 64 x 64: two waves per SIMD (a 128-row
+    // wave tile's 128 fp32 accumulators do not fit beside the rest)
     typedef QTile<4, 4, 2, 2> Tile;
-    if ((size_t)M * K >= (1u << 31) || (size_t)(K / 16) * N * 4 >= (1u << 31)) {
-        set_error("int2_int8_gemm: M*K and K*N/4 must be below 2^31 bytes");
+    const size_t es = Aq ? 1 : 2;
+    if ((size_t)M * K * es >= (1u << 31) || (size_t)(K / 16) * N * 4 >= (1u << 31)) {
+        set_error("int2_int8_gemm: the A operand and B must each be below 2^31 bytes");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
-    return launch_status(int8_gemm_launch<Tile>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st));
+    const hipError_t e = Aq
+        ? int8_gemm_launch<Tile, false>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+        : int8_gemm_launch<Tile, true>(dtype, A, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return launch_status(e);
 }
 
 ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st) {

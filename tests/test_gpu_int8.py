@@ -185,10 +185,50 @@ def test_s8_decode_bit_exact(dev):
     assert np.array_equal(got, want)
 
 
-def test_int8_gemm_requires_aq(dev):
+def test_int8_gemm_requires_a_or_aq(dev):
     import torch
     import ternocl_amd as T
     with pytest.raises(T.TernoclError):
         T.int2_int8_gemm(None, None, torch.zeros(32, device="cuda"), torch.zeros(16, dtype=torch.int32, device="cuda"),
                          torch.zeros(16, dtype=torch.float16, device="cuda"),
                          torch.zeros(16, dtype=torch.float16, device="cuda"), None, None, 1, 16, 128)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_quant_a_scales_only(dev, orc, bf16):
+    """Aq = None writes SA alone (the reference's quant_a without WRITE_Q), bit-exact."""
+    import torch
+    import ternocl_amd as T
+    M, K = 45, 1024
+    A = synth.activations(synth.rng(8), (M, K), bf16)
+    dA = dev_dt(A, bf16)
+    dSA = torch.zeros((K // 128, T.ldsa(M)), dtype=dA.dtype, device="cuda")
+    T.quant_a(dA, dSA, None, M, K)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(dSA)[:, :M], orc.scale_a(A, M, K, bf16)[:, :M])
+
+
+IN_GEMM_SHAPES = [(1, 256, 16), (100, 2048, 1040), (129, 640, 2064), (1024, 4096, 1024)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", IN_GEMM_SHAPES)
+def test_int8_gemm_in_gemm_quantization(dev, orc, M, K, N, bf16):
+    """QMODE 1 (A quantized while staged) gives the upfront mode's C bit for bit, and so
+    the oracle's within tolerance; the reference driver's A ~ U[-5, 5] and every code."""
+    import torch
+    import ternocl_amd as T
+    print(f"int8 in-GEMM quantization M={M} K={K} N={N} bf16={bf16}", flush=True)
+    A, B, SB, other, bias_f = _int8_case(4000 + M + N, M, K, N, bf16, ref_dist=True, all_codes=True)
+    dA, dSA, dAq = _quant(T, torch, A, M, K, bf16)
+    dB, dSB, dO = dev_raw(B), dev_dt(SB, bf16), dev_dt(other, bf16)
+    dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+    up = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+    ig = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+    T.int2_int8_gemm(None, dAq, dSA, dB, dSB, up, dO, dBias, M, N, K, 5, False)
+    T.int2_int8_gemm(dA, None, dSA, dB, dSB, ig, dO, dBias, M, N, K, 5, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(up), host_u16(ig))
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, 5, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(ig), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
