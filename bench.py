@@ -380,8 +380,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the M = 2, 4, 8 sweep and the VALU engine")
     ap.add_argument("--only-headline", action="store_true", help="skip the prefill, C1, C4 and C5 workloads")
     ap.add_argument("--probe", type=int, default=0, metavar="N",
-                    help="counter-collection mode for rocprofv3 --pmc: N eager launches per shape plus "
-                         "a 64 MiB device copy (the calibration kernel of known size); prints one line")
+                    help="counter-collection mode for rocprofv3 --pmc: N eager launches per GEMV shape, "
+                         "a 64 MiB device copy (the calibration kernel of known size) and N calls of the "
+                         "int8 prefill (quant_a + s8 x s2 GEMM, M=1024 K=4096 N=14336); prints one line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -405,6 +406,17 @@ def main():
                 sb.launch()
         for _ in range(4):  # an elementwise kernel reading 64 MiB and writing 64 MiB: the
             torch.add(src, 1, out=dst)  # calibration of the FETCH_SIZE / WRITE_SIZE counters
+        del src, dst
+        M, K, N = 1024, 4096, 14336  # the prefill workload, one weight set (counters, not timing)
+        g = synth.rng(33)
+        A, B, SB = synth.activations(g, (M, K), False), synth.int2_weights(g, K, N), synth.scales(g, K, N, False)
+        dA, dB, dSB = dev16(torch, A, False), dev32(torch, B), dev16(torch, SB, False)
+        dSA = torch.empty((K // 128, T.ldsa(M)), dtype=torch.float16, device="cuda")
+        dAq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        dC = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        for _ in range(args.probe):
+            T.quant_a(dA, dSA, dAq, M, K)
+            T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, None, None, M, N, K)
         torch.cuda.synchronize()
         print(json.dumps({"probe": args.probe, "bytes_per_launch": {f"K{sb.K}_N{sb.N}": sb.bytes() for sb in sbs},
                           "copy_bytes": 64 << 20}), flush=True)
