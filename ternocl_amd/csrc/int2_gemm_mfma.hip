@@ -34,6 +34,7 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf168_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;           // K per LDS stage
 constexpr int A_PITCH = BK + 8;  // DT elements per LDS row (16 bytes of padding)
@@ -113,6 +114,10 @@ struct ARows {
     __device__ __forceinline__ const uint16_t *row(int r, int K) const {
         return A + (size_t)(idx ? idx[r] / div : r) * K;
     }
+    // byte offset of row r from A (the A operand stays below 2^31 bytes)
+    __device__ __forceinline__ uint32_t rowoff(int r, int K) const {
+        return (uint32_t)(idx ? idx[r] / div : r) * (uint32_t)K * 2u;
+    }
 };
 
 template <int NMB, int NCB> struct TileCfg {
@@ -124,43 +129,48 @@ template <int NMB, int NCB> struct TileCfg {
 // One BM x BN output tile of rows [0, mrows) of ar (mrows <= BM) and columns
 // [n0, n0 + BN) (columns >= N masked); C row r is crow0 + r.
 template <int NMB, int NCB, bool BF16>
-__device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint32_t *__restrict__ B,
-                                          const uint16_t *__restrict__ S, void *__restrict__ C,
-                                          const uint16_t *__restrict__ Other, const void *__restrict__ Bias,
-                                          int crow0, int N, int K, int n0, int postop, int out_f32,
-                                          uint16_t *lds) {
+__device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
+                                          const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
+                                          void *__restrict__ C, const uint16_t *__restrict__ Other,
+                                          const void *__restrict__ Bias, int crow0, int N, int K, int n0,
+                                          int postop, int out_f32, uint16_t *lds) {
     using Cfg = TileCfg<NMB, NCB>;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c16 = lane & 15, q = lane >> 4, h = q & 1;
     const int wm = (wave >> 1) * 16 * NMB, wn = (wave & 1) * 16 * NCB;
     const int stages = K / BK;
 
-    // A staging: chunk id = tid + 256u -> row id >> 2, 16-element chunk id & 3
-    const uint16_t *arow[Cfg::ACH];
+    // All operand loads are buffer loads with per-lane offsets set up once and
+    // issued unconditionally (a load under a branch is waited for at the
+    // branch's end); the loads issued past the last stage read in-range memory
+    // (A: stage clamped) or return 0 (B, S: past the buffer's end).
+    //
+    // A staging: chunk id = tid + 256u -> row id >> 2, 16-element chunk id & 3.
+    // Rows past mrows re-read row mrows - 1: their outputs are never stored.
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(ar.A, a_bytes);
+    uint32_t va[Cfg::ACH];
 #pragma unroll
     for (int u = 0; u < Cfg::ACH; ++u) {
         const int id = tid + 256 * u, r = id >> 2;
-        arow[u] = ar.row(r < mrows ? r : mrows - 1, K) + 16 * (id & 3);
+        va[u] = ar.rowoff(r < mrows ? r : mrows - 1, K) + 32u * (id & 3);
     }
     uint4 av[Cfg::ACH][2];
     auto a_load = [&](int st) {
+        const int sc = (st < stages ? st : stages - 1) * BK * 2;  // bytes, uniform
 #pragma unroll
-        for (int u = 0; u < Cfg::ACH; ++u) {
-            const uint4 *p = (const uint4 *)(arow[u] + st * BK);
-            av[u][0] = p[0];
-            av[u][1] = p[1];
-        }
+        for (int u = 0; u < Cfg::ACH; ++u)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u] + 16 * e, sc, 0);
+                av[u][e] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
+            }
     };
-    // Rows past mrows are zeroed here, not at the load: touching the loaded
-    // registers right after the loads would make the wave wait for them.
     auto a_store = [&](uint16_t *buf) {
 #pragma unroll
         for (int u = 0; u < Cfg::ACH; ++u) {
             const int id = tid + 256 * u;
-            const bool live = (id >> 2) < mrows;
-            const uint4 a0 = live ? av[u][0] : make_uint4(0, 0, 0, 0);
-            const uint4 a1 = live ? av[u][1] : make_uint4(0, 0, 0, 0);
-            const uint32_t v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const uint32_t v[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
+                                   av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
             uint32_t o[8];
             chunk_interleave(v, o);
             uint4 *d = (uint4 *)(buf + (size_t)(id >> 2) * A_PITCH + 16 * (id & 3));
@@ -170,28 +180,30 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint
     };
 
     // B words of this wave for stage st: block cb, k-step ks -> word
-    // kp = 4 st + 2 ks + q / 2 of column n0 + wn + 16 cb + c16, half q % 2
-    const uint32_t *bcol[NCB];
-    const uint16_t *scol[NCB];
-#pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-        const int n = n0 + wn + 16 * cb + c16;
-        const int nc = n < N ? n : N - 1;
-        bcol[cb] = B + (size_t)(q >> 1) * N + nc;
-        scol[cb] = S + nc;
-    }
+    // kp = 4 st + 2 ks + q / 2 of column n0 + wn + 16 cb + c16, half q % 2.
+    // vb[ks] advances one stage per load; a 16-column block past N (when
+    // N % BN != 0) reads the next row's words -- in range, feeding outputs
+    // that are not stored -- or, past the last row, 0.
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
+    uint32_t vb[2];
+    vb[0] = (uint32_t)(((q >> 1) * N + wn + c16) * 4);
+    vb[1] = vb[0] + (uint32_t)(8 * N);
+    const uint32_t vs0 = (uint32_t)((wn + c16) * 2);
     uint32_t bw[NCB][2], sraw[NCB];
-    auto b_load = [&](int st) {
-        const size_t r0 = (size_t)st * 4 * N;  // uniform
+    auto b_load = [&]() {
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) bw[cb][ks] = bcol[cb][r0 + (size_t)(2 * ks) * N];
+            for (int ks = 0; ks < 2; ++ks)
+                bw[cb][ks] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb[ks] + 64 * cb, 0, 0);
+        vb[0] += (uint32_t)(16 * N);
+        vb[1] += (uint32_t)(16 * N);
     };
-    auto s_load = [&](int g) {
-        const size_t r0 = (size_t)g * N;
+    auto s_load = [&](int g) {  // the scales of group g (past the last: 0)
+        const uint32_t v = vs0 + (uint32_t)(g * 2 * N);
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) sraw[cb] = scol[cb][r0];
+        for (int cb = 0; cb < NCB; ++cb) sraw[cb] = __builtin_amdgcn_raw_buffer_load_b16(rS, v + 32 * cb, 0, 0);
     };
 
     f32x4_t acc[NMB][NCB];
@@ -202,7 +214,7 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint
 
     ScaleOp<BF16> sop[NCB];
     a_load(0);
-    b_load(0);
+    b_load();
     s_load(0);
     a_store(lds);
     for (int st = 0; st < stages; ++st) {
@@ -214,16 +226,15 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint
             bwc[cb][0] = bw[cb][0];
             bwc[cb][1] = bw[cb][1];
         }
-        if ((st & 1) == 0) {  // a new 128-row scale group
+        if ((st & 1) == 0) {  // a new 128-row scale group (uniform; no loads inside)
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) sop[cb].set(sraw[cb]);
         }
-        const bool more = st + 1 < stages;
-        if (more) {  // next stage's loads in flight during this stage's MFMAs
-            a_load(st + 1);
-            b_load(st + 1);
-            if (st & 1) s_load((st + 1) >> 1);
-        }
+        // next stage's loads in flight during this stage's MFMAs; the scales of
+        // the group after this one are loaded on the group's second stage
+        a_load(st + 1);
+        b_load();
+        s_load((st >> 1) + 1);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             uint32_t af[NMB][4];
@@ -241,7 +252,7 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, int mrows, const uint
                 for (int mb = 0; mb < NMB; ++mb) acc[mb][cb] = mfma16<BF16>(af[mb], bf, acc[mb][cb]);
             }
         }
-        if (more) a_store(lds + (size_t)((st + 1) & 1) * Cfg::BM * A_PITCH);
+        a_store(lds + (size_t)((st + 1) & 1) * Cfg::BM * A_PITCH);  // after the last stage: never read
     }
 
     // Epilogue through LDS, one 16-column block at a time: lane (c16, q) holds
@@ -286,8 +297,8 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     xcd_tile_of(blockIdx.x, mt, nt, tm, tn);
     const ARows ar{A + (size_t)tm * Cfg::BM * K, nullptr, 1};
     const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
-    gemm_tile<NMB, NCB, BF16>(ar, mrows, B, S, C, Other, Bias, tm * Cfg::BM, N, K, tn * Cfg::BN, postop,
-                              out_f32, lds);
+    gemm_tile<NMB, NCB, BF16>(ar, (uint32_t)((size_t)mrows * K * 2), mrows, B, S, C, Other, Bias, tm * Cfg::BM,
+                              N, K, tn * Cfg::BN, postop, out_f32, lds);
 }
 
 // Grouped GEMM of the MoE prefill (int2_moe/int2_moe_prefill.cl:72-141): the
@@ -304,7 +315,7 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
                 const int *__restrict__ perm, int topk, const uint32_t *__restrict__ B_all,
                 const uint16_t *__restrict__ S_all, void *__restrict__ C_all,
                 const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
-                int ntn) {
+                int ntn, int arows) {
     using Cfg = TileCfg<kMoeNMB, NCB>;
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
@@ -318,10 +329,14 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
     const int e = lo, row0 = meta[e];
     const int m0 = (tile - meta[E + 1 + e]) * Cfg::BM;
     const int mrows = min(Cfg::BM, meta[e + 1] - row0 - m0);
+    // A rows: token rows of A_all through perm (arows rows in all), or the
+    // sorted rows themselves
     const ARows ar = perm ? ARows{A_all, perm + row0 + m0, topk}
                           : ARows{A_all + (size_t)(row0 + m0) * K, nullptr, 1};
-    gemm_tile<kMoeNMB, NCB, BF16>(ar, mrows, B_all + (size_t)e * (K / 16) * N, S_all + (size_t)e * (K / kGS) * N,
-                                  C_all, Other_all, nullptr, row0 + m0, N, K, tn * Cfg::BN, postop, out_f32, lds);
+    const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : mrows) * K * 2);
+    gemm_tile<kMoeNMB, NCB, BF16>(ar, a_bytes, mrows, B_all + (size_t)e * (K / 16) * N,
+                                  S_all + (size_t)e * (K / kGS) * N, C_all, Other_all, nullptr, row0 + m0, N, K,
+                                  tn * Cfg::BN, postop, out_f32, lds);
 }
 
 // Test hook: the B fragments the GEMM builds at unit scale (DT 1.0),
@@ -395,7 +410,7 @@ void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, c
     const int max_tiles = (G + Cfg::BM - 1) / Cfg::BM + E;  // each expert's ragged tail adds at most one tile
     hipLaunchKernelGGL((k_int2_moe_gemm<NCB, BF16>), dim3((unsigned)(max_tiles * ntn)), dim3(256), 0, st, meta,
                        (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
-                       (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn);
+                       (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn, perm ? G / topk : G);
 }
 
 }  // namespace
