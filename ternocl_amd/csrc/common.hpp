@@ -141,6 +141,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
+// Workgroup -> (m tile, n tile) of a GEMM grid of mt x nt tiles, for a
+// launch of 8 * ceil(mt * nt / 8) workgroups.  Workgroups are dealt to the 8
+// XCDs round-robin (id % 8 runs on XCD id % 8); XCD x takes the contiguous
+// range [x * per, (x + 1) * per) of the tiles in M-major order, so the
+// workgroups of one XCD share the same few A row blocks (the larger operand
+// per tile: DT or int8 rows against 2-bit weight columns) in that XCD's L2,
+// and each row block is fetched into about one L2 instead of all eight.
+// Returns false for the padding workgroups past the last tile.
+__device__ __forceinline__ bool xcd_tile_ashare(int id, int mt, int nt, int &tm, int &tn) {
+    const int tiles = mt * nt, per = (tiles + 7) / 8;
+    const int t = (id & 7) * per + (id >> 3);
+    if (t >= tiles) return false;
+    tm = t / nt;
+    tn = t - tm * nt;
+    return true;
+}
+__host__ __device__ inline int xcd_ashare_grid(int mt, int nt) { return 8 * ((mt * nt + 7) / 8); }
+
 // Workgroup -> (m tile, n tile) of a GEMM grid of mt x nt tiles.  Workgroups
 // are dealt to the 8 XCDs round-robin (x, x+8, x+16, ... run on XCD x); those
 // take all M tiles of column strip x, then of strip x+8, ... (when the strip

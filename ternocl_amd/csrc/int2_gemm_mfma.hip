@@ -294,7 +294,7 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
     int tm, tn;
-    xcd_tile_of(blockIdx.x, mt, nt, tm, tn);
+    if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
     const ARows ar{A + (size_t)tm * Cfg::BM * K, nullptr, 1};
     const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
     gemm_tile<NMB, NCB, BF16>(ar, (uint32_t)((size_t)mrows * K * 2), mrows, B, S, C, Other, Bias, tm * Cfg::BM,
@@ -387,7 +387,7 @@ void gemm_launch(const void *A, const uint32_t *B, const void *S, void *C, const
                  int M, int N, int K, int postop, int out_f32, hipStream_t st) {
     using Cfg = TileCfg<NMB, NCB>;
     const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
-    hipLaunchKernelGGL((k_int2_gemm<NMB, NCB, BF16>), dim3(mt * nt), dim3(256), 0, st, (const uint16_t *)A, B,
+    hipLaunchKernelGGL((k_int2_gemm<NMB, NCB, BF16>), dim3(xcd_ashare_grid(mt, nt)), dim3(256), 0, st, (const uint16_t *)A, B,
                        (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
 }
 

@@ -162,7 +162,7 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
 
     const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     int tm, tn;
-    xcd_tile_of(blockIdx.x, mt, nt, tm, tn);
+    if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
     const int m0 = tm * BM, n0 = tn * BN;
     const int mrows = min(BM, M - m0);
     const int groups = K / kGS;
@@ -411,7 +411,7 @@ static hipError_t int8_gemm_launch(int dtype, const void *Asrc, const void *SA, 
                                    const void *SB, void *C, const void *Other, const void *Bias, int M,
                                    int N, int K, int postop, int out_f32, hipStream_t st) {
     const int mt = (M + TC::BM - 1) / TC::BM, nt = (N + TC::BN - 1) / TC::BN;
-    const dim3 grid(mt * nt), block(TC::THREADS);
+    const dim3 grid(xcd_ashare_grid(mt, nt)), block(TC::THREADS);
     if (dtype == TERNOCL_BF16)
         hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, QA>), grid, block, 0, st, Asrc, (const uint16_t *)SA, B,
                            (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
