@@ -120,24 +120,34 @@ struct ARows {
     }
 };
 
-template <int NMB, int NCB> struct TileCfg {
-    static constexpr int BM = 32 * NMB, BN = 32 * NCB;
-    static constexpr int ACH = BM / 64;  // 16-element A chunks per thread per stage
-    static constexpr size_t lds_elems = 2 * (size_t)BM * A_PITCH;
+constexpr int kEpPitch = 20;  // epilogue floats per row: 16 + 4 (16-byte aligned rows)
+
+// Tile shape: WVM x WVN waves, each owning NMB x NCB blocks of 16 x 16 outputs.
+template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
+    static constexpr int NMB = NMB_, NCB = NCB_, WVM = WVM_, WVN = WVN_;
+    static constexpr int THREADS = 64 * WVM * WVN;
+    static constexpr int BM = 16 * NMB * WVM, BN = 16 * NCB * WVN;
+    static constexpr int ACH = BM * 4 / THREADS;  // 16-element A chunks per thread per stage
+    static_assert(BM * 4 % THREADS == 0, "A chunks must divide evenly");
+    // LDS (DT elements): two A stages while K runs, then the epilogue's
+    // per-wave [16 NMB][kEpPitch] fp32 blocks
+    static constexpr size_t stage_elems = 2 * (size_t)BM * A_PITCH;
+    static constexpr size_t epi_elems = (size_t)(THREADS / 64) * 16 * NMB * kEpPitch * 2;
+    static constexpr size_t lds_elems = stage_elems > epi_elems ? stage_elems : epi_elems;
 };
 
 // One BM x BN output tile of rows [0, mrows) of ar (mrows <= BM) and columns
 // [n0, n0 + BN) (columns >= N masked); C row r is crow0 + r.
-template <int NMB, int NCB, bool BF16>
+template <class Cfg, bool BF16>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
                                           const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                           void *__restrict__ C, const uint16_t *__restrict__ Other,
                                           const void *__restrict__ Bias, int crow0, int N, int K, int n0,
                                           int postop, int out_f32, uint16_t *lds) {
-    using Cfg = TileCfg<NMB, NCB>;
+    constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c16 = lane & 15, q = lane >> 4, h = q & 1;
-    const int wm = (wave >> 1) * 16 * NMB, wn = (wave & 1) * 16 * NCB;
+    const int wm = (wave / Cfg::WVN) * 16 * NMB, wn = (wave % Cfg::WVN) * 16 * NCB;
     const int stages = K / BK;
 
     // All operand loads are buffer loads with per-lane offsets set up once and
@@ -145,13 +155,13 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // branch's end); the loads issued past the last stage read in-range memory
     // (A: stage clamped) or return 0 (B, S: past the buffer's end).
     //
-    // A staging: chunk id = tid + 256u -> row id >> 2, 16-element chunk id & 3.
+    // A staging: chunk id = tid + THREADS u -> row id >> 2, 16-element chunk id & 3.
     // Rows past mrows re-read row mrows - 1: their outputs are never stored.
     const __amdgpu_buffer_rsrc_t rA = buf_rsrc(ar.A, a_bytes);
     uint32_t va[Cfg::ACH];
 #pragma unroll
     for (int u = 0; u < Cfg::ACH; ++u) {
-        const int id = tid + 256 * u, r = id >> 2;
+        const int id = tid + TH * u, r = id >> 2;
         va[u] = ar.rowoff(r < mrows ? r : mrows - 1, K) + 32u * (id & 3);
     }
     uint4 av[Cfg::ACH][2];
@@ -168,7 +178,7 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     auto a_store = [&](uint16_t *buf) {
 #pragma unroll
         for (int u = 0; u < Cfg::ACH; ++u) {
-            const int id = tid + 256 * u;
+            const int id = tid + TH * u;
             const uint32_t v[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
                                    av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
             uint32_t o[8];
@@ -261,7 +271,6 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // row for epi_store4.  (Reading the accumulators only in fully unrolled
     // loops also keeps the array in registers.)
     const float fix = BF16 ? 1.0f : 0.5f;  // fp16 fragments carry 2x the weight
-    constexpr int kEpPitch = 20;           // floats per row: 16 + 4 (16-byte aligned rows)
     float *ct = (float *)lds + (size_t)wave * 16 * NMB * kEpPitch;
     __syncthreads();  // the A buffers are free
 #pragma unroll
@@ -285,19 +294,18 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     }
 }
 
-template <int NMB, int NCB, bool BF16>
-__global__ void __launch_bounds__(256)
+template <class Cfg, bool BF16>
+__global__ void __launch_bounds__(Cfg::THREADS)
 k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
             const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
-    using Cfg = TileCfg<NMB, NCB>;
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
     int tm, tn;
     if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
     const ARows ar{A + (size_t)tm * Cfg::BM * K, nullptr, 1};
     const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
-    gemm_tile<NMB, NCB, BF16>(ar, (uint32_t)((size_t)mrows * K * 2), mrows, B, S, C, Other, Bias, tm * Cfg::BM,
+    gemm_tile<Cfg, BF16>(ar, (uint32_t)((size_t)mrows * K * 2), mrows, B, S, C, Other, Bias, tm * Cfg::BM,
                               N, K, tn * Cfg::BN, postop, out_f32, lds);
 }
 
@@ -317,6 +325,7 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
                 const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
                 int ntn, int arows) {
     using Cfg = TileCfg<kMoeNMB, NCB>;
+    static_assert(Cfg::THREADS == 256, "launch bounds");
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
     if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
@@ -334,7 +343,7 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
     const ARows ar = perm ? ARows{A_all, perm + row0 + m0, topk}
                           : ARows{A_all + (size_t)(row0 + m0) * K, nullptr, 1};
     const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : mrows) * K * 2);
-    gemm_tile<kMoeNMB, NCB, BF16>(ar, a_bytes, mrows, B_all + (size_t)e * (K / 16) * N,
+    gemm_tile<Cfg, BF16>(ar, a_bytes, mrows, B_all + (size_t)e * (K / 16) * N,
                                   S_all + (size_t)e * (K / kGS) * N, C_all, Other_all, nullptr, row0 + m0, N, K,
                                   tn * Cfg::BN, postop, out_f32, lds);
 }
@@ -358,22 +367,25 @@ __global__ void k_int2_gemm_decode(const uint32_t *__restrict__ B, uint32_t *__r
 // ---- host side: tile choice ----------------------------------------------------
 
 struct GemmPlan {
-    int nmb, ncb;
+    int nmb, ncb, wvm, wvn;
 };
 
 // Fewest idle MFMA slots over the machine (ragged tiles and the last partial
 // round of workgroups over the 256 CUs), weighted by the relative MAC rate of
-// each tile size (larger tiles decode fewer B words and read less A per MAC).
+// each tile shape (larger tiles decode fewer B words and read less A per MAC;
+// eight-wave tiles keep two waves per SIMD, four-wave 256 x 256 tiles one).
 GemmPlan gemm_plan(int M, int N) {
-    static const GemmPlan cands[] = {{8, 8}, {8, 4}, {4, 8}, {4, 4}};
-    static const double eff[] = {1.0, 0.88, 0.88, 0.75};
-    GemmPlan best = cands[3];
+    static const GemmPlan cands[] = {{8, 4, 2, 4}, {8, 8, 2, 2}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
+    static const double eff[] = {1.0, 0.9, 0.75, 0.7, 0.88};
+    static const int per_cu[] = {1, 1, 1, 1, 2};  // resident workgroups per CU
+    GemmPlan best = cands[4];
     double best_t = 1e300;
-    for (int c = 0; c < 4; ++c) {
-        const int BM = 32 * cands[c].nmb, BN = 32 * cands[c].ncb;
+    for (int c = 0; c < 5; ++c) {
+        const int BM = 16 * cands[c].nmb * cands[c].wvm, BN = 16 * cands[c].ncb * cands[c].wvn;
         const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-        const long rounds = (tiles + 255) / 256;
-        const double t = (double)rounds * BM * BN / eff[c];
+        const long slots = 256L * per_cu[c];
+        const long rounds = (tiles + slots - 1) / slots;
+        const double t = (double)rounds * BM * BN * per_cu[c] / eff[c];
         if (t < best_t * 0.999) {
             best_t = t;
             best = cands[c];
@@ -382,23 +394,24 @@ GemmPlan gemm_plan(int M, int N) {
     return best;
 }
 
-template <int NMB, int NCB, bool BF16>
+template <class Cfg, bool BF16>
 void gemm_launch(const void *A, const uint32_t *B, const void *S, void *C, const void *Other, const void *Bias,
                  int M, int N, int K, int postop, int out_f32, hipStream_t st) {
-    using Cfg = TileCfg<NMB, NCB>;
     const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
-    hipLaunchKernelGGL((k_int2_gemm<NMB, NCB, BF16>), dim3(xcd_ashare_grid(mt, nt)), dim3(256), 0, st, (const uint16_t *)A, B,
-                       (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32);
+    hipLaunchKernelGGL((k_int2_gemm<Cfg, BF16>), dim3(xcd_ashare_grid(mt, nt)), dim3(Cfg::THREADS), 0, st,
+                       (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K,
+                       postop, out_f32);
 }
 
 template <bool BF16>
 void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const void *S, void *C,
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
-    if (p.nmb == 8 && p.ncb == 8) gemm_launch<8, 8, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.nmb == 8) gemm_launch<8, 4, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.ncb == 8) gemm_launch<4, 8, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else gemm_launch<4, 4, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (p.wvn == 4) gemm_launch<TileCfg<8, 4, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.nmb == 8 && p.ncb == 8) gemm_launch<TileCfg<8, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.nmb == 8) gemm_launch<TileCfg<8, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.ncb == 8) gemm_launch<TileCfg<4, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
 template <int NCB, bool BF16>
