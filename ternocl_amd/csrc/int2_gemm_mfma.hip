@@ -38,7 +38,7 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;           // K per LDS stage
 constexpr int A_PITCH = BK + 8;  // DT elements per LDS row (16 bytes of padding)
-constexpr int kMoeNMB = 4;       // MoE tiles: 128 rows (experts hold a few hundred rows each)
+constexpr int kMoeTileRows = 128;  // MoE row tiles (experts hold a few hundred rows each)
 
 template <bool BF16>
 __device__ __forceinline__ f32x4_t mfma16(const uint32_t a[4], const uint32_t b[4], f32x4_t c) {
@@ -317,15 +317,14 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // gather fused into the A-tile load), else from A_all[p].  Expert e's weights:
 // B_all + e*(K/16)*N, S_all + e*(K/128)*N; C and Other are indexed by the
 // sorted row p.
-template <int NCB, bool BF16>
-__global__ void __launch_bounds__(256)
+template <class Cfg, bool BF16>
+__global__ void __launch_bounds__(Cfg::THREADS)
 k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all,
                 const int *__restrict__ perm, int topk, const uint32_t *__restrict__ B_all,
                 const uint16_t *__restrict__ S_all, void *__restrict__ C_all,
                 const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
                 int ntn, int arows) {
-    using Cfg = TileCfg<kMoeNMB, NCB>;
-    static_assert(Cfg::THREADS == 256, "launch bounds");
+    static_assert(Cfg::BM == kMoeTileRows, "MoE row tiles are kMoeTileRows rows");
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
     if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
@@ -414,32 +413,36 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
     else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
-template <int NCB, bool BF16>
+template <class Cfg, bool BF16>
 void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, const uint32_t *B_all,
                 const void *S_all, void *C_all, const void *Other_all, int E, int G, int N, int K, int postop,
                 int out_f32, hipStream_t st) {
-    using Cfg = TileCfg<kMoeNMB, NCB>;
     const int ntn = (N + Cfg::BN - 1) / Cfg::BN;
     const int max_tiles = (G + Cfg::BM - 1) / Cfg::BM + E;  // each expert's ragged tail adds at most one tile
-    hipLaunchKernelGGL((k_int2_moe_gemm<NCB, BF16>), dim3((unsigned)(max_tiles * ntn)), dim3(256), 0, st, meta,
+    hipLaunchKernelGGL((k_int2_moe_gemm<Cfg, BF16>), dim3((unsigned)(max_tiles * ntn)), dim3(Cfg::THREADS), 0, st, meta,
                        (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
                        (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn, perm ? G / topk : G);
 }
 
 }  // namespace
 
-int moe_tile_rows() { return TileCfg<kMoeNMB, 4>::BM; }
+int moe_tile_rows() { return kMoeTileRows; }
 
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
                             int E, int G, int N, int K, int postop, int out_f32, hipStream_t st) {
-    const bool wide = N % 256 == 0;  // 256-column tiles when they divide N, else 128
+    // 128-row tiles of eight waves: 256 columns (waves of 64 x 64) unless the
+    // ragged last column tile would idle more than 1/10 of the MFMA work, then
+    // 128 (waves of 64 x 32)
+    typedef TileCfg<4, 4, 2, 4> Wide;
+    typedef TileCfg<4, 2, 2, 4> Narrow;
+    const bool wide = (long)((N + 255) / 256) * 256 * 10 <= (long)N * 11;
     if (dtype == TERNOCL_BF16) {
-        if (wide) moe_launch<8, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
-        else moe_launch<4, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        if (wide) moe_launch<Wide, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else moe_launch<Narrow, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
     } else {
-        if (wide) moe_launch<8, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
-        else moe_launch<4, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        if (wide) moe_launch<Wide, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else moe_launch<Narrow, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
     }
     return check_launch();
 }
