@@ -14,10 +14,11 @@
 // The route is a stable counting sort (rows of an expert in assignment order),
 // so every run produces the same permutation: the reference's atomic-order
 // permutation is not reproducible.  One workgroup: a histogram (LDS atomics,
-// order-free), the offsets, then chunks of 1024 assignments in order where each
-// wave ranks its lanes among equal expert ids with log2(E) ballots, the waves'
-// per-expert counts are prefix-summed in wave order, and every assignment gets
-// its slot.  Assignments whose expert id is outside [0, E) are dropped: no row,
+// order-free), the offsets, then blocks of 16384 assignments in order, each
+// wave holding a contiguous segment of the block in registers and ranking its
+// lanes among equal expert ids with log2(E) ballots; the waves' per-expert
+// counts are prefix-summed in wave order, and every assignment gets its slot.
+// Assignments whose expert id is outside [0, E) are dropped: no row,
 // inv = -1, no contribution to the combine.  The gather is not a separate pass
 // in the layer: the grouped GEMM reads row perm[p] / topk of X directly.
 #include "common.hpp"
@@ -32,67 +33,142 @@ ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const
 namespace {
 
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
+constexpr int kRouteChunks = 16;                                 // 64-id chunks per wave and block
+constexpr int kRouteBlock = kRouteWaves * kRouteChunks * 64;     // ids per block (16384)
 
+// Stable counting sort in one workgroup, in blocks of kRouteBlock ids: wave w
+// owns the contiguous segment [w, w + 1) * kRouteChunks * 64 of a block and
+// holds its ids in registers.  Pass 1 ranks every block into per-wave counts
+// (wave-private LDS rows, no atomics), whose sums give the histogram and the
+// offsets.  Pass 2 prefix-sums the per-wave counts in wave order on top of each
+// expert's running base (blocks in order, waves in order, chunks in order,
+// lanes in order: the stable order) and places every id.  Global loads happen
+// at the start of a block and stores at its end: no memory latency inside the
+// loops.
 __global__ void __launch_bounds__(kRouteThreads)
 k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict__ perm,
             int *__restrict__ inv, int G, int E, int rpt) {
     extern __shared__ int sh[];
-    int *cnt = sh, *base = sh + E, *wcnt = sh + 2 * E;  // wcnt [kRouteWaves][E]
+    int *cnt = sh, *run = sh + E, *wcnt = sh + 2 * E;  // wcnt [kRouteWaves][E]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int e = tid; e < E; e += kRouteThreads) cnt[e] = 0;
-    __syncthreads();
-    for (int g = tid; g < G; g += kRouteThreads) {
-        const int e = ids[g];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int r = 0, t = 0;
-        for (int e = 0; e < E; ++e) {
-            meta[e] = r;
-            meta[E + 1 + e] = t;
-            base[e] = r;
-            r += cnt[e];
-            t += (cnt[e] + rpt - 1) / rpt;
-        }
-        meta[E] = r;
-        meta[2 * E + 1] = t;
-    }
     const unsigned long long below = (1ull << lane) - 1ull;
-    for (int c0 = 0; c0 < G; c0 += kRouteThreads) {
-        for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wcnt[i] = 0;
-        __syncthreads();  // also orders base[] after the offsets on the first chunk
-        const int g = c0 + tid;
-        const int eg = g < G ? ids[g] : -1;
-        const bool valid = eg >= 0 && eg < E;  // out-of-range ids are dropped
-        const int e = valid ? eg : 0;
-        unsigned long long same = __ballot(valid);
-        for (int b = 0; (1 << b) < E; ++b) {
-            const bool bit = (e >> b) & 1;
-            const unsigned long long bal = __ballot(valid && bit);
-            same &= bit ? bal : ~bal;
+    int *mine = wcnt + wave * E;  // this wave's running counts
+    int eid[kRouteChunks], loc[kRouteChunks];
+
+    // Load a block's ids (wave w: the contiguous segment w of the block), then
+    // rank them: per 64-id chunk, lanes with equal expert ids find each other
+    // with log2(E) ballots, read the wave's running count of that expert and
+    // the chunk's leader advances it (LDS operations of one wave run in order).
+    auto load_block = [&](int b0) {
+        const int seg0 = b0 + wave * kRouteChunks * 64;
+#pragma unroll
+        for (int c = 0; c < kRouteChunks; ++c) {
+            const int g = seg0 + c * 64 + lane;
+            eid[c] = g < G ? ids[g] : -1;
         }
-        const int rank = __popcll(same & below);
-        if (valid && rank == 0) wcnt[wave * E + e] = __popcll(same);
-        __syncthreads();
+    };
+    auto rank_block = [&]() {
+#pragma unroll
+        for (int c = 0; c < kRouteChunks; ++c) {
+            const bool valid = eid[c] >= 0 && eid[c] < E;  // out-of-range ids are dropped
+            const int e = valid ? eid[c] : 0;
+            unsigned long long same = __ballot(valid);
+            for (int bit = 0; (1 << bit) < E; ++bit) {
+                const bool on = (e >> bit) & 1;
+                const unsigned long long bal = __ballot(valid && on);
+                same &= on ? bal : ~bal;
+            }
+            const int before = valid ? mine[e] : 0;  // every lane reads before the leader writes
+            loc[c] = before + __popcll(same & below);
+            if (valid && (same & below) == 0ull) mine[e] = before + __popcll(same);
+        }
+    };
+    // per-wave counts -> bases: wcnt[w][e] = run[e] + counts of waves < w
+    auto wave_bases = [&]() {
         for (int x = tid; x < E; x += kRouteThreads) {
-            int run = base[x];
+            int r = run[x];
             for (int w = 0; w < kRouteWaves; ++w) {
                 const int c = wcnt[w * E + x];
-                wcnt[w * E + x] = run;
-                run += c;
+                wcnt[w * E + x] = r;
+                r += c;
             }
-            base[x] = run;
+            run[x] = r;
         }
+    };
+    auto place_block = [&](int b0) {
+        const int seg0 = b0 + wave * kRouteChunks * 64;
+#pragma unroll
+        for (int c = 0; c < kRouteChunks; ++c) {
+            const int g = seg0 + c * 64 + lane;
+            if (eid[c] >= 0 && eid[c] < E) {
+                const int p = mine[eid[c]] + loc[c];
+                perm[p] = g;
+                inv[g] = p;
+            } else if (g < G) {
+                inv[g] = -1;
+            }
+        }
+    };
+
+    // Pass 1: every block's ids ranked into per-wave counts (no atomics).
+    for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wcnt[i] = 0;
+    __syncthreads();
+    for (int b0 = 0; b0 < G; b0 += kRouteBlock) {
+        load_block(b0);
+        rank_block();
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += kRouteThreads) {
+        int c = 0;
+        for (int w = 0; w < kRouteWaves; ++w) c += wcnt[w * E + x];
+        cnt[x] = c;
+    }
+    __syncthreads();
+    if (wave == 0) {  // row and row-tile offsets: a 64-lane inclusive scan per 64 experts
+        int r0 = 0, t0 = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const int c = e < E ? cnt[e] : 0, tl = (c + rpt - 1) / rpt;
+            int r = c, t = tl;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int ru = __shfl_up(r, o), tu = __shfl_up(t, o);
+                if (lane >= o) { r += ru; t += tu; }
+            }
+            if (e < E) {
+                meta[e] = r0 + r - c;
+                meta[E + 1 + e] = t0 + t - tl;
+                run[e] = r0 + r - c;
+            }
+            r0 += __shfl(r, 63);
+            t0 += __shfl(t, 63);
+        }
+        if (lane == 0) {
+            meta[E] = r0;
+            meta[2 * E + 1] = t0;
+        }
+    }
+    __syncthreads();
+
+    // Pass 2: place.  One block (G <= kRouteBlock): its ranks are still in
+    // registers and wcnt holds its per-wave counts.  Otherwise each block is
+    // loaded and ranked again, on top of the running bases.
+    if (G <= kRouteBlock) {
+        wave_bases();
         __syncthreads();
-        if (valid) {
-            const int p = wcnt[wave * E + e] + rank;
-            perm[p] = g;
-            inv[g] = p;
-        } else if (g < G) {
-            inv[g] = -1;
-        }
-        __syncthreads();  // wcnt is cleared for the next chunk
+        place_block(0);
+        return;
+    }
+    for (int b0 = 0; b0 < G; b0 += kRouteBlock) {
+        load_block(b0);
+        for (int e = lane; e < E; e += 64) mine[e] = 0;
+        __syncthreads();
+        rank_block();
+        __syncthreads();
+        wave_bases();
+        __syncthreads();
+        place_block(b0);
+        __syncthreads();  // wcnt is reset for the next block
     }
 }
 

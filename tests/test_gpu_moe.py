@@ -36,7 +36,7 @@ def _route(T, ids, G, E):
 
 
 @pytest.mark.parametrize("G,E,skew", [(1, 1, False), (100, 7, False), (16384, 64, False), (16384, 64, True),
-                                      (20000, 128, True), (3000, 512, False), (5000, 33, True)])
+                                      (20000, 128, True), (3000, 512, False), (5000, 33, True), (40000, 64, False)])
 def test_moe_route_matches_stable_sort(dev, orc, G, E, skew):
     import ternocl_amd as T
     g = synth.rng(G + E)
