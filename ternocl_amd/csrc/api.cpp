@@ -72,10 +72,7 @@ ternocl_status moe_combine_run(int dtype, const float *Y, const int *inv, const 
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
                             int E, int G, int N, int K, int postop, int out_f32, hipStream_t st);
-struct MoeWs {
-    size_t meta, perm, inv, u, h, y, total;
-};
-MoeWs moe_ws_layout(int T, int E, int topk, int H, int I);
+MoeWs moe_ws_layout(int T, int E, int topk, int H, int I);  // moe.hip
 ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
                                int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                                const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,

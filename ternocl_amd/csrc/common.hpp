@@ -179,6 +179,10 @@ __device__ __forceinline__ void xcd_tile_of(int id, int mt, int nt, int &tm, int
 
 // ---- host side ----------------------------------------------------------
 namespace tcl {
+// Byte offsets of the MoE layer's workspace regions (moe.hip: moe_ws_layout).
+struct MoeWs {
+    size_t meta, perm, inv, h, y, total;
+};
 // Records the HIP error text for ternocl_last_error() and maps it to a status.
 ternocl_status launch_status(hipError_t e);
 ternocl_status check_launch();

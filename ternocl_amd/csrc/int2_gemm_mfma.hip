@@ -138,12 +138,17 @@ template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
 
 // One BM x BN output tile of rows [0, mrows) of ar (mrows <= BM) and columns
 // [n0, n0 + BN) (columns >= N masked); C row r is crow0 + r.
-template <class Cfg, bool BF16>
+// DUAL: the MoE gate/up pair in one pass over A -- acc from (B, S) is the up
+// projection, acc2 from (B2, S2) the gate; C = DT(silu(gate) * DT(up)), the
+// two-launch sequence's result (up rounded to DT, then POSTOP 1) bit for bit.
+template <class Cfg, bool BF16, bool DUAL = false>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
                                           const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                           void *__restrict__ C, const uint16_t *__restrict__ Other,
                                           const void *__restrict__ Bias, int crow0, int N, int K, int n0,
-                                          int postop, int out_f32, uint16_t *lds) {
+                                          int postop, int out_f32, uint16_t *lds,
+                                          const uint32_t *__restrict__ B2 = nullptr,
+                                          const uint16_t *__restrict__ S2 = nullptr) {
     constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c16 = lane & 15, q = lane >> 4, h = q & 1;
@@ -196,33 +201,48 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // that are not stored -- or, past the last row, 0.
     const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
     const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
+    // (DUAL: the gate weights, same shape, same offsets)
+    const __amdgpu_buffer_rsrc_t rB2 = buf_rsrc(DUAL ? B2 + n0 : B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rS2 = buf_rsrc(DUAL ? S2 + n0 : S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
     uint32_t vb[2];
     vb[0] = (uint32_t)(((q >> 1) * N + wn + c16) * 4);
     vb[1] = vb[0] + (uint32_t)(8 * N);
     const uint32_t vs0 = (uint32_t)((wn + c16) * 2);
-    uint32_t bw[NCB][2], sraw[NCB];
+    constexpr int NB = DUAL ? 2 : 1;  // weight matrices
+    uint32_t bw[NB][NCB][2], sraw[NB][NCB];
     auto b_load = [&]() {
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
+        for (int m = 0; m < NB; ++m)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-                bw[cb][ks] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb[ks] + 64 * cb, 0, 0);
+            for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    bw[m][cb][ks] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(m ? rB2 : rB, vb[ks] + 64 * cb, 0, 0);
         vb[0] += (uint32_t)(16 * N);
         vb[1] += (uint32_t)(16 * N);
     };
     auto s_load = [&](int g) {  // the scales of group g (past the last: 0)
         const uint32_t v = vs0 + (uint32_t)(g * 2 * N);
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) sraw[cb] = __builtin_amdgcn_raw_buffer_load_b16(rS, v + 32 * cb, 0, 0);
+        for (int m = 0; m < NB; ++m)
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb)
+                sraw[m][cb] = __builtin_amdgcn_raw_buffer_load_b16(m ? rS2 : rS, v + 32 * cb, 0, 0);
     };
 
-    f32x4_t acc[NMB][NCB];
+    f32x4_t acc[NMB][NCB], acc2[DUAL ? NMB : 1][DUAL ? NCB : 1];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) acc[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (DUAL) {
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) acc2[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
-    ScaleOp<BF16> sop[NCB];
+    ScaleOp<BF16> sop[NB][NCB];
     a_load(0);
     b_load();
     s_load(0);
@@ -230,15 +250,19 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     for (int st = 0; st < stages; ++st) {
         __syncthreads();  // stage st staged; stage st - 1 consumed
         const uint16_t *abuf = lds + (size_t)(st & 1) * Cfg::BM * A_PITCH;
-        uint32_t bwc[NCB][2];
+        uint32_t bwc[NB][NCB][2];
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            bwc[cb][0] = bw[cb][0];
-            bwc[cb][1] = bw[cb][1];
-        }
+        for (int m = 0; m < NB; ++m)
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                bwc[m][cb][0] = bw[m][cb][0];
+                bwc[m][cb][1] = bw[m][cb][1];
+            }
         if ((st & 1) == 0) {  // a new 128-row scale group (uniform; no loads inside)
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) sop[cb].set(sraw[cb]);
+            for (int m = 0; m < NB; ++m)
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) sop[m][cb].set(sraw[m][cb]);
         }
         // next stage's loads in flight during this stage's MFMAs; the scales of
         // the group after this one are loaded on the group's second stage
@@ -257,9 +281,15 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
                 uint32_t bf[4];
-                frag(bwc[cb][ks], h, sop[cb], bf);
+                frag(bwc[0][cb][ks], h, sop[0][cb], bf);
 #pragma unroll
                 for (int mb = 0; mb < NMB; ++mb) acc[mb][cb] = mfma16<BF16>(af[mb], bf, acc[mb][cb]);
+                if constexpr (DUAL) {
+                    uint32_t bg[4];
+                    frag(bwc[NB - 1][cb][ks], h, sop[NB - 1][cb], bg);
+#pragma unroll
+                    for (int mb = 0; mb < NMB; ++mb) acc2[mb][cb] = mfma16<BF16>(af[mb], bg, acc2[mb][cb]);
+                }
             }
         }
         a_store(lds + (size_t)((st + 1) & 1) * Cfg::BM * A_PITCH);  // after the last stage: never read
@@ -275,20 +305,51 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     __syncthreads();  // the A buffers are free
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
+        const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
+        float up[DUAL ? NMB : 1][4];  // DUAL: DT(up) of this lane's 4 outputs per pass
+        if constexpr (DUAL) {
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) {
+                const f32x4_t v = acc[mb][cb] * fix;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * kEpPitch + c16] = v[i];
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int pass = 0; pass < NMB; ++pass) {
+                const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * kEpPitch + 4 * (lane & 3));
+                const float v4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) up[pass][i] = dt2f<BF16>(f2dt<BF16>(v4[i]));
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+        }
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
-            const f32x4_t v = acc[mb][cb] * fix;
+            const f32x4_t v = (DUAL ? acc2[DUAL ? mb : 0][DUAL ? cb : 0] : acc[mb][cb]) * fix;
 #pragma unroll
             for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * kEpPitch + c16] = v[i];
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
         __builtin_amdgcn_wave_barrier();
-        const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
+#pragma unroll
         for (int pass = 0; pass < NMB; ++pass) {
             const int r = wm + 16 * pass + (lane >> 2);
             const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * kEpPitch + 4 * (lane & 3));
             const float v4[4] = {t.x, t.y, t.z, t.w};
-            if (r < mrows && n < N) epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, crow0 + r, n, v4);
+            if (r < mrows && n < N) {
+                if constexpr (DUAL) {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = f2dt<BF16>(epi_apply(v4[i], 1, up[pass][i], 0.0f));
+                    *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
+                        make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                } else {
+                    epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, crow0 + r, n, v4);
+                }
+            }
         }
         __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
     }
@@ -317,13 +378,13 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // gather fused into the A-tile load), else from A_all[p].  Expert e's weights:
 // B_all + e*(K/16)*N, S_all + e*(K/128)*N; C and Other are indexed by the
 // sorted row p.
-template <class Cfg, bool BF16>
+template <class Cfg, bool BF16, bool DUAL>
 __global__ void __launch_bounds__(Cfg::THREADS)
 k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all,
                 const int *__restrict__ perm, int topk, const uint32_t *__restrict__ B_all,
                 const uint16_t *__restrict__ S_all, void *__restrict__ C_all,
                 const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
-                int ntn, int arows) {
+                int ntn, int arows, const uint32_t *__restrict__ B2_all, const uint16_t *__restrict__ S2_all) {
     static_assert(Cfg::BM == kMoeTileRows, "MoE row tiles are kMoeTileRows rows");
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
@@ -342,9 +403,10 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
     const ARows ar = perm ? ARows{A_all, perm + row0 + m0, topk}
                           : ARows{A_all + (size_t)(row0 + m0) * K, nullptr, 1};
     const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : mrows) * K * 2);
-    gemm_tile<Cfg, BF16>(ar, a_bytes, mrows, B_all + (size_t)e * (K / 16) * N,
-                                  S_all + (size_t)e * (K / kGS) * N, C_all, Other_all, nullptr, row0 + m0, N, K,
-                                  tn * Cfg::BN, postop, out_f32, lds);
+    const size_t bo = (size_t)e * (K / 16) * N, so = (size_t)e * (K / kGS) * N;
+    gemm_tile<Cfg, BF16, DUAL>(ar, a_bytes, mrows, B_all + bo, S_all + so, C_all, Other_all, nullptr, row0 + m0,
+                               N, K, tn * Cfg::BN, postop, out_f32, lds, DUAL ? B2_all + bo : nullptr,
+                               DUAL ? S2_all + so : nullptr);
 }
 
 // Test hook: the B fragments the GEMM builds at unit scale (DT 1.0),
@@ -413,15 +475,16 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
     else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
-template <class Cfg, bool BF16>
+template <class Cfg, bool BF16, bool DUAL = false>
 void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, const uint32_t *B_all,
                 const void *S_all, void *C_all, const void *Other_all, int E, int G, int N, int K, int postop,
-                int out_f32, hipStream_t st) {
+                int out_f32, hipStream_t st, const uint32_t *B2_all = nullptr, const void *S2_all = nullptr) {
     const int ntn = (N + Cfg::BN - 1) / Cfg::BN;
     const int max_tiles = (G + Cfg::BM - 1) / Cfg::BM + E;  // each expert's ragged tail adds at most one tile
-    hipLaunchKernelGGL((k_int2_moe_gemm<Cfg, BF16>), dim3((unsigned)(max_tiles * ntn)), dim3(Cfg::THREADS), 0, st, meta,
-                       (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
-                       (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn, perm ? G / topk : G);
+    hipLaunchKernelGGL((k_int2_moe_gemm<Cfg, BF16, DUAL>), dim3((unsigned)(max_tiles * ntn)), dim3(Cfg::THREADS), 0,
+                       st, meta, (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
+                       (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn, perm ? G / topk : G, B2_all,
+                       (const uint16_t *)S2_all);
 }
 
 }  // namespace
@@ -443,6 +506,24 @@ ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const
     } else {
         if (wide) moe_launch<Wide, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
         else moe_launch<Narrow, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+    }
+    return check_launch();
+}
+
+// The gate/up pair of the MoE layer in one launch: Hs = DT(silu(A x Bg) * DT(A x Bu)),
+// bit-identical to moe_gemm_run(up, postop 0) followed by moe_gemm_run(gate, postop 1).
+ternocl_status moe_gate_up_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
+                               const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
+                               int E, int G, int N, int K, hipStream_t st) {
+    typedef TileCfg<4, 4, 2, 4> Wide;
+    typedef TileCfg<4, 2, 2, 4> Narrow;
+    const bool wide = (long)((N + 255) / 256) * 256 * 10 <= (long)N * 11;
+    if (dtype == TERNOCL_BF16) {
+        if (wide) moe_launch<Wide, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+        else moe_launch<Narrow, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+    } else {
+        if (wide) moe_launch<Wide, false, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+        else moe_launch<Narrow, false, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
     }
     return check_launch();
 }

@@ -8,6 +8,8 @@
 //             perm (sorted row -> assignment g = t * topk + j), inv = perm^-1
 //   up        U = X[perm / topk] x B_up[e]                 (DT, POSTOP 0)
 //   gate      Hs = silu(X[perm / topk] x B_gate[e]) * U    (DT, POSTOP 1)
+//             (the layer runs the two as one launch, U kept in registers:
+//             the same operations, bit for bit)
 //   down      Y = Hs x B_down[e]                           (fp32)
 //   combine   O[t, n] = DT(sum_j RW[g] * Y[inv[g], n]),  g = t * topk + j, j in order
 //
@@ -29,6 +31,9 @@ int moe_tile_rows();  // int2_gemm_mfma.hip
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
                             int E, int G, int N, int K, int postop, int out_f32, hipStream_t st);
+ternocl_status moe_gate_up_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
+                               const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
+                               int E, int G, int N, int K, hipStream_t st);
 
 namespace {
 
@@ -238,10 +243,7 @@ ternocl_status moe_combine_run(int dtype, const float *Y, const int *inv, const 
     return check_launch();
 }
 
-// Workspace of the layer: meta | perm | inv | U | Hs | Y, each 256-byte aligned.
-struct MoeWs {
-    size_t meta, perm, inv, u, h, y, total;
-};
+// Workspace of the layer: meta | perm | inv | Hs | Y, each 256-byte aligned.
 MoeWs moe_ws_layout(int T, int E, int topk, int H, int I) {
     const size_t G = (size_t)T * topk;
     MoeWs w;
@@ -249,7 +251,6 @@ MoeWs moe_ws_layout(int T, int E, int topk, int H, int I) {
     w.meta = o; o = align_up(o + (size_t)(2 * E + 2) * 4, 256);
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
-    w.u = o;    o = align_up(o + G * I * 2, 256);
     w.h = o;    o = align_up(o + G * I * 2, 256);
     w.y = o;    o = align_up(o + G * H * 4, 256);
     w.total = o;
@@ -263,13 +264,13 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
     const MoeWs w = moe_ws_layout(T, E, topk, H, I);
     char *b = (char *)ws;
     int *meta = (int *)(b + w.meta), *perm = (int *)(b + w.perm), *inv = (int *)(b + w.inv);
-    void *U = b + w.u, *Hs = b + w.h;
+    void *Hs = b + w.h;
     float *Y = (float *)(b + w.y);
     const int G = T * topk;
     ternocl_status s;
     if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
-    if ((s = moe_gemm_run(dtype, meta, X, perm, topk, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK) return s;
-    if ((s = moe_gemm_run(dtype, meta, X, perm, topk, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK) return s;
+    // up and gate in one pass over the gathered rows (U never leaves the registers)
+    if ((s = moe_gate_up_run(dtype, meta, X, perm, topk, Bu, Su, Bg, Sg, Hs, E, G, I, H, st)) != TERNOCL_OK) return s;
     if ((s = moe_gemm_run(dtype, meta, Hs, nullptr, 1, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK) return s;
     return moe_combine_run(dtype, Y, inv, RW, O, T, topk, H, st);
 }

@@ -214,3 +214,34 @@ def test_moe_layer_workload_shape(dev, orc):
     assert rel < 1e-2, rel
     again = _layer(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16)
     assert np.array_equal(out, again)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("I", [384, 512])
+def test_moe_layer_equals_stage_composition(dev, orc, bf16, I):
+    """The layer (up and gate as one launch) gives, bit for bit, what the separate entry
+    points give stage by stage: route, up (POSTOP 0), gate (POSTOP 1 on up), down (fp32),
+    combine.  I = 384 takes 128-column tiles, I = 512 256-column tiles."""
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H = 160, 8, 4, 256
+    g = synth.rng(31 + I)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+    W = _weights(g, E, H, I, bf16)
+    got = _layer(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16)
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    G = Tk * topk
+    dt = torch.bfloat16 if bf16 else torch.float16
+    meta, perm, inv = _route(T, ids, G, E)
+    dX = dev_dt(X, bf16)
+    U = torch.zeros((G, I), dtype=dt, device="cuda")
+    Hs = torch.zeros((G, I), dtype=dt, device="cuda")
+    Y = torch.zeros((G, H), dtype=torch.float32, device="cuda")
+    O = torch.zeros((Tk, H), dtype=dt, device="cuda")
+    T.int2_moe_gemm(meta, dX, perm, topk, dev_raw(Bu), dev_dt(Su, bf16), U, None, E, G, I, H, 0, False)
+    T.int2_moe_gemm(meta, dX, perm, topk, dev_raw(Bg), dev_dt(Sg, bf16), Hs, U, E, G, I, H, 1, False)
+    T.int2_moe_gemm(meta, Hs, None, 1, dev_raw(Bd), dev_dt(Sd, bf16), Y, None, E, G, H, I, 0, True)
+    T.int2_moe_combine(Y, inv, dev_dt(RW, bf16), O, Tk, topk, H)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, host_u16(O))
