@@ -15,8 +15,9 @@
 // column's sign stream at SR[s-1]); the slices reduce through LDS in slice
 // order (deterministic).  Per 64-row chunk a lane loads the column's two
 // bitmap words and three sign words (the chunk consumes at most 64 sign bits
-// from the column's rank onwards); loads run two chunks (bitmap) and one chunk
-// (signs, whose address needs the rank, i.e. the previous bitmap words) ahead.
+// from the column's rank onwards); loads run four chunks (bitmap) and three
+// chunks (signs, whose address needs the rank, i.e. the previous bitmap words)
+// ahead.
 // Decode per 32-row word: the word's sign window is funnel-shifted out of the
 // three sign words (v_alignbit); each 4-row nibble m and the next four window
 // bits s index a 256-entry LDS table of four DT codes +1 / -1 / 0 (a 4-bit
@@ -103,11 +104,23 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
 #pragma unroll
     for (int r = 0; r < MR; ++r) ar[r] = (const uint32_t *)(A + (size_t)min(m0 + r, M - 1) * K);
 
+    // Loads run ahead of the decode in a ring of kL chunk slots: bitmap words
+    // kL chunks ahead, sign words kL - 1 chunks ahead (a chunk's sign address
+    // needs the ranks of the chunks before it, i.e. their bitmap words), group
+    // scales likewise, all unconditionally (a load under a branch is waited
+    // for at once, and with it -- vmcnt counts in order -- every load issued
+    // before it).  The chunk loop is unrolled by kL so each slot is a fixed
+    // register set: copying a register whose load is in flight would wait for
+    // it.  Bitmap words of chunks past the slice read as 0, so the rank stops
+    // there and the sign loads repeat the last window (inside the stream and
+    // its pad words).
+    constexpr int kL = 4;
     auto bm_load = [&](int c, uint32_t b[2]) {
         const int cc = c < chunks ? c : chunks - 1;
         const size_t kp = (size_t)((k0 >> 5) + 2 * cc);
-        b[0] = Bc[kp * N + nc];
-        b[1] = Bc[(kp + 1) * N + nc];
+        const uint32_t x = Bc[kp * N + nc], y = Bc[(kp + 1) * N + nc];
+        b[0] = c < chunks ? x : 0u;
+        b[1] = c < chunks ? y : 0u;
     };
     auto sg_load = [&](uint32_t r, uint32_t q[3]) {
         const uint32_t w = r >> 5;
@@ -115,50 +128,68 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
         q[1] = sg[w + 1];
         q[2] = sg[w + 2];
     };
+    const int groups = K / kGS;
+    auto s_load = [&](int c) {
+        const int g = min((k0 + 64 * c) >> 7, groups - 1);
+        return (uint32_t)S[(size_t)g * N + nc];
+    };
 
     float acc[MR], part[MR];
 #pragma unroll
     for (int r = 0; r < MR; ++r) acc[r] = part[r] = 0.0f;
 
-    uint32_t bmA[2], bmB[2], qA[3];
-    bm_load(0, bmA);
-    bm_load(1, bmB);
-    sg_load(R, qA);
-    for (int c = 0; c < chunks; ++c) {
-        const uint32_t b0 = bmA[0], b1 = bmA[1];
-        uint32_t q[3] = {qA[0], qA[1], qA[2]};
-        const uint32_t r0 = R, r1 = __builtin_popcount(b0) + r0;
-        R = __builtin_popcount(b1) + r1;
-        // next chunk's signs (its rank is known now) and the bitmap two chunks ahead
-        sg_load(R, qA);
-        bmA[0] = bmB[0]; bmA[1] = bmB[1];
-        bm_load(c + 2, bmB);
+    // slot u holds chunk c with c % kL == u
+    uint32_t bm[kL][2], q[kL][3], rs[kL], sc[kL];
+#pragma unroll
+    for (int i = 0; i < kL; ++i) bm_load(i, bm[i]);
+#pragma unroll
+    for (int i = 0; i + 1 < kL; ++i) {
+        rs[i] = i ? rs[i - 1] + __builtin_popcount(bm[i - 1][0]) + __builtin_popcount(bm[i - 1][1]) : R;
+        sg_load(rs[i], q[i]);
+        sc[i] = s_load(i);
+    }
+    for (int c0 = 0; c0 < chunks; c0 += kL) {
+#pragma unroll
+        for (int u = 0; u < kL; ++u) {
+            const int c = c0 + u;
+            if (c >= chunks) break;  // uniform
+            const int un = (u + kL - 1) % kL, up = (u + kL - 2) % kL;  // slots of chunks c + kL - 1, c + kL - 2
+            const uint32_t b0 = bm[u][0], b1 = bm[u][1];
+            const uint32_t r0 = rs[u], r1 = __builtin_popcount(b0) + r0;
+            const uint32_t qc[3] = {q[u][0], q[u][1], q[u][2]};
+            const uint32_t scu = sc[u];
+            // chunk c + kL - 1: rank (from chunk c + kL - 2), signs, scale; chunk c + kL: bitmap
+            rs[un] = rs[up] + __builtin_popcount(bm[up][0]) + __builtin_popcount(bm[up][1]);
+            sg_load(rs[un], q[un]);
+            sc[un] = s_load(c + kL - 1);
+            bm_load(c + kL, bm[u]);
 
-        const int k = k0 + 64 * c;
-        const uint32_t base = r0 >> 5;
+            const int k = k0 + 64 * c;
+            const uint32_t base = r0 >> 5;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint2 e[8];
-            bc_decode_word(lut, h ? b1 : b0, bc_window(q, base, h ? r1 : r0), e);
-            const int kd = (k + 32 * h) >> 1;  // first activation pair of the word
+            for (int h = 0; h < 2; ++h) {
+                uint2 e[8];
+                bc_decode_word(lut, h ? b1 : b0, bc_window(qc, base, h ? r1 : r0), e);
+                const int kd = (k + 32 * h) >> 1;  // first activation pair of the word
 #pragma unroll
-            for (int r = 0; r < MR; ++r) {
-                float pr = part[r];
+                for (int r = 0; r < MR; ++r) {
+                    float pr = part[r];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    pr = dot2<BF16>(e[i].x, ar[r][kd + 2 * i], pr);
-                    pr = dot2<BF16>(e[i].y, ar[r][kd + 2 * i + 1], pr);
+                    for (int i = 0; i < 8; ++i) {
+                        pr = dot2<BF16>(e[i].x, ar[r][kd + 2 * i], pr);
+                        pr = dot2<BF16>(e[i].y, ar[r][kd + 2 * i + 1], pr);
+                    }
+                    part[r] = pr;
                 }
-                part[r] = pr;
             }
-        }
-        // group end (or slice end mid-group): apply the group's scale
-        if (((k + 64) & (kGS - 1)) == 0 || c + 1 == chunks) {
-            const float s = dt2f<BF16>(S[(size_t)(k >> 7) * N + nc]);
+            // group end (or slice end mid-group): apply the group's scale
+            if (((k + 64) & (kGS - 1)) == 0 || c + 1 == chunks) {
+                const float s = dt2f<BF16>(scu);
 #pragma unroll
-            for (int r = 0; r < MR; ++r) {
-                acc[r] += part[r] * s;
-                part[r] = 0.0f;
+                for (int r = 0; r < MR; ++r) {
+                    acc[r] += part[r] * s;
+                    part[r] = 0.0f;
+                }
             }
         }
     }
