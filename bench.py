@@ -377,7 +377,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-sample-s", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-sweep", action="store_true", help="skip the M = 2, 4, 8 sweep and the VALU engine")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the M = 2, 4, 8 sweep and the VALU and bf16-MFMA engines")
     ap.add_argument("--only-headline", action="store_true", help="skip the prefill, C1, C4 and C5 workloads")
     ap.add_argument("--probe", type=int, default=0, metavar="N",
                     help="counter-collection mode for rocprofv3 --pmc: N eager launches per GEMV shape, "
@@ -478,6 +478,14 @@ def main():
             del sb
             torch.cuda.empty_cache()
         extra["valu_engine_m1"] = valu
+        bf = {}
+        for K, N in SHAPES:
+            sb = ShapeBench(torch, T, synth, formats, 1, K, N, 600, tile=T.gemv_tile(T.MFMA))
+            us = per_launch_us(torch, sb, 100)
+            bf[f"K{K}_N{N}"] = {"us": round(us, 3), "GB/s": round(sb.bytes() / (us * 1e-6) / 1e9, 1)}
+            del sb
+            torch.cuda.empty_cache()
+        extra["bf16_mfma_engine_m1"] = bf
 
     if not args.only_headline:
         extra["prefill"] = bench_c3(torch, T, synth, formats, orc)
@@ -511,7 +519,7 @@ def main():
         "config": {"workload": "int2_fp16_upcvt decode GEMV, M=1, bf16, bias+residual epilogue, "
                                "step = (K=4096,N=14336) + (K=14336,N=4096)",
                    "M": 1, "shapes": [list(s) for s in SHAPES], "epilogue": "acc + bias[n] + residual",
-                   "engine": "mfma"},
+                   "engine": "fp8 x fp4 block-scaled MFMA (engine 4)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "shapes": shapes,

@@ -70,8 +70,10 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint
 /* Decode-GEMV tile, the reference's -DSGM/-DNSG_N/-DLS/-DU knobs for this
  * hardware.  Every field 0 = automatic. */
 typedef struct {
-    int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: MFMA GEMV (M <= 16);
-                            3: MFMA prefill GEMM (any M, 128 x 128 tiles; the M > 16 engine) */
+    int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: bf16/fp16 MFMA GEMV (M <= 16);
+                            3: MFMA prefill GEMM (any M, 128 x 128 tiles; the M > 16 engine);
+                            4: block-scaled fp8 x fp4 MFMA GEMV (M <= 4, A 16-byte aligned;
+                               the automatic choice where it applies) */
     int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
     int cols_per_lane;   /* MFMA: adjacent columns per lane, 1, 2 or 4 (16-, 32- or 64-column strips) */
     int groups_per_wave; /* MFMA: 128-row groups per wave per LDS window, 1..16 (power of
@@ -80,7 +82,8 @@ typedef struct {
 } ternocl_gemv_tile;
 
 /* Same as ternocl_int2_fp16_upcvt_gemm with an explicit tile (NULL = automatic:
- * the MFMA GEMV for M <= 16, the prefill GEMM above).  When M > 16 the engine
+ * the fp8 x fp4 GEMV for M <= 4 (A 16-byte aligned), the bf16/fp16 MFMA GEMV
+ * for other M <= 16, the prefill GEMM above).  When M > 16 the engine
  * must be 0 or 3. */
 ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const uint32_t *B,
                                                const void *S, void *C, const void *Other,
@@ -98,7 +101,9 @@ ternocl_status ternocl_workspace_zero(void *ws, size_t ws_bytes, void *stream);
  * too: ternocl_int2_gemv_decode writes, per B word, the 8 packed DT pairs that
  * engine (1 = VALU GEMV, 2 = MFMA GEMV, 3 = prefill GEMM) builds (layout
  * [K/16][N][8] uint32); the prefill GEMM folds the group scale into its
- * fragments, and the hook builds them at unit scale (DT 1.0). */
+ * fragments, and the hook builds them at unit scale (DT 1.0).  Engine 4 (the
+ * fp8 x fp4 GEMV) writes its 2 fp4 dwords per word instead ([K/16][N][2]:
+ * nibble n of dword h = row 2n + h as e2m1 v/2). */
 ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
                                     int N, void *stream);
 ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,

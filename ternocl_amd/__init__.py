@@ -110,7 +110,7 @@ def workspace_zero(ws, stream=None) -> None:
 
 
 GemvTile = _abi.GemvTile
-VALU, MFMA, GEMM = 1, 2, 3  # engines: VALU GEMV, MFMA GEMV, MFMA prefill GEMM
+VALU, MFMA, GEMM, F4 = 1, 2, 3, 4  # engines: VALU GEMV, MFMA GEMV, MFMA prefill GEMM, fp8 x fp4 GEMV
 
 
 def gemv_tile(engine: int = 0, waves: int = 0, cols_per_lane: int = 0, groups_per_wave: int = 0,
@@ -139,7 +139,8 @@ def int2_dequant(B, S, W, K: int, N: int, stream=None) -> None:
 
 
 def int2_gemv_decode(B, D, K: int, N: int, bf16: bool, engine: int = MFMA, stream=None) -> None:
-    """D[word][j] = the packed DT pair j an engine builds from each B word (test hook)."""
+    """D[word][j] = the packed DT pair j an engine builds from each B word (test hook;
+    engine 4 writes its two fp4 dwords per word)."""
     _check(lib().ternocl_int2_gemv_decode(BF16 if bf16 else FP16, engine, _ptr(B), _ptr(D), K, N,
                                           _stream(stream)))
 

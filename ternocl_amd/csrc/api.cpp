@@ -38,6 +38,12 @@ ternocl_status int2_gemv_mfma_run(int dtype, const void *A, const uint32_t *B, c
                                   hipStream_t st);
 ternocl_status int2_mfma_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N,
                                     hipStream_t st);
+// kernels (int2_gemv_f4.hip)
+bool int2_gemv_f4_supports(int M, int N, const void *A);
+ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
+                                const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                int out_f32, int waves, int cpl, int gpw, hipStream_t st);
+ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (int2_gemm_mfma.hip)
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
@@ -147,11 +153,15 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
     if (s != TERNOCL_OK) return s;
     (void)ws; (void)ws_bytes;
     const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0};
-    if (t.engine < 0 || t.engine > 3) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..3");
+    if (t.engine < 0 || t.engine > 4) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..4");
     if (t.engine == 3 || (M > 16 && t.engine == 0))
         return int2_gemm_mfma_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32,
                                   (hipStream_t)stream);
     if (M <= 16) {
+        // automatic: the fp8 x fp4 engine where it applies, else the bf16/fp16 MFMA GEMV
+        if (t.engine == 4 || (t.engine == 0 && int2_gemv_f4_supports(M, N, A)))
+            return int2_gemv_f4_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,
+                                    t.cols_per_lane, t.groups_per_wave, (hipStream_t)stream);
         if (t.engine == 1) {
             if (M > 8) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the VALU GEMV takes M <= 8");
             return int2_gemv_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,
@@ -185,8 +195,9 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
     ternocl_status s = check_dtype(dtype);
     if (s != TERNOCL_OK) return s;
     if (!B || !D) FAIL(TERNOCL_ERR_INVALID_ARG, "B and D must be non-null");
-    if (engine < 1 || engine > 3) FAIL(TERNOCL_ERR_INVALID_ARG, "engine must be 1 (VALU), 2 (MFMA GEMV) or 3 (GEMM)");
+    if (engine < 1 || engine > 4) FAIL(TERNOCL_ERR_INVALID_ARG, "engine must be 1 (VALU), 2 (MFMA GEMV), 3 (GEMM) or 4 (fp8 x fp4 GEMV)");
     if (N < 16 || N % 16 || K < 16 || K % 16) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % 16 == 0");
+    if (engine == 4) return int2_f4_decode_run(B, D, K, N, (hipStream_t)stream);
     if (engine == 3) return int2_gemm_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     if (engine == 2) return int2_mfma_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     return int2_gemv_decode_run(dtype, B, D, K, N, (hipStream_t)stream);

@@ -1,0 +1,590 @@
+// int2_gemv_f4.hip -- decode GEMV for packed 2-bit ternary weights on the
+// gfx950 block-scaled fp8 x fp4 matrix cores (engine 4, the default for
+// M <= 4).  Replaces int2_fp16_upcvt_gemm
+// (int2_fp16_upcvt/int2_fp16_upcvt.cl:193-290):
+//
+//   C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(B[k,n])))
+//
+// A decode GEMV streams the weights once; what bounds it after the memory is
+// the VALU work done per weight while the stream arrives.  This engine keeps
+// that work small on both operands:
+//
+// * Weights become fp4 (e2m1) MFMA operands with six bit operations per 16
+//   weights: a code's two bits (b1 b0) go to bits 3 and 0 of a nibble, which
+//   is +0, +0.5, -0.5 (and -0 for the unused code 2) for codes 0, 1, 3, i.e.
+//   exactly v / 2.  A word's even rows fill one dword, its odd rows another.
+// * Activations become fp8 (e4m3) "pieces" that sum to the activation:
+//   piece p = rne_e4m3(r_p / s_p), r_0 = a, r_{p+1} = r_p - piece_p * s_p, with
+//   a power-of-two scale s_p per piece and per 32-activation block taken from
+//   the block's largest |r_p| (the MFMA's E8M0 block scales: that largest
+//   value lands in [128, 256)).  Each piece of each activation row is its own
+//   MFMA row, so one v_mfma_scale_f32_16x16x128_f8f6f4 computes
+//   sum piece * v / 2 for all pieces and rows of a 128-row scale group over
+//   16 columns.
+// * Exactness.  The products are exact, but the MFMA adds the products of a
+//   32-block with about 12 bits below the block's largest product (measured
+//   on gfx950: a product 2^13 below the largest one loses its low bits).  So
+//   every piece but the last leaves values below s_p / 2 (more than 2^8 below
+//   the block's largest) to the next piece: a piece row's block then spans at
+//   most 12 bits (4-bit significands from 2^8 down to 2^-1, in units of s_p)
+//   and adds exactly.  bf16 takes 3 pieces, fp16 4 (rows 4m..4m+3 of the
+//   MFMA); a bf16 / fp16 activation within 2^12 of its block's largest is
+//   represented exactly, smaller ones to about 2^-20 of that largest value.
+// Operand layout of the 16x16x128 MFMA (lane l, r = l % 16, q = l / 16),
+// measured on gfx950: A (8 dwords of fp8) byte s of lane (r, q) is k = 16q + s
+// for s < 16 and 64 + 16q + (s - 16) otherwise; B (4 dwords of fp4) nibble s
+// of lane (c, q) is k = 32q + s; the E8M0 scale of A rows r, k in
+// [32b, 32b + 32) comes from lane r + 16b; D element i of lane (c, q) is row
+// 4q + i, column c.  So lane (c, q) takes words 2q and 2q + 1 of each group
+// (its B dwords: even rows of word 2q, odd rows of 2q, even of 2q + 1, odd of
+// 2q + 1), and the activations are staged in that k order.
+//
+// Work split (as the bf16 MFMA engine): a workgroup owns a strip of 16 * CPL
+// columns over all of K; waves take contiguous runs of GPW groups per LDS
+// window; each wave stages its own groups' pieces (no workgroup barrier
+// before its MACs); wave partials are reduced through LDS in wave order
+// (deterministic bit for bit).
+#include "common.hpp"
+
+#include <climits>
+
+namespace tcl {
+namespace {
+
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x2_t __attribute__((ext_vector_type(2)));
+
+// Pieces per activation (bf16 3, fp16 4) in MFMA rows 4m .. 4m + P - 1: an
+// activation row's pieces sit in one lane of the MFMA result (rows 4q..4q+3).
+__host__ __device__ constexpr int f4_pieces(bool bf16) { return bf16 ? 3 : 4; }
+constexpr int kF4RowStride = 4;
+constexpr int kF4MaxM = 16 / kF4RowStride;
+
+// One weight word (rows 0..15 of a column) -> fp4 dwords: d0 nibble n = row 2n,
+// d1 nibble n = row 2n + 1; nibble = (b1 << 3) | b0 of the row's code.
+__device__ __forceinline__ void f4_decode(uint32_t w, uint32_t &d0, uint32_t &d1) {
+    d0 = ((w << 2) & 0x88888888u) | (w & 0x11111111u);
+    d1 = (w & 0x88888888u) | ((w >> 2) & 0x11111111u);
+}
+
+// E8M0 exponent (biased, 2..254) of the scale that maps a block whose
+// largest magnitude has fp32 biased exponent e into [128, 256): 2^(e - 134)
+// (at least 2^-125, so that half of it is still a normal fp32 number).
+__device__ __forceinline__ uint32_t f4_scale_exp(uint32_t maxbits) {
+    const int e = (int)(maxbits >> 23) - 7;
+    return (uint32_t)(e < 2 ? 2 : (e > 254 ? 254 : e));
+}
+
+// max over the 4 lanes of a quad (lanes 4b .. 4b + 3: one 32-activation block)
+__device__ __forceinline__ uint32_t quad_max(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));  // [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));  // [2,3,0,1]
+    return v;
+}
+
+// Four fp32 values (rows i0, i1, i2, i3 of a block) -> four e4m3 bytes of x / s.
+__device__ __forceinline__ uint32_t f8x4(float a, float b, float c, float d, float s) {
+    s16x2_t r = {0, 0};
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, a, b, s, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, c, d, s, true);
+    uint32_t u;
+    __builtin_memcpy(&u, &r, 4);
+    return u;
+}
+// ... and back: the four values times s.
+__device__ __forceinline__ void f8x4_back(uint32_t u, float s, float o[4]) {
+    const f32x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)u, s, false);
+    const f32x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)u, s, true);
+    o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
+}
+
+// Byte offset, inside a piece row's 128 bytes, of the 4 even-row bytes of
+// the activations 8u .. 8u + 7 of a group (the odd-row bytes follow 8 bytes
+// later).  In MFMA k order a 16-activation block b16 keeps its even rows at
+// k = 16 b16 + 0..7 and its odd rows at 16 b16 + 8..15; k = 16 b16 + s' sits in
+// byte 32 b16 + s' (b16 < 4) or 32 (b16 - 4) + 16 + s' (b16 >= 4).
+__device__ __forceinline__ int f4_byte_off(int u) {
+    const int b16 = u >> 1, half = u & 1;
+    return (b16 < 4 ? 32 * b16 : 32 * (b16 - 4) + 16) + 4 * half;
+}
+
+// LDS of one window of one wave: data [GPW][RR][128] bytes, then scales
+// [GPW][RR][4] bytes (RR = MFMA rows in use), rounded up to 16 bytes.
+__host__ __device__ constexpr int f4_window_bytes(int rr, int gpw) { return (gpw * rr * 132 + 15) & ~15; }
+
+// Activation staging of one window: tasks (m, gl, u) = 8 activations
+// A[m, 128 g + 8u .. + 7] of row m < MR, window group gl < GPW, u < 16; task
+// idx = (m * GPW + gl) * 16 + u; lane takes idx = lane + 64 t.  A quad of
+// lanes holds one 32-activation block (u = 4b .. 4b + 3).
+template <int MR, int GPW, bool BF16> struct F4Stage {
+    static constexpr int P = f4_pieces(BF16), RS = kF4RowStride, RR = RS * MR;
+    static constexpr int T = MR * GPW * 16, TPL = (T + 63) / 64;
+    uint4 raw[TPL];
+    // Unconditional loads (row and group clamped into range): a load under a
+    // branch is waited for at the branch's end.
+    __device__ __forceinline__ void load(const uint16_t *__restrict__ A, int M, int K, int groups, int g0,
+                                         int lane) {
+#pragma unroll
+        for (int t = 0; t < TPL; ++t) {
+            const int idx = lane + 64 * t, u = idx & 15, mg = idx >> 4;
+            const int m = mg / GPW, gl = mg % GPW;
+            const int mc = m < M ? m : M - 1, g = g0 + gl < groups ? g0 + gl : groups - 1;
+            raw[t] = *(const uint4 *)(A + (size_t)mc * K + (size_t)g * kGS + 8 * u);
+        }
+    }
+    __device__ __forceinline__ void store(uint8_t *data, int lane) const {
+#pragma unroll
+        for (int t = 0; t < TPL; ++t) {
+            const int idx = lane + 64 * t, u = idx & 15, mg = idx >> 4;
+            const int m = mg / GPW, gl = mg % GPW;
+            const bool live = idx < T;
+            const uint32_t w[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
+            float f[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[2 * i] = dt2f<BF16>(w[i] & 0xffffu);
+                f[2 * i + 1] = dt2f<BF16>(w[i] >> 16);
+            }
+            float r[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r[i] = f[i];
+            const int row0 = (gl * RR + RS * m) * 128 + f4_byte_off(u);
+            const int srow0 = GPW * RR * 128 + (gl * RR + RS * m) * 4 + (u >> 2);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                float mx = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(r[i]));
+                const uint32_t se = f4_scale_exp(quad_max(__float_as_uint(mx)));
+                const float s = __uint_as_float(se << 23);
+                float x[8];
+                if (p + 1 < P) {  // values below s / 2 go to the next piece
+                    const float thr = __uint_as_float((se - 1) << 23);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) x[i] = fabsf(r[i]) < thr ? 0.0f : r[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) x[i] = r[i];
+                }
+                const uint32_t ev = f8x4(x[0], x[2], x[4], x[6], s);
+                const uint32_t od = f8x4(x[1], x[3], x[5], x[7], s);
+                if (live) {
+                    *(uint32_t *)(data + row0 + p * 128) = ev;
+                    *(uint32_t *)(data + row0 + p * 128 + 8) = od;
+                    if ((u & 3) == 0) data[srow0 + p * 4] = (uint8_t)se;
+                }
+                if (p + 1 < P) {  // residual for the next piece
+                    float be[4], bo[4];
+                    f8x4_back(ev, s, be);
+                    f8x4_back(od, s, bo);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        r[2 * i] -= be[i];
+                        r[2 * i + 1] -= bo[i];
+                    }
+                }
+            }
+        }
+    }
+};
+
+template <int CPL> struct F4Words;
+template <> struct F4Words<1> {
+    uint32_t v[1];
+    __device__ void load(const uint32_t *p) { v[0] = *p; }
+};
+template <> struct F4Words<2> {
+    uint32_t v[2];
+    __device__ void load(const uint32_t *p) {
+        const uint2 t = *(const uint2 *)p;
+        v[0] = t.x; v[1] = t.y;
+    }
+};
+template <> struct F4Words<4> {
+    uint32_t v[4];
+    __device__ void load(const uint32_t *p) {
+        const uint4 t = *(const uint4 *)p;
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+};
+
+// This wave's weight words (words 2q and 2q + 1 of each group) and raw scale
+// bits of one window; loads unconditional (group clamped; groups past K are
+// never consumed).
+template <int CPL, int GPW> struct F4Slab {
+    F4Words<CPL> w[GPW][2];
+    uint32_t sc[GPW][(CPL + 1) / 2];
+    __device__ __forceinline__ void load(const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
+                                         int N, int groups, int g0w, int q, int n0) {
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            const int g = g0w + gi < groups ? g0w + gi : groups - 1;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) w[gi][t].load(B + ((size_t)g * 8 + 2 * q + t) * N + n0);
+            if constexpr (CPL == 4) {
+                const uint2 t = *(const uint2 *)(S + (size_t)g * N + n0);
+                sc[gi][0] = t.x;
+                sc[gi][1] = t.y;
+            } else if constexpr (CPL == 2) {
+                sc[gi][0] = *(const uint32_t *)(S + (size_t)g * N + n0);
+            } else {
+                sc[gi][0] = S[(size_t)g * N + n0];
+            }
+        }
+    }
+    __device__ __forceinline__ uint32_t scale(int gi, int j) const {
+        return CPL == 1 ? sc[gi][0] : ((j & 1) ? sc[gi][j >> 1] >> 16 : sc[gi][j >> 1] & 0xffffu);
+    }
+};
+
+// Epilogue operands of the outputs a lane of wave 0 stores: row m = q,
+// columns n0 + j.  Buffer loads with no branch: the other waves (and an
+// operand the post-op does not use) pass an offset past the buffer's end,
+// which returns 0 without a memory access, so the loads can be issued early
+// and waited for only at the epilogue.
+template <int MR, int CPL, bool BF16> struct F4EpiIn {
+    static constexpr int OPL = 1;  // outputs per lane: row m = q
+    // raw bits, converted only in the epilogue (a conversion here would make
+    // the compiler wait for these loads, which follow every weight load)
+    uint32_t o[OPL][CPL], b[CPL];
+    __device__ __forceinline__ void load(const uint16_t *__restrict__ Other, const void *__restrict__ Bias,
+                                         int postop, int out_f32, int M, int N, int q, int n0, bool mine) {
+        const bool uo = postop_needs_other(postop), ub = postop_needs_bias(postop);
+        const uint32_t ob = uo ? (uint32_t)((size_t)M * N * 2) : 0u;
+        const uint32_t bb = ub ? (uint32_t)((size_t)N * (out_f32 ? 4 : 2)) : 0u;
+        const __amdgpu_buffer_rsrc_t ro = buf_rsrc(uo ? Other : nullptr, ob);
+        const __amdgpu_buffer_rsrc_t rb = buf_rsrc(ub ? Bias : nullptr, bb);
+        const int m = q < M ? q : M - 1;
+        const uint32_t off = 0x7ffffff0u;
+        const int bsz = out_f32 ? 4 : 2;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t oo = mine ? (uint32_t)(((size_t)m * N + n0 + j) * 2) : off;
+            o[0][j] = __builtin_amdgcn_raw_buffer_load_b16(ro, oo, 0, 0);
+            const uint32_t bo = mine ? (uint32_t)((n0 + j) * bsz) : off;
+            b[j] = out_f32 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb, bo, 0, 0)
+                           : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, bo, 0, 0);
+        }
+    }
+    __device__ __forceinline__ float other(int h, int j) const { return dt2f<BF16>(o[h][j]); }
+    __device__ __forceinline__ float bias(int j, int out_f32) const {
+        return out_f32 ? __uint_as_float(b[j]) : dt2f<BF16>(b[j]);
+    }
+};
+
+// Workgroup barrier between a window's activation loads and its weight loads
+// (no data wait): every wave's activation requests enter the memory pipeline
+// ahead of the weight stream.  The returned zero passes through an asm so the
+// weight loads stay below the barrier.
+__device__ __forceinline__ int f4_loads_after_barrier() {
+    __builtin_amdgcn_s_barrier();
+    int zero = 0;
+    asm volatile("" : "+s"(zero));
+    return zero;
+}
+
+template <int MR, int CPL, int GPW, bool BF16>
+__global__ void __launch_bounds__(512)
+k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
+               const uint16_t *__restrict__ S, void *__restrict__ C,
+               const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
+               int K, int postop, int out_f32, int swz) {
+    constexpr int RS = kF4RowStride, RR = RS * MR, P = f4_pieces(BF16);
+    static_assert(RR <= 16, "too many MFMA rows");
+    extern __shared__ uint8_t lds8[];
+    const int W = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, q = lane >> 4;
+    const int groups = K / kGS;
+    const int gw = W * GPW;
+    const int windows = (groups + gw - 1) / gw;
+    int strip = blockIdx.x;
+    if (swz) {  // strips 2j, 2j+1 (sharing 128-byte lines) on the same XCD
+        const int qq = blockIdx.x >> 3, x = blockIdx.x & 7;
+        strip = (((qq >> 1) << 3) + x) * 2 + (qq & 1);
+    }
+    const int n0 = strip * 16 * CPL + CPL * c;
+    constexpr int WB = f4_window_bytes(RR, GPW);
+    const int nbuf = windows > 1 ? 2 : 1;
+    uint8_t *wlds = lds8 + (size_t)wave * nbuf * WB;
+    const int rho = c & (RR - 1);  // A row (piece row) this lane feeds; rows >= RR are don't-care
+
+    F4Stage<MR, GPW, BF16> st;
+    st.load(A, M, K, groups, wave * GPW, lane);
+    int after = f4_loads_after_barrier();
+    F4Slab<CPL, GPW> cur;
+    cur.load(B + after, S + after, N, groups, wave * GPW, q, n0);
+    F4EpiIn<MR, CPL, BF16> ein;  // behind the weights: waited for only at the epilogue
+    ein.load(Other, Bias, postop, out_f32, M, N, q, n0, wave == 0);
+    st.store(wlds, lane);
+
+    constexpr int ROWS = P;  // live result rows of lane q: the pieces of row m = q
+    float acc[CPL][ROWS];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) acc[j][i] = 0.0f;
+
+    for (int win = 0; win < windows; ++win) {
+        asm volatile("" ::: "memory");  // staging writes precede the reads (in-order LDS per wave)
+        const uint8_t *buf = wlds + (size_t)(win & 1) * WB;
+        const bool more = win + 1 < windows;
+        F4Slab<CPL, GPW> nxt;
+        if (more) {
+            st.load(A, M, K, groups, (win + 1) * gw + wave * GPW, lane);
+            after = f4_loads_after_barrier();
+            nxt.load(B + after, S + after, N, groups, (win + 1) * gw + wave * GPW, q, n0);
+        }
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            const int g = win * gw + wave * GPW + gi;
+            if (g >= groups) break;  // uniform across the wave
+            const uint8_t *row = buf + (gi * RR + rho) * 128 + 32 * q;
+            const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
+            const int sa = buf[GPW * RR * 128 + (gi * RR + rho) * 4 + q];
+            const v8i_t av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                              (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                uint32_t d0, d1, e0, e1;
+                f4_decode(cur.w[gi][0].v[j], d0, d1);
+                f4_decode(cur.w[gi][1].v[j], e0, e1);
+                const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
+                const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa, 0, 127);
+                const float s = dt2f<BF16>(cur.scale(gi, j));
+#pragma unroll
+                for (int i = 0; i < ROWS; ++i) acc[j][i] = d[i] * s + acc[j][i];
+            }
+        }
+        if (more) {
+            asm volatile("" ::: "memory");
+            uint8_t *nb = wlds + (size_t)((win + 1) & 1) * WB;
+            st.store(nb, lane);
+            cur = nxt;
+        }
+    }
+
+    // ---- pieces -> outputs (2x: the fp4 operand held v / 2), then waves ----
+    // lane q holds rows 4q .. 4q + P - 1: the pieces of output row m = q
+    constexpr int OPL = F4EpiIn<MR, CPL, BF16>::OPL, QV = MR;
+    float out[CPL][OPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        float t = acc[j][0];
+#pragma unroll
+        for (int i = 1; i < P; ++i) t += acc[j][i];
+        out[j][0] = t * 2.0f;
+    }
+    const bool live = q < QV;
+    if (W > 1) {
+        float *red = (float *)(lds8 + (size_t)nbuf * W * WB);  // [W-1][CPL][QV*16][OPL]
+        constexpr int JS = QV * 16 * OPL;
+        if (wave != 0 && live) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int h = 0; h < OPL; ++h) red[((wave - 1) * CPL + j) * JS + (q * 16 + c) * OPL + h] = out[j][h];
+        }
+        __syncthreads();
+        if (wave != 0 || !live) return;
+        for (int w2 = 1; w2 < W; ++w2)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int h = 0; h < OPL; ++h) out[j][h] += red[((w2 - 1) * CPL + j) * JS + (q * 16 + c) * OPL + h];
+    }
+    if (!live) return;
+#pragma unroll
+    for (int h = 0; h < OPL; ++h) {
+        const int m = q + h;
+        if (m >= M) break;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const float r = epi_apply(out[j][h], postop, ein.other(h, j), ein.bias(j, out_f32));
+            const size_t oi = (size_t)m * N + n0 + j;
+            if (out_f32) ((float *)C)[oi] = r;
+            else ((uint16_t *)C)[oi] = (uint16_t)f2dt<BF16>(r);
+        }
+    }
+}
+
+struct F4Plan {
+    int cpl, waves, gpw, mr;
+    size_t lds;
+};
+
+constexpr size_t kF4MaxLds = 96 * 1024;
+
+int f4_mr(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
+
+size_t f4_lds(int MR, int waves, int gpw, int cpl, int groups) {
+    const int rr = kF4RowStride * MR;
+    const int gw = waves * gpw, windows = (groups + gw - 1) / gw;
+    const size_t stage = (size_t)(windows > 1 ? 2 : 1) * waves * f4_window_bytes(rr, gpw);
+    return stage + (size_t)(waves - 1) * cpl * MR * 16 * 4;
+}
+
+// Automatic tile: 2 columns per lane (32-column strips) when that still gives
+// >= 384 workgroups, else 1; then waves x groups-per-wave (<= 4) covering K
+// with the fewest idle group slots, then the fewest windows.
+F4Plan f4_plan(bool bf16, int M, int N, int K, int waves, int cpl, int gpw) {
+    const int MR = f4_mr(M), groups = K / kGS;
+    F4Plan p;
+    p.mr = MR;
+    p.cpl = cpl > 0 ? cpl : ((N % 32 == 0 && N / 32 >= 384) ? 2 : 1);
+    int bw = 8, bg = 1;
+    long best = LONG_MIN;
+    for (int g : {1, 2, 4, 8, 16}) {
+        if (gpw > 0 && g != gpw) continue;
+        if (MR * g > 16) continue;      // staging registers: MR * GPW / 4 tasks per lane
+        if (p.cpl * g > 16) continue;   // weight registers: 2 * CPL * GPW words per lane
+        for (int w = 1; w <= 8; ++w) {
+            if (waves > 0 && w != waves) continue;
+            if (f4_lds(MR, w, g, p.cpl, groups) > kF4MaxLds) continue;
+            const int gw = w * g, windows = (groups + gw - 1) / gw;
+            const int idle = windows * gw - groups;
+            // fewest idle group slots, then fewest windows, then more waves;
+            // automatic tiles keep <= 4 groups per wave (measured best)
+            if (gpw == 0 && g > 4) continue;
+            const long score = -(long)idle * 100000 - (long)windows * 100 + w;
+            if (score > best) { best = score; bw = w; bg = g; }
+        }
+    }
+    p.waves = bw;
+    p.gpw = bg;
+    p.lds = f4_lds(MR, bw, bg, p.cpl, groups);
+    return p;
+}
+
+template <int MR, int CPL, int GPW, bool BF16>
+hipError_t f4_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
+                       const void *Other, const void *Bias, int M, int N, int K, int postop,
+                       int out_f32, hipStream_t st) {
+    if constexpr (kF4RowStride * MR > 16) {
+        return hipErrorInvalidValue;
+    } else {
+        const int strips = N / (16 * CPL);
+        const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
+        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16>), dim3(strips), dim3(64 * p.waves), p.lds,
+                           st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other,
+                           Bias, M, N, K, postop, out_f32, swz);
+        return hipGetLastError();
+    }
+}
+
+template <int MR, int CPL, bool BF16>
+hipError_t f4_launch_g(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
+                       const void *Other, const void *Bias, int M, int N, int K, int postop,
+                       int out_f32, hipStream_t st) {
+    switch (p.gpw) {
+    case 1: return f4_launch_t<MR, CPL, 1, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 2: return f4_launch_t<MR, CPL, 2, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 4: return f4_launch_t<MR, CPL, 4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 8:
+        if constexpr (MR <= 2 && CPL <= 2) return f4_launch_t<MR, CPL, 8, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        return hipErrorInvalidValue;
+    default:
+        if constexpr (MR == 1 && CPL == 1) return f4_launch_t<MR, CPL, 16, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        return hipErrorInvalidValue;
+    }
+}
+
+template <int MR, bool BF16>
+hipError_t f4_launch_c(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
+                       const void *Other, const void *Bias, int M, int N, int K, int postop,
+                       int out_f32, hipStream_t st) {
+    if (p.cpl == 4) return f4_launch_g<MR, 4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (p.cpl == 2) return f4_launch_g<MR, 2, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return f4_launch_g<MR, 1, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+}
+
+template <bool BF16>
+hipError_t f4_launch(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
+                     const void *Other, const void *Bias, int M, int N, int K, int postop,
+                     int out_f32, hipStream_t st) {
+    switch (p.mr) {
+    case 1: return f4_launch_c<1, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 2: return f4_launch_c<2, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 4: return f4_launch_c<4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    default: return f4_launch_c<4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    }
+}
+
+// Decode hook: the two fp4 dwords the kernel builds from each word,
+// D[word][0] = rows 0, 2, .., 14, D[word][1] = rows 1, 3, .., 15.
+__global__ void k_int2_f4_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, size_t words) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= words) return;
+    uint32_t d0, d1;
+    f4_decode(B[i], d0, d1);
+    D[2 * i] = d0;
+    D[2 * i + 1] = d1;
+}
+
+}  // namespace
+
+// Whether the fp8 x fp4 engine takes a call: M <= 4, A 16-byte aligned (it
+// reads A with 16-byte loads), and byte offsets into C, Other and Bias below
+// 2^31 (its buffer loads use 32-bit offsets).
+bool int2_gemv_f4_supports(int M, int N, const void *A) {
+    return M >= 1 && M <= kF4MaxM && ((uintptr_t)A & 15) == 0 && (size_t)M * N * 4 < 0x7ff00000u;
+}
+
+ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
+                                const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                int out_f32, int waves, int cpl, int gpw, hipStream_t st) {
+    const bool bf16 = dtype == TERNOCL_BF16;
+    if (M > kF4MaxM) {
+        set_error("the fp8 x fp4 GEMV takes M <= 4");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    if ((size_t)M * N * 4 >= 0x7ff00000u) {
+        set_error("the fp8 x fp4 GEMV takes M * N * 4 < 2^31 bytes of output");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    if (cpl != 0 && cpl != 1 && cpl != 2 && cpl != 4) {
+        set_error("cols_per_lane must be 0 (automatic), 1, 2 or 4");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    if (gpw != 0 && gpw != 1 && gpw != 2 && gpw != 4 && gpw != 8 && gpw != 16) {
+        set_error("groups_per_wave must be 0 (automatic), 1, 2, 4, 8 or 16");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    if (gpw * f4_mr(M) > 16 || gpw * (cpl ? cpl : 1) > 16) {
+        set_error("groups_per_wave * (M rounded up to a power of two) and groups_per_wave * "
+                  "cols_per_lane must be <= 16");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    if (waves < 0 || waves > 8) {
+        set_error("waves must be 0 (automatic) .. 8");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    if (((uintptr_t)A & 15) != 0) {
+        set_error("the fp8 x fp4 GEMV reads A with 16-byte loads: A must be 16-byte aligned");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    const F4Plan p = f4_plan(bf16, M, N, K, waves, cpl, gpw);
+    if (N % (16 * p.cpl)) {
+        set_error("N must be a multiple of 16 * cols_per_lane");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    if (p.lds > kF4MaxLds) {
+        set_error("GEMV tile needs more than 96 KiB of LDS: use fewer waves or groups per wave");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    const hipError_t e = bf16 ? f4_launch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st)
+                              : f4_launch<false>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return launch_status(e);
+}
+
+ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st) {
+    const size_t words = (size_t)(K / 16) * N;
+    const unsigned blocks = (unsigned)((words + 255) / 256);
+    hipLaunchKernelGGL(k_int2_f4_decode, dim3(blocks), dim3(256), 0, st, B, D, words);
+    return check_launch();
+}
+
+}  // namespace tcl

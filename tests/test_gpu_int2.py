@@ -24,7 +24,10 @@ SHAPES = [(1, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (2, 4096, 14336),
           (16, 4096, 4096), (13, 1024, 272), (11, 640, 48)]
 
 
-@pytest.mark.parametrize("engine", [1, 2])
+F4_MAX_M = {False: 4, True: 4}  # the fp8 x fp4 engine: 4 fp8 pieces per fp16, 3 per bf16
+
+
+@pytest.mark.parametrize("engine", [1, 2, 4])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("M,K,N", SHAPES)
 def test_gemv_parity(dev, orc, M, K, N, bf16, engine):
@@ -32,6 +35,8 @@ def test_gemv_parity(dev, orc, M, K, N, bf16, engine):
     import ternocl_amd as T
     if engine == 1 and M > 8:
         pytest.skip("the VALU GEMV takes M <= 8")
+    if engine == 4 and M > F4_MAX_M[bf16]:
+        pytest.skip("the fp8 x fp4 GEMV takes M <= 4")
     print(f"gemv parity M={M} K={K} N={N} bf16={bf16} engine={engine}", flush=True)
     A, B, S, other, bias_f = _inputs(1000 + M + K + N, M, K, N, bf16)
     dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, False, tile=T.gemv_tile(engine))
@@ -75,7 +80,9 @@ def test_gemv_reference_distribution_rule(dev, orc, bf16):
 TILES = [(1, 1, 0, 0, 4), (1, 3, 0, 0, 4), (1, 4, 0, 0, 4), (1, 1, 0, 0, 8), (1, 5, 0, 0, 8),
          (1, 8, 0, 0, 8), (1, 2, 0, 0, 16), (1, 8, 0, 0, 16), (1, 0, 0, 0, 0),
          (2, 1, 1, 1, 0), (2, 8, 1, 1, 0), (2, 4, 2, 1, 0), (2, 8, 2, 2, 0), (2, 2, 1, 4, 0),
-         (2, 8, 2, 4, 0), (2, 3, 2, 2, 0), (2, 0, 0, 0, 0), (0, 0, 0, 0, 0)]
+         (2, 8, 2, 4, 0), (2, 3, 2, 2, 0), (2, 0, 0, 0, 0), (0, 0, 0, 0, 0),
+         (4, 0, 0, 0, 0), (4, 1, 1, 1, 0), (4, 8, 1, 1, 0), (4, 4, 2, 1, 0), (4, 8, 2, 2, 0),
+         (4, 2, 1, 4, 0), (4, 8, 2, 4, 0), (4, 3, 2, 2, 0), (4, 8, 4, 2, 0), (4, 5, 1, 8, 0)]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -113,7 +120,8 @@ def test_gemv_plan_too_big_for_lds_is_rejected(dev):
 
 
 @pytest.mark.parametrize("M,tile", [(1, (1, 2, 0, 0, 16)), (8, (1, 2, 0, 0, 16)), (8, (2, 0, 0, 0, 0)),
-                                    (16, (2, 0, 0, 0, 0)), (3, (2, 2, 1, 1, 0))])
+                                    (16, (2, 0, 0, 0, 0)), (3, (2, 2, 1, 1, 0)), (1, (4, 2, 1, 16, 0)),
+                                    (4, (4, 0, 0, 0, 0)), (3, (4, 2, 2, 1, 0)), (1, (4, 8, 2, 4, 0))])
 def test_gemv_multi_window(dev, orc, M, tile):
     """K long enough for several LDS rounds / windows (double-buffered staging)."""
     import torch
@@ -175,3 +183,104 @@ def test_gemv_decode_bit_exact(dev, bf16, engine):
             vals = formats.dt_to_f32(((got[..., d] >> (16 * half)) & 0xFFFF).astype(np.uint16), bf16)
             v = (vals - (128.0 if bf16 else 1024.0)) / 2.0 ** p - 2
             assert np.array_equal(v.astype(np.int8), sv[..., row])
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemv_f4_decode_bit_exact(dev, bf16):
+    """The fp8 x fp4 engine's weight decode: per word two fp4 dwords, nibble n
+    of dword h = row 2n + h, nibble = (b1 << 3) | b0 of the code (e2m1 +0, +0.5,
+    -0.5, -0 for codes 0, 1, 3, 2), i.e. exactly v / 2."""
+    import torch
+    import ternocl_amd as T
+    K, N = 256, 64
+    g = synth.rng(14)
+    B = synth.int2_weights(g, K, N)
+    B[0, :16] = np.arange(16, dtype=np.uint32) * 0x11111111  # every code in every field
+    D = torch.empty(((K // 16) * N * 2,), dtype=torch.int32, device="cuda")
+    T.int2_gemv_decode(dev_raw(B), D, K, N, bf16, engine=T.F4)
+    torch.cuda.synchronize()
+    got = host_u32(D).reshape(K // 16, N, 2)
+    codes = (B[..., None] >> (2 * np.arange(16, dtype=np.uint32))) & 3
+    nib = ((codes >> 1) << 3) | (codes & 1)
+    e2m1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.0, -0.5, -1, -1.5, -2, -3, -4, -6])
+    sv = formats.unpack_int2(B, K).reshape(K // 16, 16, N).transpose(0, 2, 1)
+    for h in range(2):
+        want = np.zeros(got.shape[:2], np.uint64)
+        for n in range(8):
+            want |= nib[..., 2 * n + h].astype(np.uint64) << np.uint64(4 * n)
+            vals = e2m1[(got[..., h] >> (4 * n)) & 15]
+            valid = codes[..., 2 * n + h] != 2
+            assert np.array_equal((2 * vals)[valid], sv[..., 2 * n + h][valid].astype(np.float64))
+        assert np.array_equal(got[..., h], want.astype(np.uint32)), f"dword {h}"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 1024), (2, 1024, 272), (4, 2048, 512)])
+def test_gemv_f4_pieces_exact(dev, orc, M, K, N, bf16):
+    """The fp8 pieces sum to each activation exactly, so the fp32 result agrees
+    with the fp32 host gold to accumulation-order rounding (far inside the
+    1e-2 rule: a dropped piece would show as ~3% errors)."""
+    import torch
+    import ternocl_amd as T
+    if M > F4_MAX_M[bf16]:
+        pytest.skip("M too large for the engine")
+    A, B, S, other, bias_f = _inputs(31 + M, M, K, N, bf16)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, True, tile=T.gemv_tile(T.F4))
+    _, acc = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, True)
+    got = host_f32(dC).astype(np.float64)
+    # |error| against the sum of |terms| the accumulation rounds over
+    l1 = np.abs(formats.dt_to_f32(A, bf16)).astype(np.float64) @ (
+        np.abs(formats.unpack_int2(B, K)).astype(np.float64) *
+        np.repeat(formats.dt_to_f32(S, bf16).astype(np.float64), 128, axis=0))
+    err = np.abs(got - acc.astype(np.float64))
+    assert (err <= 4e-6 * l1 + 1e-7).all(), f"max err/l1 {float((err / (l1 + 1e-30)).max()):.3g}"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemv_f4_outlier_channels(dev, orc, bf16):
+    """LLM-like activations: N(0,1) with outlier channels 300x larger.  The
+    flush rule keeps every piece row of a block inside the MFMA's exact adding
+    window, so the result stays at fp32-accumulation accuracy (the oracle is
+    itself within ~1e-5 of the exact sum here)."""
+    import torch
+    import ternocl_amd as T
+    M, K, N = 1, 4096, 512
+    g = synth.rng(77)
+    a = g.standard_normal((M, K)).astype(np.float32)
+    a[0, 5::61] *= 300.0
+    A = formats.f32_to_dt(a, bf16)
+    B = synth.int2_weights(g, K, N)
+    S = synth.scales(g, K, N, bf16)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = np.zeros(N, np.float32)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, True, tile=T.gemv_tile(T.F4))
+    _, acc = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, True)
+    d = np.abs(host_f32(dC).astype(np.float64) - acc)
+    assert d.max() < 1e-4, f"max |d| {d.max():.3g}"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemv_f4_wide_dynamic_range(dev, orc, bf16):
+    """Activations spanning many binades inside one 32-block (outliers, tiny
+    values, zeros of both signs, fp16 subnormals): the per-piece block scales
+    still give the gold within the north-star rule."""
+    import torch
+    import ternocl_amd as T
+    M, K, N = 1, 4096, 512
+    g = synth.rng(77)
+    a = g.standard_normal((M, K)).astype(np.float32)
+    a *= np.exp2(g.integers(-14, 9 if bf16 else 5, (M, K))).astype(np.float32)  # 2^-14 .. 2^8 (fp16 2^4)
+    a[0, ::97] = 0.0
+    a[0, 1::97] = -0.0
+    a[0, 5::61] *= 3000.0 if bf16 else 100.0                        # outliers
+    if not bf16:
+        a[0, 7::53] = 3e-6                                            # fp16 subnormals
+    A = formats.f32_to_dt(a, bf16)
+    B = synth.int2_weights(g, K, N)
+    S = synth.scales(g, K, N, bf16)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = np.zeros(N, np.float32)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, True, tile=T.gemv_tile(T.F4))
+    _, acc = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, True)
+    bad, dmax = allclose_report(host_f32(dC), acc)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
