@@ -9,27 +9,32 @@
 // the VALU work done per weight while the stream arrives.  This engine keeps
 // that work small on both operands:
 //
-// * Weights become fp4 (e2m1) MFMA operands with six bit operations per 16
-//   weights: a code's two bits (b1 b0) go to bits 3 and 0 of a nibble, which
-//   is +0, +0.5, -0.5 (and -0 for the unused code 2) for codes 0, 1, 3, i.e.
-//   exactly v / 2.  A word's even rows fill one dword, its odd rows another.
+// * Weights become fp4 (e2m1) MFMA operands with three bit operations per 16
+//   weights: a code's two bits (b1 b0) land on bits 3 and 2 of a nibble, the
+//   e2m1 sign and upper exponent bit, so codes 0, 1, 3 read as +0, +2.0, -2.0
+//   (the unused code 2 as -0), i.e. exactly 2v: a word's even rows are
+//   (w << 2) & 0xCCCCCCCC, its odd rows w & 0xCCCCCCCC.
 // * Activations become fp8 (e4m3) "pieces" that sum to the activation:
 //   piece p = rne_e4m3(r_p / s_p), r_0 = a, r_{p+1} = r_p - piece_p * s_p, with
-//   a power-of-two scale s_p per piece and per 32-activation block taken from
-//   the block's largest |r_p| (the MFMA's E8M0 block scales: that largest
-//   value lands in [128, 256)).  Each piece of each activation row is its own
-//   MFMA row, so one v_mfma_scale_f32_16x16x128_f8f6f4 computes
-//   sum piece * v / 2 for all pieces and rows of a 128-row scale group over
-//   16 columns.
+//   a power-of-two scale s_p per 32-activation block taken from the block's
+//   largest |r_p| (which lands in [128, 256)); the last piece uses the
+//   previous scale / 16 instead, enough for every residual (at most half an
+//   ulp of a 4-bit value, |r / s_prev| <= 8).  The scales are the MFMA's E8M0
+//   block scales.  Each piece of each activation row is its own MFMA row, so
+//   one v_mfma_scale_f32_16x16x128_f8f6f4 computes sum piece * 2v for all
+//   pieces and rows of a 128-row scale group over 16 columns.
 // * Exactness.  The products are exact, but the MFMA adds the products of a
 //   32-block with about 12 bits below the block's largest product (measured
 //   on gfx950: a product 2^13 below the largest one loses its low bits).  So
-//   every piece but the last leaves values below s_p / 2 (more than 2^8 below
-//   the block's largest) to the next piece: a piece row's block then spans at
-//   most 12 bits (4-bit significands from 2^8 down to 2^-1, in units of s_p)
-//   and adds exactly.  bf16 takes 3 pieces, fp16 4 (rows 4m..4m+3 of the
-//   MFMA); a bf16 / fp16 activation within 2^12 of its block's largest is
-//   represented exactly, smaller ones to about 2^-20 of that largest value.
+//   every piece but the last leaves values below s_p / 2 to the next piece: a
+//   piece row's block then spans at most 12 bits (4-bit significands from
+//   2^8 down to 2^-1, in units of s_p) and adds exactly.  bf16 takes 3
+//   pieces, fp16 4 (rows 4m..4m+3 of the MFMA); an activation within about
+//   2^14 of its block's largest is represented exactly, smaller ones to about
+//   2^-20 of that largest value.
+// * Per group and column the VALU then does one FMA per piece row
+//   (acc += d * S[g,n]); the factor 1/2 is applied once at the end.
+//
 // Operand layout of the 16x16x128 MFMA (lane l, r = l % 16, q = l / 16),
 // measured on gfx950: A (8 dwords of fp8) byte s of lane (r, q) is k = 16q + s
 // for s < 16 and 64 + 16q + (s - 16) otherwise; B (4 dwords of fp4) nibble s
@@ -63,10 +68,10 @@ constexpr int kF4RowStride = 4;
 constexpr int kF4MaxM = 16 / kF4RowStride;
 
 // One weight word (rows 0..15 of a column) -> fp4 dwords: d0 nibble n = row 2n,
-// d1 nibble n = row 2n + 1; nibble = (b1 << 3) | b0 of the row's code.
+// d1 nibble n = row 2n + 1; nibble = (b1 << 3) | (b0 << 2) of the row's code.
 __device__ __forceinline__ void f4_decode(uint32_t w, uint32_t &d0, uint32_t &d1) {
-    d0 = ((w << 2) & 0x88888888u) | (w & 0x11111111u);
-    d1 = (w & 0x88888888u) | ((w >> 2) & 0x11111111u);
+    d0 = (w << 2) & 0xCCCCCCCCu;
+    d1 = w & 0xCCCCCCCCu;
 }
 
 // E8M0 exponent (biased, 2..254) of the scale that maps a block whose
@@ -152,16 +157,24 @@ template <int MR, int GPW, bool BF16> struct F4Stage {
             for (int i = 0; i < 8; ++i) r[i] = f[i];
             const int row0 = (gl * RR + RS * m) * 128 + f4_byte_off(u);
             const int srow0 = GPW * RR * 128 + (gl * RR + RS * m) * 4 + (u >> 2);
+            uint32_t se = 0;
 #pragma unroll
             for (int p = 0; p < P; ++p) {
-                float mx = 0.0f;
+                // piece p's block scale: 2^(e - 134) for the block's largest
+                // |r_p|; the last piece takes the previous scale / 16, which
+                // bounds its residuals (|r| <= 8 s_prev) without a reduction
+                if (p + 1 < P) {
+                    float mx = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(r[i]));
-                const uint32_t se = f4_scale_exp(quad_max(__float_as_uint(mx)));
+                    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(r[i]));
+                    se = f4_scale_exp(quad_max(__float_as_uint(mx)));
+                } else {
+                    se = se > 5 ? se - 4 : 1;
+                }
                 const float s = __uint_as_float(se << 23);
                 float x[8];
                 if (p + 1 < P) {  // values below s / 2 go to the next piece
-                    const float thr = __uint_as_float((se - 1) << 23);
+                    const float thr = 0.5f * s;
 #pragma unroll
                     for (int i = 0; i < 8; ++i) x[i] = fabsf(r[i]) < thr ? 0.0f : r[i];
                 } else {
@@ -367,7 +380,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         }
     }
 
-    // ---- pieces -> outputs (2x: the fp4 operand held v / 2), then waves ----
+    // ---- pieces -> outputs (x 1/2: the fp4 operand held 2v), then waves ----
     // lane q holds rows 4q .. 4q + P - 1: the pieces of output row m = q
     constexpr int OPL = F4EpiIn<MR, CPL, BF16>::OPL, QV = MR;
     float out[CPL][OPL];
@@ -376,7 +389,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         float t = acc[j][0];
 #pragma unroll
         for (int i = 1; i < P; ++i) t += acc[j][i];
-        out[j][0] = t * 2.0f;
+        out[j][0] = t * 0.5f;
     }
     const bool live = q < QV;
     if (W > 1) {
@@ -514,7 +527,7 @@ hipError_t f4_launch(const F4Plan &p, const void *A, const uint32_t *B, const vo
 }
 
 // Decode hook: the two fp4 dwords the kernel builds from each word,
-// D[word][0] = rows 0, 2, .., 14, D[word][1] = rows 1, 3, .., 15.
+// D[word][0] = rows 0, 2, .., 14, D[word][1] = rows 1, 3, .., 15 (e2m1 2v).
 __global__ void k_int2_f4_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, size_t words) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= words) return;

@@ -188,8 +188,8 @@ def test_gemv_decode_bit_exact(dev, bf16, engine):
 @pytest.mark.parametrize("bf16", [False, True])
 def test_gemv_f4_decode_bit_exact(dev, bf16):
     """The fp8 x fp4 engine's weight decode: per word two fp4 dwords, nibble n
-    of dword h = row 2n + h, nibble = (b1 << 3) | b0 of the code (e2m1 +0, +0.5,
-    -0.5, -0 for codes 0, 1, 3, 2), i.e. exactly v / 2."""
+    of dword h = row 2n + h, nibble = (b1 << 3) | (b0 << 2) of the code (e2m1
+    +0, +2, -2, -0 for codes 0, 1, 3, 2), i.e. exactly 2v."""
     import torch
     import ternocl_amd as T
     K, N = 256, 64
@@ -201,7 +201,7 @@ def test_gemv_f4_decode_bit_exact(dev, bf16):
     torch.cuda.synchronize()
     got = host_u32(D).reshape(K // 16, N, 2)
     codes = (B[..., None] >> (2 * np.arange(16, dtype=np.uint32))) & 3
-    nib = ((codes >> 1) << 3) | (codes & 1)
+    nib = ((codes >> 1) << 3) | ((codes & 1) << 2)
     e2m1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.0, -0.5, -1, -1.5, -2, -3, -4, -6])
     sv = formats.unpack_int2(B, K).reshape(K // 16, 16, N).transpose(0, 2, 1)
     for h in range(2):
@@ -210,7 +210,7 @@ def test_gemv_f4_decode_bit_exact(dev, bf16):
             want |= nib[..., 2 * n + h].astype(np.uint64) << np.uint64(4 * n)
             vals = e2m1[(got[..., h] >> (4 * n)) & 15]
             valid = codes[..., 2 * n + h] != 2
-            assert np.array_equal((2 * vals)[valid], sv[..., 2 * n + h][valid].astype(np.float64))
+            assert np.array_equal((vals / 2)[valid], sv[..., 2 * n + h][valid].astype(np.float64))
         assert np.array_equal(got[..., h], want.astype(np.uint32)), f"dword {h}"
 
 
