@@ -298,8 +298,12 @@ __device__ __forceinline__ int f4_loads_after_barrier() {
     return zero;
 }
 
+// Waves per workgroup at most: 16 for one row and 16-column strips (the
+// long-K shapes, whose activation staging is the bulk of the VALU work), else 8.
+__host__ __device__ constexpr int f4_max_waves(int mr, int cpl) { return mr == 1 && cpl == 1 ? 16 : 8; }
+
 template <int MR, int CPL, int GPW, bool BF16>
-__global__ void __launch_bounds__(512)
+__global__ void __launch_bounds__(64 * f4_max_waves(MR, CPL))
 k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ S, void *__restrict__ C,
                const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
@@ -454,7 +458,10 @@ F4Plan f4_plan(bool bf16, int M, int N, int K, int waves, int cpl, int gpw) {
         if (gpw > 0 && g != gpw) continue;
         if (MR * g > 16) continue;      // staging registers: MR * GPW / 4 tasks per lane
         if (p.cpl * g > 16) continue;   // weight registers: 2 * CPL * GPW words per lane
-        for (int w = 1; w <= 8; ++w) {
+        // more than 8 waves only pays for long K (measured: K = 14336 gains,
+        // K = 4096 loses)
+        const int wmax = (waves > 0 || groups > 64) ? f4_max_waves(MR, p.cpl) : 8;
+        for (int w = 1; w <= wmax; ++w) {
             if (waves > 0 && w != waves) continue;
             if (f4_lds(MR, w, g, p.cpl, groups) > kF4MaxLds) continue;
             const int gw = w * g, windows = (groups + gw - 1) / gw;
@@ -571,8 +578,8 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
                   "cols_per_lane must be <= 16");
         return TERNOCL_ERR_INVALID_ARG;
     }
-    if (waves < 0 || waves > 8) {
-        set_error("waves must be 0 (automatic) .. 8");
+    if (waves < 0 || waves > 16) {
+        set_error("waves must be 0 (automatic) .. 16");
         return TERNOCL_ERR_INVALID_ARG;
     }
     if (((uintptr_t)A & 15) != 0) {
@@ -580,6 +587,10 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
         return TERNOCL_ERR_INVALID_ARG;
     }
     const F4Plan p = f4_plan(bf16, M, N, K, waves, cpl, gpw);
+    if (p.waves > f4_max_waves(p.mr, p.cpl)) {
+        set_error("more than 8 waves per workgroup only for M = 1 with 16-column strips (cols_per_lane 1)");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
     if (N % (16 * p.cpl)) {
         set_error("N must be a multiple of 16 * cols_per_lane");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;

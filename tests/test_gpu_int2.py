@@ -82,7 +82,8 @@ TILES = [(1, 1, 0, 0, 4), (1, 3, 0, 0, 4), (1, 4, 0, 0, 4), (1, 1, 0, 0, 8), (1,
          (2, 1, 1, 1, 0), (2, 8, 1, 1, 0), (2, 4, 2, 1, 0), (2, 8, 2, 2, 0), (2, 2, 1, 4, 0),
          (2, 8, 2, 4, 0), (2, 3, 2, 2, 0), (2, 0, 0, 0, 0), (0, 0, 0, 0, 0),
          (4, 0, 0, 0, 0), (4, 1, 1, 1, 0), (4, 8, 1, 1, 0), (4, 4, 2, 1, 0), (4, 8, 2, 2, 0),
-         (4, 2, 1, 4, 0), (4, 8, 2, 4, 0), (4, 3, 2, 2, 0), (4, 8, 4, 2, 0), (4, 5, 1, 8, 0)]
+         (4, 2, 1, 4, 0), (4, 8, 2, 4, 0), (4, 3, 2, 2, 0), (4, 8, 4, 2, 0), (4, 5, 1, 8, 0),
+         (4, 14, 1, 2, 0), (4, 16, 1, 1, 0)]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -121,7 +122,8 @@ def test_gemv_plan_too_big_for_lds_is_rejected(dev):
 
 @pytest.mark.parametrize("M,tile", [(1, (1, 2, 0, 0, 16)), (8, (1, 2, 0, 0, 16)), (8, (2, 0, 0, 0, 0)),
                                     (16, (2, 0, 0, 0, 0)), (3, (2, 2, 1, 1, 0)), (1, (4, 2, 1, 16, 0)),
-                                    (4, (4, 0, 0, 0, 0)), (3, (4, 2, 2, 1, 0)), (1, (4, 8, 2, 4, 0))])
+                                    (4, (4, 0, 0, 0, 0)), (3, (4, 2, 2, 1, 0)), (1, (4, 8, 2, 4, 0)),
+                                    (1, (4, 14, 1, 4, 0)), (1, (4, 0, 0, 0, 0))])
 def test_gemv_multi_window(dev, orc, M, tile):
     """K long enough for several LDS rounds / windows (double-buffered staging)."""
     import torch
