@@ -16,22 +16,23 @@
 //   (w << 2) & 0xCCCCCCCC, its odd rows w & 0xCCCCCCCC.
 // * Activations become fp8 (e4m3) "pieces" that sum to the activation:
 //   piece p = rne_e4m3(r_p / s_p), r_0 = a, r_{p+1} = r_p - piece_p * s_p, with
-//   a power-of-two scale s_p per 32-activation block taken from the block's
-//   largest |r_p| (which lands in [128, 256)); the last piece uses the
-//   previous scale / 16 instead, enough for every residual (at most half an
-//   ulp of a 4-bit value, |r / s_prev| <= 8).  The scales are the MFMA's E8M0
-//   block scales.  Each piece of each activation row is its own MFMA row, so
-//   one v_mfma_scale_f32_16x16x128_f8f6f4 computes sum piece * 2v for all
-//   pieces and rows of a 128-row scale group over 16 columns.
+//   a power-of-two scale s_p per 32-activation block that puts the block's
+//   largest |r_p| in [1, 2); the last piece uses the previous scale / 16,
+//   enough for every residual (at most half an ulp of a 4-bit value below 2,
+//   |r / s_prev| <= 1/16).  The scales are the MFMA's E8M0 block scales.  Each
+//   piece of each activation row is its own MFMA row, so one
+//   v_mfma_scale_f32_16x16x128_f8f6f4 computes sum piece * 2v for all pieces
+//   and rows of a 128-row scale group over 16 columns.
 // * Exactness.  The products are exact, but the MFMA adds the products of a
 //   32-block with about 12 bits below the block's largest product (measured
-//   on gfx950: a product 2^13 below the largest one loses its low bits).  So
-//   every piece but the last leaves values below s_p / 2 to the next piece: a
-//   piece row's block then spans at most 12 bits (4-bit significands from
-//   2^8 down to 2^-1, in units of s_p) and adds exactly.  bf16 takes 3
-//   pieces, fp16 4 (rows 4m..4m+3 of the MFMA); an activation within about
-//   2^14 of its block's largest is represented exactly, smaller ones to about
-//   2^-20 of that largest value.
+//   on gfx950: next to a product of 128, products with bits below 2^-5 lose
+//   them).  With the block's largest value in [1, 2), a piece holds 4-bit
+//   values down to 2^-6 and e4m3 subnormals (multiples of 2^-9) below, and
+//   values under 2^-10 round to 0 and stay whole in the residual: a piece
+//   row's block spans at most 11 bits (products below 4 with bits down to
+//   2^-8) and adds exactly.  bf16 takes 3 pieces, fp16 4 (rows 4m..4m+3 of
+//   the MFMA); an activation within about 2^10 of its block's largest is
+//   represented exactly, smaller ones to about 2^-16 of that largest value.
 // * Per group and column the VALU then does one FMA per piece row
 //   (acc += d * S[g,n]); the factor 1/2 is applied once at the end.
 //
@@ -74,12 +75,11 @@ __device__ __forceinline__ void f4_decode(uint32_t w, uint32_t &d0, uint32_t &d1
     d1 = w & 0xCCCCCCCCu;
 }
 
-// E8M0 exponent (biased, 2..254) of the scale that maps a block whose
-// largest magnitude has fp32 biased exponent e into [128, 256): 2^(e - 134)
-// (at least 2^-125, so that half of it is still a normal fp32 number).
+// E8M0 exponent (biased, 1..254) of the scale that maps a block whose
+// largest magnitude has fp32 biased exponent e into [1, 2): 2^(e - 127).
 __device__ __forceinline__ uint32_t f4_scale_exp(uint32_t maxbits) {
-    const int e = (int)(maxbits >> 23) - 7;
-    return (uint32_t)(e < 2 ? 2 : (e > 254 ? 254 : e));
+    const int e = (int)(maxbits >> 23);
+    return (uint32_t)(e < 1 ? 1 : (e > 254 ? 254 : e));
 }
 
 // max over the 4 lanes of a quad (lanes 4b .. 4b + 3: one 32-activation block)
@@ -160,9 +160,9 @@ template <int MR, int GPW, bool BF16> struct F4Stage {
             uint32_t se = 0;
 #pragma unroll
             for (int p = 0; p < P; ++p) {
-                // piece p's block scale: 2^(e - 134) for the block's largest
+                // piece p's block scale: 2^(e - 127) for the block's largest
                 // |r_p|; the last piece takes the previous scale / 16, which
-                // bounds its residuals (|r| <= 8 s_prev) without a reduction
+                // bounds its residuals (|r| <= s_prev / 16) without a reduction
                 if (p + 1 < P) {
                     float mx = 0.0f;
 #pragma unroll
@@ -172,15 +172,7 @@ template <int MR, int GPW, bool BF16> struct F4Stage {
                     se = se > 5 ? se - 4 : 1;
                 }
                 const float s = __uint_as_float(se << 23);
-                float x[8];
-                if (p + 1 < P) {  // values below s / 2 go to the next piece
-                    const float thr = 0.5f * s;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) x[i] = fabsf(r[i]) < thr ? 0.0f : r[i];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) x[i] = r[i];
-                }
+                const float *x = r;
                 const uint32_t ev = f8x4(x[0], x[2], x[4], x[6], s);
                 const uint32_t od = f8x4(x[1], x[3], x[5], x[7], s);
                 if (live) {
