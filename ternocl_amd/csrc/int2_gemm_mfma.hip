@@ -40,18 +40,25 @@ constexpr int BK = 64;           // K per LDS stage
 constexpr int A_PITCH = BK + 8;  // DT elements per LDS row (16 bytes of padding)
 constexpr int kMoeTileRows = 128;  // MoE row tiles (experts hold a few hundred rows each)
 
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x16_{f16,bf16}: on gfx950 twice the throughput of the
+// 16x16x32 shape (measured: 2.05 vs 1.15 PFLOP/s in a pure MFMA loop).  Lane
+// (c, q) = (l % 32, l / 32) holds 8 k values of A row c / B column c, slot s of
+// A pairing with slot s of B; result element i is row 8(i/4) + 4q + i%4,
+// column c.
 template <bool BF16>
-__device__ __forceinline__ f32x4_t mfma16(const uint32_t a[4], const uint32_t b[4], f32x4_t c) {
+__device__ __forceinline__ f32x16_t mfma32(const uint32_t a[4], const uint32_t b[4], f32x16_t c) {
     if constexpr (BF16) {
         bf168_t x, y;
         __builtin_memcpy(&x, a, 16);
         __builtin_memcpy(&y, b, 16);
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, c, 0, 0, 0);
     } else {
         half8_t x, y;
         __builtin_memcpy(&x, a, 16);
         __builtin_memcpy(&y, b, 16);
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, c, 0, 0, 0);
     }
 }
 
@@ -120,19 +127,20 @@ struct ARows {
     }
 };
 
-constexpr int kEpPitch = 20;  // epilogue floats per row: 16 + 4 (16-byte aligned rows)
+constexpr int kEpPitch = 36;  // epilogue floats per row: 32 + 4 (16-byte aligned rows)
 
-// Tile shape: WVM x WVN waves, each owning NMB x NCB blocks of 16 x 16 outputs.
+// Tile shape: WVM x WVN waves, each owning NMB x NCB blocks of 16 x 16 outputs
+// (NMB, NCB even: the MFMAs are 32 x 32).
 template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
     static constexpr int NMB = NMB_, NCB = NCB_, WVM = WVM_, WVN = WVN_;
     static constexpr int THREADS = 64 * WVM * WVN;
     static constexpr int BM = 16 * NMB * WVM, BN = 16 * NCB * WVN;
     static constexpr int ACH = BM * 4 / THREADS;  // 16-element A chunks per thread per stage
     static_assert(BM * 4 % THREADS == 0, "A chunks must divide evenly");
-    // LDS (DT elements): two A stages while K runs, then the epilogue's
-    // per-wave [16 NMB][kEpPitch] fp32 blocks
-    static constexpr size_t stage_elems = 2 * (size_t)BM * A_PITCH;
-    static constexpr size_t epi_elems = (size_t)(THREADS / 64) * 16 * NMB * kEpPitch * 2;
+    // LDS (DT elements): three A stages while K runs, then the epilogue's
+    // per-wave [8 NMB][kEpPitch] fp32 blocks
+    static constexpr size_t stage_elems = 3 * (size_t)BM * A_PITCH;
+    static constexpr size_t epi_elems = (size_t)(THREADS / 64) * 8 * NMB * kEpPitch * 2;
     static constexpr size_t lds_elems = stage_elems > epi_elems ? stage_elems : epi_elems;
 };
 
@@ -151,7 +159,6 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
                                           const uint16_t *__restrict__ S2 = nullptr) {
     constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c16 = lane & 15, q = lane >> 4, h = q & 1;
     const int wm = (wave / Cfg::WVN) * 16 * NMB, wn = (wave % Cfg::WVN) * 16 * NCB;
     const int stages = K / BK;
 
@@ -169,23 +176,25 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         const int id = tid + TH * u, r = id >> 2;
         va[u] = ar.rowoff(r < mrows ? r : mrows - 1, K) + 32u * (id & 3);
     }
-    uint4 av[Cfg::ACH][2];
-    auto a_load = [&](int st) {
+    // two register sets: stage t's A chunks live in av[t & 1] from their load,
+    // issued two stages ahead, to their LDS store in the middle of stage t - 1
+    uint4 av[2][Cfg::ACH][2];
+    auto a_load = [&](int st, int set) __attribute__((always_inline)) {
         const int sc = (st < stages ? st : stages - 1) * BK * 2;  // bytes, uniform
 #pragma unroll
         for (int u = 0; u < Cfg::ACH; ++u)
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u] + 16 * e, sc, 0);
-                av[u][e] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
+                av[set][u][e] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
             }
     };
-    auto a_store = [&](uint16_t *buf) {
+    auto a_store = [&](uint16_t *buf, int set) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < Cfg::ACH; ++u) {
             const int id = tid + TH * u;
-            const uint32_t v[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
-                                   av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
+            const uint32_t v[8] = {av[set][u][0].x, av[set][u][0].y, av[set][u][0].z, av[set][u][0].w,
+                                   av[set][u][1].x, av[set][u][1].y, av[set][u][1].z, av[set][u][1].w};
             uint32_t o[8];
             chunk_interleave(v, o);
             uint4 *d = (uint4 *)(buf + (size_t)(id >> 2) * A_PITCH + 16 * (id & 3));
@@ -194,164 +203,203 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         }
     };
 
-    // B words of this wave for stage st: block cb, k-step ks -> word
-    // kp = 4 st + 2 ks + q / 2 of column n0 + wn + 16 cb + c16, half q % 2.
-    // vb[ks] advances one stage per load; a 16-column block past N (when
-    // N % BN != 0) reads the next row's words -- in range, feeding outputs
-    // that are not stored -- or, past the last row, 0.
+    // B words of this wave for stage st: 32-column block cb, 16-row k-step ks ->
+    // word kp = 4 st + ks of column n0 + wn + 32 cb + c32 (lanes q = 0, 1 read
+    // the same word and decode its halves q).  vb advances one stage per load;
+    // a 32-column block past N (when N % BN != 0) reads the next row's words --
+    // in range, feeding outputs that are not stored -- or, past the last row, 0.
+    static_assert(NMB % 2 == 0 && NCB % 2 == 0, "32 x 32 MFMA blocks");
+    constexpr int MB2 = NMB / 2, CB2 = NCB / 2;
+    const int c32 = lane & 31, q32 = lane >> 5;
     const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
     const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
     // (DUAL: the gate weights, same shape, same offsets)
     const __amdgpu_buffer_rsrc_t rB2 = buf_rsrc(DUAL ? B2 + n0 : B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
     const __amdgpu_buffer_rsrc_t rS2 = buf_rsrc(DUAL ? S2 + n0 : S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
-    uint32_t vb[2];
-    vb[0] = (uint32_t)(((q >> 1) * N + wn + c16) * 4);
-    vb[1] = vb[0] + (uint32_t)(8 * N);
-    const uint32_t vs0 = (uint32_t)((wn + c16) * 2);
+    uint32_t vb = (uint32_t)((wn + c32) * 4);
+    const uint32_t vs0 = (uint32_t)((wn + c32) * 2);
     constexpr int NB = DUAL ? 2 : 1;  // weight matrices
-    uint32_t bw[NB][NCB][2], sraw[NB][NCB];
+    uint32_t bw[NB][CB2][4], sraw[NB][CB2];
     auto b_load = [&]() {
 #pragma unroll
         for (int m = 0; m < NB; ++m)
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb)
+            for (int cb = 0; cb < CB2; ++cb)
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    bw[m][cb][ks] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(m ? rB2 : rB, vb[ks] + 64 * cb, 0, 0);
-        vb[0] += (uint32_t)(16 * N);
-        vb[1] += (uint32_t)(16 * N);
+                for (int ks = 0; ks < 4; ++ks)
+                    bw[m][cb][ks] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                        m ? rB2 : rB, vb + (uint32_t)(ks * N * 4) + 128 * cb, 0, 0);
+        vb += (uint32_t)(16 * N);
     };
     auto s_load = [&](int g) {  // the scales of group g (past the last: 0)
         const uint32_t v = vs0 + (uint32_t)(g * 2 * N);
 #pragma unroll
         for (int m = 0; m < NB; ++m)
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb)
-                sraw[m][cb] = __builtin_amdgcn_raw_buffer_load_b16(m ? rS2 : rS, v + 32 * cb, 0, 0);
+            for (int cb = 0; cb < CB2; ++cb)
+                sraw[m][cb] = __builtin_amdgcn_raw_buffer_load_b16(m ? rS2 : rS, v + 64 * cb, 0, 0);
     };
 
-    f32x4_t acc[NMB][NCB], acc2[DUAL ? NMB : 1][DUAL ? NCB : 1];
+    f32x16_t acc[MB2][CB2], acc2[DUAL ? MB2 : 1][DUAL ? CB2 : 1];
 #pragma unroll
-    for (int mb = 0; mb < NMB; ++mb)
+    for (int mb = 0; mb < MB2; ++mb)
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) acc[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int cb = 0; cb < CB2; ++cb) acc[mb][cb] = f32x16_t{};
     if constexpr (DUAL) {
 #pragma unroll
-        for (int mb = 0; mb < NMB; ++mb)
+        for (int mb = 0; mb < MB2; ++mb)
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) acc2[mb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int cb = 0; cb < CB2; ++cb) acc2[mb][cb] = f32x16_t{};
     }
 
-    ScaleOp<BF16> sop[NB][NCB];
-    a_load(0);
+    ScaleOp<BF16> sop[NB][CB2];
+    a_load(0, 0);
     b_load();
     s_load(0);
-    a_store(lds);
-    for (int st = 0; st < stages; ++st) {
-        __syncthreads();  // stage st staged; stage st - 1 consumed
-        const uint16_t *abuf = lds + (size_t)(st & 1) * Cfg::BM * A_PITCH;
-        uint32_t bwc[NB][NCB][2];
+    a_load(1, 1);
+    a_store(lds, 0);
+    __syncthreads();
+    // Stage st reads LDS buffer st % 3.  B words and scales are loaded one
+    // stage ahead, A two stages ahead (register set st & 1).  Between k-steps 1
+    // and 2 a wave stores stage st + 1's A into buffer (st + 1) % 3, reads its
+    // k-step 2 fragments, and then meets the stage's one barrier: after it,
+    // every wave's store for stage st + 1 is visible, and the buffer the next
+    // stage overwrites, (st + 2) % 3, was last read in stage st - 1, before
+    // that stage's barrier.  So no wave waits at a barrier for data it needs
+    // right after it, and the MFMAs queued before the barrier keep running.
+    // K is a multiple of 128: the stage count is even and the loop runs in
+    // pairs with the register set fixed at compile time.
+    constexpr uint32_t kBuf = (uint32_t)Cfg::BM * A_PITCH;  // DT elements per buffer
+    uint32_t cur = 0;  // st % 3
+    auto stage = [&](int st, int par) __attribute__((always_inline)) {
+        const uint16_t *abuf = lds + cur * kBuf;
+        const uint32_t nxt = cur == 2 ? 0 : cur + 1;
+        uint32_t bwc[NB][CB2][4];
 #pragma unroll
         for (int m = 0; m < NB; ++m)
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) {
-                bwc[m][cb][0] = bw[m][cb][0];
-                bwc[m][cb][1] = bw[m][cb][1];
-            }
-        if ((st & 1) == 0) {  // a new 128-row scale group (uniform; no loads inside)
+            for (int cb = 0; cb < CB2; ++cb)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) bwc[m][cb][ks] = bw[m][cb][ks];
+        if (par == 0) {  // a new 128-row scale group
 #pragma unroll
             for (int m = 0; m < NB; ++m)
 #pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) sop[m][cb].set(sraw[m][cb]);
+                for (int cb = 0; cb < CB2; ++cb) sop[m][cb].set(sraw[m][cb]);
         }
-        // next stage's loads in flight during this stage's MFMAs; the scales of
-        // the group after this one are loaded on the group's second stage
-        a_load(st + 1);
+        // B and scale loads first: the next stage waits for them, not for the
+        // A loads issued after them.  The scales of the group after this one
+        // are loaded on the group's second stage.  (sched_barrier: the
+        // scheduler would otherwise sink the loads below the MFMAs, next to
+        // their consumers.)
         b_load();
         s_load((st >> 1) + 1);
+        a_load(st + 2, par);
+        __builtin_amdgcn_sched_barrier(0);
+        // A fragments of k-step ks: row wm + 32 mb + c32, elements 8 q32 ..
+        // 8 q32 + 7 of the stage's 16-element chunk ks (stored as pairs (j, j + 8))
+        auto a_frags = [&](int ks, uint32_t af[MB2][4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            uint32_t af[NMB][4];
-#pragma unroll
-            for (int mb = 0; mb < NMB; ++mb) {
-                const uint4 v = *(const uint4 *)(abuf + (size_t)(wm + 16 * mb + c16) * A_PITCH +
-                                                 (2 * ks + (q >> 1)) * 16 + 8 * h);
+            for (int mb = 0; mb < MB2; ++mb) {
+                const uint4 v = *(const uint4 *)(abuf + (size_t)(wm + 32 * mb + c32) * A_PITCH + 16 * ks + 8 * q32);
                 af[mb][0] = v.x; af[mb][1] = v.y; af[mb][2] = v.z; af[mb][3] = v.w;
             }
+        };
+        uint32_t af[MB2][4];
+        a_frags(0, af);
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) {
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks == 2) {
+                __builtin_amdgcn_sched_barrier(0);
+                a_store(lds + nxt * kBuf, par ^ 1);  // past the last stage: never read
+                a_frags(2, af);
+                __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+            } else if (ks > 0) {
+                a_frags(ks, af);
+            }
+#pragma unroll
+            for (int cb = 0; cb < CB2; ++cb) {
                 uint32_t bf[4];
-                frag(bwc[0][cb][ks], h, sop[0][cb], bf);
+                frag(bwc[0][cb][ks], q32, sop[0][cb], bf);
 #pragma unroll
-                for (int mb = 0; mb < NMB; ++mb) acc[mb][cb] = mfma16<BF16>(af[mb], bf, acc[mb][cb]);
+                for (int mb = 0; mb < MB2; ++mb) acc[mb][cb] = mfma32<BF16>(af[mb], bf, acc[mb][cb]);
                 if constexpr (DUAL) {
                     uint32_t bg[4];
-                    frag(bwc[NB - 1][cb][ks], h, sop[NB - 1][cb], bg);
+                    frag(bwc[NB - 1][cb][ks], q32, sop[NB - 1][cb], bg);
 #pragma unroll
-                    for (int mb = 0; mb < NMB; ++mb) acc2[mb][cb] = mfma16<BF16>(af[mb], bg, acc2[mb][cb]);
+                    for (int mb = 0; mb < MB2; ++mb) acc2[mb][cb] = mfma32<BF16>(af[mb], bg, acc2[mb][cb]);
                 }
             }
         }
-        a_store(lds + (size_t)((st + 1) & 1) * Cfg::BM * A_PITCH);  // after the last stage: never read
+        cur = nxt;
+    };
+    for (int st = 0; st < stages; st += 2) {
+        stage(st, 0);
+        stage(st + 1, 1);
     }
 
-    // Epilogue through LDS, one 16-column block at a time: lane (c16, q) holds
-    // rows 16mb + 4q + i of column 16cb + c16; it writes them to its wave's
-    // [16 NMB][kEpPitch] fp32 block, then reads back 4 adjacent columns of one
-    // row for epi_store4.  (Reading the accumulators only in fully unrolled
-    // loops also keeps the array in registers.)
+    // Epilogue through LDS, one 32-column block and 16-row half of each 32-row
+    // block at a time: lane (c32, q32) holds rows 32mb + 8(i/4) + 4q32 + i%4 of
+    // column 32cb + c32, so elements i in [8hf, 8hf + 8) are the rows
+    // 32mb + 16hf + [0, 16).  Every lane writes those to its wave's
+    // [8 NMB][kEpPitch] fp32 block, then reads back 4 adjacent columns of one
+    // row for epi_store4 (8 lanes cover a row's 32 columns).  The accumulators
+    // are read only in fully unrolled loops, which keeps them in registers.
     const float fix = BF16 ? 1.0f : 0.5f;  // fp16 fragments carry 2x the weight
-    float *ct = (float *)lds + (size_t)wave * 16 * NMB * kEpPitch;
+    float *ct = (float *)lds + (size_t)wave * 8 * NMB * kEpPitch;
     __syncthreads();  // the A buffers are free
+    auto put = [&](auto &a, int cb, int hf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-        const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
-        float up[DUAL ? NMB : 1][4];  // DUAL: DT(up) of this lane's 4 outputs per pass
-        if constexpr (DUAL) {
+        for (int mb = 0; mb < MB2; ++mb)
 #pragma unroll
-            for (int mb = 0; mb < NMB; ++mb) {
-                const f32x4_t v = acc[mb][cb] * fix;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * kEpPitch + c16] = v[i];
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int pass = 0; pass < NMB; ++pass) {
-                const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * kEpPitch + 4 * (lane & 3));
-                const float v4[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) up[pass][i] = dt2f<BF16>(f2dt<BF16>(v4[i]));
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);
-            __builtin_amdgcn_wave_barrier();
-        }
-#pragma unroll
-        for (int mb = 0; mb < NMB; ++mb) {
-            const f32x4_t v = (DUAL ? acc2[DUAL ? mb : 0][DUAL ? cb : 0] : acc[mb][cb]) * fix;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * kEpPitch + c16] = v[i];
-        }
+            for (int j = 0; j < 8; ++j)
+                ct[(16 * mb + 8 * (j >> 2) + 4 * q32 + (j & 3)) * kEpPitch + c32] = a[mb][cb][8 * hf + j] * fix;
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
         __builtin_amdgcn_wave_barrier();
+    };
 #pragma unroll
-        for (int pass = 0; pass < NMB; ++pass) {
-            const int r = wm + 16 * pass + (lane >> 2);
-            const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * kEpPitch + 4 * (lane & 3));
-            const float v4[4] = {t.x, t.y, t.z, t.w};
-            if (r < mrows && n < N) {
-                if constexpr (DUAL) {
-                    uint32_t o[4];
+    for (int cb = 0; cb < CB2; ++cb) {
+        const int n = n0 + wn + 32 * cb + 4 * (lane & 7);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) o[i] = f2dt<BF16>(epi_apply(v4[i], 1, up[pass][i], 0.0f));
-                    *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
-                        make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-                } else {
-                    epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, crow0 + r, n, v4);
+        for (int hf = 0; hf < 2; ++hf) {
+            float up[DUAL ? NMB : 1][4];  // DUAL: DT(up) of this lane's 4 outputs per pass
+            if constexpr (DUAL) {
+                put(acc, cb, hf);
+#pragma unroll
+                for (int pass = 0; pass < NMB; ++pass) {
+                    const float4 t = *(const float4 *)(ct + (8 * pass + (lane >> 3)) * kEpPitch + 4 * (lane & 7));
+                    const float v4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) up[pass][i] = dt2f<BF16>(f2dt<BF16>(v4[i]));
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_wave_barrier();
+                put(acc2, cb, hf);
+            } else {
+                put(acc, cb, hf);
+            }
+#pragma unroll
+            for (int pass = 0; pass < NMB; ++pass) {
+                // block row 8 pass + lane / 8 = 16 mb + j -> tile row 32 mb + 16 hf + j
+                const int br = 8 * pass + (lane >> 3);
+                const int r = wm + 32 * (br >> 4) + 16 * hf + (br & 15);
+                const float4 t = *(const float4 *)(ct + br * kEpPitch + 4 * (lane & 7));
+                const float v4[4] = {t.x, t.y, t.z, t.w};
+                if (r < mrows && n < N) {
+                    if constexpr (DUAL) {
+                        uint32_t o[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[i] = f2dt<BF16>(epi_apply(v4[i], 1, up[pass][i], 0.0f));
+                        *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
+                            make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                    } else {
+                        epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, crow0 + r, n, v4);
+                    }
                 }
             }
+            __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes
         }
-        __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
     }
 }
 
@@ -436,12 +484,12 @@ struct GemmPlan {
 // each tile shape (larger tiles decode fewer B words and read less A per MAC;
 // eight-wave tiles keep two waves per SIMD, four-wave 256 x 256 tiles one).
 GemmPlan gemm_plan(int M, int N) {
-    static const GemmPlan cands[] = {{8, 4, 2, 4}, {8, 8, 2, 2}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
-    static const double eff[] = {1.0, 0.9, 0.75, 0.7, 0.88};
-    static const int per_cu[] = {1, 1, 1, 1, 2};  // resident workgroups per CU
-    GemmPlan best = cands[4];
+    static const GemmPlan cands[] = {{8, 4, 2, 4}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
+    static const double eff[] = {1.0, 0.75, 0.7, 0.88};
+    static const int per_cu[] = {1, 1, 1, 2};  // resident workgroups per CU
+    GemmPlan best = cands[3];
     double best_t = 1e300;
-    for (int c = 0; c < 5; ++c) {
+    for (int c = 0; c < 4; ++c) {
         const int BM = 16 * cands[c].nmb * cands[c].wvm, BN = 16 * cands[c].ncb * cands[c].wvn;
         const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
         const long slots = 256L * per_cu[c];
@@ -469,7 +517,6 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
     if (p.wvn == 4) gemm_launch<TileCfg<8, 4, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.nmb == 8 && p.ncb == 8) gemm_launch<TileCfg<8, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else if (p.nmb == 8) gemm_launch<TileCfg<8, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else if (p.ncb == 8) gemm_launch<TileCfg<4, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
