@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -117,6 +118,67 @@ __device__ __forceinline__ void epi_store4(void *C, const uint16_t *Other, const
         t.x = f2dt<BF16>(r[0]) | (f2dt<BF16>(r[1]) << 16);
         t.y = f2dt<BF16>(r[2]) | (f2dt<BF16>(r[3]) << 16);
         *(uint2 *)((uint16_t *)C + i) = t;
+    }
+}
+
+// The same with the postop and output type fixed at compile time: kernels
+// with many outputs per lane dispatch once (a uniform branch) to one of these
+// instead of evaluating the postop switch per output.
+template <int P> __device__ __forceinline__ float epi_apply_c(float v, float other, float bias) {
+    if constexpr (P == 1) return v * sigmoid_ref(v) * other;
+    else if constexpr (P == 2) return v + other;
+    else if constexpr (P == 3) return v + bias;
+    else if constexpr (P == 4) return sigmoid_ref(v);
+    else if constexpr (P == 5) return (v + bias) + other;
+    else return v;
+}
+template <bool BF16, int P, bool F32>
+__device__ __forceinline__ void epi_store4_c(void *C, const uint16_t *Other, const void *Bias, int N, int m, int n,
+                                             const float v[4]) {
+    const size_t i = (size_t)m * N + n;
+    float o[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (postop_needs_other(P)) {
+        const uint2 t = *(const uint2 *)(Other + i);
+        o[0] = dt2f<BF16>(t.x & 0xffffu); o[1] = dt2f<BF16>(t.x >> 16);
+        o[2] = dt2f<BF16>(t.y & 0xffffu); o[3] = dt2f<BF16>(t.y >> 16);
+    }
+    if constexpr (postop_needs_bias(P)) {
+        if constexpr (F32) {
+            const float4 t = *(const float4 *)((const float *)Bias + n);
+            b[0] = t.x; b[1] = t.y; b[2] = t.z; b[3] = t.w;
+        } else {
+            const uint2 t = *(const uint2 *)((const uint16_t *)Bias + n);
+            b[0] = dt2f<BF16>(t.x & 0xffffu); b[1] = dt2f<BF16>(t.x >> 16);
+            b[2] = dt2f<BF16>(t.y & 0xffffu); b[3] = dt2f<BF16>(t.y >> 16);
+        }
+    }
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = epi_apply_c<P>(v[c], o[c], b[c]);
+    if constexpr (F32) {
+        *(float4 *)((float *)C + i) = make_float4(r[0], r[1], r[2], r[3]);
+    } else {
+        uint2 t;
+        t.x = f2dt<BF16>(r[0]) | (f2dt<BF16>(r[1]) << 16);
+        t.y = f2dt<BF16>(r[2]) | (f2dt<BF16>(r[3]) << 16);
+        *(uint2 *)((uint16_t *)C + i) = t;
+    }
+}
+
+// Calls f(std::integral_constant<int, P>, std::integral_constant<bool, F32>)
+// for the runtime (postop, out_f32); postop outside 0..5 acts as 0.
+template <class Fn> __device__ __forceinline__ void epi_dispatch(int postop, int out_f32, Fn &&f) {
+    auto go = [&](auto p) __attribute__((always_inline)) {
+        if (out_f32) f(p, std::integral_constant<bool, true>{});
+        else f(p, std::integral_constant<bool, false>{});
+    };
+    switch (postop) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    case 4: go(std::integral_constant<int, 4>{}); break;
+    case 5: go(std::integral_constant<int, 5>{}); break;
+    default: go(std::integral_constant<int, 0>{}); break;
     }
 }
 

@@ -358,49 +358,58 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
         __builtin_amdgcn_wave_barrier();
     };
+    // The postop and output type are fixed at compile time inside: one uniform
+    // branch here instead of a switch per output (which cost more than the
+    // rest of the epilogue together).
+    auto epilogue = [&](auto P_, auto F_) __attribute__((always_inline)) {
+        constexpr int P = decltype(P_)::value;
+        constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
-    for (int cb = 0; cb < CB2; ++cb) {
-        const int n = n0 + wn + 32 * cb + 4 * (lane & 7);
+        for (int cb = 0; cb < CB2; ++cb) {
+            const int n = n0 + wn + 32 * cb + 4 * (lane & 7);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            float up[DUAL ? NMB : 1][4];  // DUAL: DT(up) of this lane's 4 outputs per pass
-            if constexpr (DUAL) {
-                put(acc, cb, hf);
+            for (int hf = 0; hf < 2; ++hf) {
+                float up[DUAL ? NMB : 1][4];  // DUAL: DT(up) of this lane's 4 outputs per pass
+                if constexpr (DUAL) {
+                    put(acc, cb, hf);
+#pragma unroll
+                    for (int pass = 0; pass < NMB; ++pass) {
+                        const float4 t = *(const float4 *)(ct + (8 * pass + (lane >> 3)) * kEpPitch + 4 * (lane & 7));
+                        const float v4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) up[pass][i] = dt2f<BF16>(f2dt<BF16>(v4[i]));
+                    }
+                    __builtin_amdgcn_s_waitcnt(0xc07f);
+                    __builtin_amdgcn_wave_barrier();
+                    put(acc2, cb, hf);
+                } else {
+                    put(acc, cb, hf);
+                }
 #pragma unroll
                 for (int pass = 0; pass < NMB; ++pass) {
-                    const float4 t = *(const float4 *)(ct + (8 * pass + (lane >> 3)) * kEpPitch + 4 * (lane & 7));
+                    // block row 8 pass + lane / 8 = 16 mb + j -> tile row 32 mb + 16 hf + j
+                    const int br = 8 * pass + (lane >> 3);
+                    const int r = wm + 32 * (br >> 4) + 16 * hf + (br & 15);
+                    const float4 t = *(const float4 *)(ct + br * kEpPitch + 4 * (lane & 7));
                     const float v4[4] = {t.x, t.y, t.z, t.w};
+                    if (r < mrows && n < N) {
+                        if constexpr (DUAL) {
+                            uint32_t o[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) up[pass][i] = dt2f<BF16>(f2dt<BF16>(v4[i]));
-                }
-                __builtin_amdgcn_s_waitcnt(0xc07f);
-                __builtin_amdgcn_wave_barrier();
-                put(acc2, cb, hf);
-            } else {
-                put(acc, cb, hf);
-            }
-#pragma unroll
-            for (int pass = 0; pass < NMB; ++pass) {
-                // block row 8 pass + lane / 8 = 16 mb + j -> tile row 32 mb + 16 hf + j
-                const int br = 8 * pass + (lane >> 3);
-                const int r = wm + 32 * (br >> 4) + 16 * hf + (br & 15);
-                const float4 t = *(const float4 *)(ct + br * kEpPitch + 4 * (lane & 7));
-                const float v4[4] = {t.x, t.y, t.z, t.w};
-                if (r < mrows && n < N) {
-                    if constexpr (DUAL) {
-                        uint32_t o[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) o[i] = f2dt<BF16>(epi_apply(v4[i], 1, up[pass][i], 0.0f));
-                        *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
-                            make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-                    } else {
-                        epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, crow0 + r, n, v4);
+                            for (int i = 0; i < 4; ++i) o[i] = f2dt<BF16>(epi_apply_c<1>(v4[i], up[pass][i], 0.0f));
+                            *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
+                                make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                        } else {
+                            epi_store4_c<BF16, P, F32>(C, Other, Bias, N, crow0 + r, n, v4);
+                        }
                     }
                 }
+                __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes
             }
-            __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes
         }
-    }
+    };
+    if constexpr (DUAL) epilogue(std::integral_constant<int, 1>{}, std::integral_constant<bool, false>{});
+    else epi_dispatch(postop, out_f32, epilogue);
 }
 
 template <class Cfg, bool BF16>

@@ -365,23 +365,30 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
     constexpr int EP = TC::EP_PITCH;
     float *ct = (float *)lds + (size_t)wave * 16 * MB * EP;
     __syncthreads();  // the A tiles are free
+    // postop and output type fixed at compile time inside (one uniform branch
+    // instead of a switch per output)
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+        constexpr int P = decltype(P_)::value;
+        constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
+        for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+            for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * EP + c16] = acc[mb][cb][i];
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
-        __builtin_amdgcn_wave_barrier();
-        const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
-        for (int pass = 0; pass < MB; ++pass) {
-            const int r = wm + 16 * pass + (lane >> 2);
-            const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * EP + 4 * (lane & 3));
-            const float v4[4] = {t.x, t.y, t.z, t.w};
-            if (r < mrows && n < N) epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, m0 + r, n, v4);
+                for (int i = 0; i < 4; ++i) ct[(16 * mb + 4 * q + i) * EP + c16] = acc[mb][cb][i];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+            __builtin_amdgcn_wave_barrier();
+            const int n = n0 + wn + 16 * cb + 4 * (lane & 3);
+#pragma unroll
+            for (int pass = 0; pass < MB; ++pass) {
+                const int r = wm + 16 * pass + (lane >> 2);
+                const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * EP + 4 * (lane & 3));
+                const float v4[4] = {t.x, t.y, t.z, t.w};
+                if (r < mrows && n < N) epi_store4_c<BF16, P, F32>(C, Other, Bias, N, m0 + r, n, v4);
+            }
+            __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
         }
-        __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
-    }
+    });
 }
 
 // Test hook: the MFMA B fragment each word decodes to (4 dwords per word).
