@@ -259,6 +259,18 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     a_load(1, 1);
     a_store(lds, 0);
     __syncthreads();
+    // A fragments of k-step ks of the stage in LDS buffer buf: row wm + 32 mb + c32,
+    // elements 8 q32 .. 8 q32 + 7 of the stage's 16-element chunk ks (stored as
+    // pairs (j, j + 8))
+    auto a_frags = [&](const uint16_t *buf, int ks, uint32_t af[MB2][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mb = 0; mb < MB2; ++mb) {
+            const uint4 v = *(const uint4 *)(buf + (size_t)(wm + 32 * mb + c32) * A_PITCH + 16 * ks + 8 * q32);
+            af[mb][0] = v.x; af[mb][1] = v.y; af[mb][2] = v.z; af[mb][3] = v.w;
+        }
+    };
+    uint32_t af0[MB2][4];  // k-step 0 fragments of the coming stage, read a stage early
+    a_frags(lds, 0, af0);
     // Stage st reads LDS buffer st % 3.  B words and scales are loaded one
     // stage ahead, A two stages ahead (register set st & 1).  Between k-steps 1
     // and 2 a wave stores stage st + 1's A into buffer (st + 1) % 3, reads its
@@ -296,27 +308,25 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         s_load((st >> 1) + 1);
         a_load(st + 2, par);
         __builtin_amdgcn_sched_barrier(0);
-        // A fragments of k-step ks: row wm + 32 mb + c32, elements 8 q32 ..
-        // 8 q32 + 7 of the stage's 16-element chunk ks (stored as pairs (j, j + 8))
-        auto a_frags = [&](int ks, uint32_t af[MB2][4]) __attribute__((always_inline)) {
-#pragma unroll
-            for (int mb = 0; mb < MB2; ++mb) {
-                const uint4 v = *(const uint4 *)(abuf + (size_t)(wm + 32 * mb + c32) * A_PITCH + 16 * ks + 8 * q32);
-                af[mb][0] = v.x; af[mb][1] = v.y; af[mb][2] = v.z; af[mb][3] = v.w;
-            }
-        };
         uint32_t af[MB2][4];
-        a_frags(0, af);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            if (ks == 2) {
+            if (ks == 0) {
+#pragma unroll
+                for (int mb = 0; mb < MB2; ++mb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) af[mb][i] = af0[mb][i];
+            } else if (ks == 2) {
                 __builtin_amdgcn_sched_barrier(0);
                 a_store(lds + nxt * kBuf, par ^ 1);  // past the last stage: never read
-                a_frags(2, af);
+                a_frags(abuf, 2, af);
                 __syncthreads();
+                // the next stage's k-step 0 fragments (its buffer is complete
+                // now): its first MFMAs wait for no LDS read
+                a_frags(lds + nxt * kBuf, 0, af0);
                 __builtin_amdgcn_sched_barrier(0);
-            } else if (ks > 0) {
-                a_frags(ks, af);
+            } else {
+                a_frags(abuf, ks, af);
             }
 #pragma unroll
             for (int cb = 0; cb < CB2; ++cb) {
