@@ -206,9 +206,12 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
             for (int r = 0; r < MR; ++r) acc[r] += red[j][r][lane];
     }
     if (n >= N) return;
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < MR; ++r)
-        if (m0 + r < M) epi_store1<BF16>(C, Other, Bias, postop, out_f32, N, m0 + r, n, acc[r]);
+        for (int r = 0; r < MR; ++r)
+            if (m0 + r < M)
+                epi_store1_c<BF16, decltype(P_)::value, decltype(F_)::value>(C, Other, Bias, N, m0 + r, n, acc[r]);
+    });
 }
 
 // SR[(s-1)*N + n] = non-zeros of column n in bitmap words kp < s * ceil(K/ls) / 32

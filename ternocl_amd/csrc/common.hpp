@@ -72,58 +72,12 @@ __device__ __forceinline__ float sigmoid_ref(float x) {
     return x <= -10.0f ? 0.0f : 1.0f / (expf(-x) + 1.0f);
 }
 
-__device__ __forceinline__ float epi_apply(float v, int postop, float other, float bias) {
-    switch (postop) {
-    case 1: return v * sigmoid_ref(v) * other;
-    case 2: return v + other;
-    case 3: return v + bias;
-    case 4: return sigmoid_ref(v);
-    case 5: return (v + bias) + other;
-    default: return v;
-    }
-}
-
 __host__ __device__ constexpr bool postop_needs_other(int p) { return p == 1 || p == 2 || p == 5; }
 __host__ __device__ constexpr bool postop_needs_bias(int p) { return p == 3 || p == 5; }
 
-// Epilogue + store of 4 consecutive outputs (m, n..n+3), n % 4 == 0.
-template <bool BF16>
-__device__ __forceinline__ void epi_store4(void *C, const uint16_t *Other, const void *Bias,
-                                           int postop, int out_f32, int N, int m, int n,
-                                           const float v[4]) {
-    const size_t i = (size_t)m * N + n;
-    float o[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
-    if (postop_needs_other(postop)) {
-        const uint2 t = *(const uint2 *)(Other + i);
-        o[0] = dt2f<BF16>(t.x & 0xffffu); o[1] = dt2f<BF16>(t.x >> 16);
-        o[2] = dt2f<BF16>(t.y & 0xffffu); o[3] = dt2f<BF16>(t.y >> 16);
-    }
-    if (postop_needs_bias(postop)) {
-        if (out_f32) {
-            const float4 t = *(const float4 *)((const float *)Bias + n);
-            b[0] = t.x; b[1] = t.y; b[2] = t.z; b[3] = t.w;
-        } else {
-            const uint2 t = *(const uint2 *)((const uint16_t *)Bias + n);
-            b[0] = dt2f<BF16>(t.x & 0xffffu); b[1] = dt2f<BF16>(t.x >> 16);
-            b[2] = dt2f<BF16>(t.y & 0xffffu); b[3] = dt2f<BF16>(t.y >> 16);
-        }
-    }
-    float r[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = epi_apply(v[c], postop, o[c], b[c]);
-    if (out_f32) {
-        *(float4 *)((float *)C + i) = make_float4(r[0], r[1], r[2], r[3]);
-    } else {
-        uint2 t;
-        t.x = f2dt<BF16>(r[0]) | (f2dt<BF16>(r[1]) << 16);
-        t.y = f2dt<BF16>(r[2]) | (f2dt<BF16>(r[3]) << 16);
-        *(uint2 *)((uint16_t *)C + i) = t;
-    }
-}
-
-// The same with the postop and output type fixed at compile time: kernels
-// with many outputs per lane dispatch once (a uniform branch) to one of these
-// instead of evaluating the postop switch per output.
+// Epilogue with the postop and output type fixed at compile time: kernels
+// dispatch once (a uniform branch, epi_dispatch) to one of these instead of
+// evaluating the postop switch per output.
 template <int P> __device__ __forceinline__ float epi_apply_c(float v, float other, float bias) {
     if constexpr (P == 1) return v * sigmoid_ref(v) * other;
     else if constexpr (P == 2) return v + other;
@@ -132,6 +86,7 @@ template <int P> __device__ __forceinline__ float epi_apply_c(float v, float oth
     else if constexpr (P == 5) return (v + bias) + other;
     else return v;
 }
+// Epilogue + store of 4 consecutive outputs (m, n..n+3), n % 4 == 0.
 template <bool BF16, int P, bool F32>
 __device__ __forceinline__ void epi_store4_c(void *C, const uint16_t *Other, const void *Bias, int N, int m, int n,
                                              const float v[4]) {
@@ -182,17 +137,16 @@ template <class Fn> __device__ __forceinline__ void epi_dispatch(int postop, int
     }
 }
 
-// Epilogue + store of one output (m, n).
-template <bool BF16>
-__device__ __forceinline__ void epi_store1(void *C, const uint16_t *Other, const void *Bias,
-                                           int postop, int out_f32, int N, int m, int n, float v) {
+// One output with the postop and output type fixed at compile time.
+template <bool BF16, int P, bool F32>
+__device__ __forceinline__ void epi_store1_c(void *C, const uint16_t *Other, const void *Bias, int N, int m, int n,
+                                             float v) {
     const size_t i = (size_t)m * N + n;
-    const float o = postop_needs_other(postop) ? dt2f<BF16>(Other[i]) : 0.0f;
+    const float o = postop_needs_other(P) ? dt2f<BF16>(Other[i]) : 0.0f;
     float b = 0.0f;
-    if (postop_needs_bias(postop))
-        b = out_f32 ? ((const float *)Bias)[n] : dt2f<BF16>(((const uint16_t *)Bias)[n]);
-    const float r = epi_apply(v, postop, o, b);
-    if (out_f32) ((float *)C)[i] = r;
+    if constexpr (postop_needs_bias(P)) b = F32 ? ((const float *)Bias)[n] : dt2f<BF16>(((const uint16_t *)Bias)[n]);
+    const float r = epi_apply_c<P>(v, o, b);
+    if constexpr (F32) ((float *)C)[i] = r;
     else ((uint16_t *)C)[i] = (uint16_t)f2dt<BF16>(r);
 }
 

@@ -231,9 +231,12 @@ k_int2_gemv(const uint16_t *__restrict__ A, const uint4 *__restrict__ B4,
         }
     }
     if (kl != 0) return;
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-        if (m < M) epi_store4<BF16>(C, Other, Bias, postop, out_f32, N, m, q4 * 4, acc[m]);
+        for (int m = 0; m < MR; ++m)
+            if (m < M)
+                epi_store4_c<BF16, decltype(P_)::value, decltype(F_)::value>(C, Other, Bias, N, m, q4 * 4, acc[m]);
+    });
 }
 
 // Test hooks: the reference-semantics unpack and the GEMV's own decode.

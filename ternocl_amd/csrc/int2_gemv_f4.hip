@@ -304,7 +304,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     static_assert(RR <= 16, "too many MFMA rows");
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int groups = K / kGS;
     const int gw = W * GPW;
@@ -406,18 +406,22 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 for (int h = 0; h < OPL; ++h) out[j][h] += red[((w2 - 1) * CPL + j) * JS + (q * 16 + c) * OPL + h];
     }
     if (!live) return;
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+        constexpr int PO = decltype(P_)::value;
+        constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
-    for (int h = 0; h < OPL; ++h) {
-        const int m = q + h;
-        if (m >= M) break;
+        for (int h = 0; h < OPL; ++h) {
+            const int m = q + h;
+            if (m >= M) break;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const float r = epi_apply(out[j][h], postop, ein.other(h, j), ein.bias(j, out_f32));
-            const size_t oi = (size_t)m * N + n0 + j;
-            if (out_f32) ((float *)C)[oi] = r;
-            else ((uint16_t *)C)[oi] = (uint16_t)f2dt<BF16>(r);
+            for (int j = 0; j < CPL; ++j) {
+                const float r = epi_apply_c<PO>(out[j][h], ein.other(h, j), ein.bias(j, F32));
+                const size_t oi = (size_t)m * N + n0 + j;
+                if constexpr (F32) ((float *)C)[oi] = r;
+                else ((uint16_t *)C)[oi] = (uint16_t)f2dt<BF16>(r);
+            }
         }
-    }
+    });
 }
 
 struct F4Plan {

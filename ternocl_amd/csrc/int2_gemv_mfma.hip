@@ -377,18 +377,22 @@ k_int2_gemv_mfma(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                     acc[j][i] += red[((w2 - 1) * CPL + j) * JS + (q * 16 + c) * ROWS + i];
     }
     if (!live) return;
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+        constexpr int PO = decltype(P_)::value;
+        constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
-    for (int i = 0; i < ROWS; ++i) {
-        const int m = 4 * q + i;
-        if (m >= M) break;
+        for (int i = 0; i < ROWS; ++i) {
+            const int m = 4 * q + i;
+            if (m >= M) break;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const float r = epi_apply(acc[j][i], postop, ein.o[i][j], ein.b[j]);
-            const size_t oi = (size_t)m * N + n0 + j;
-            if (out_f32) ((float *)C)[oi] = r;
-            else ((uint16_t *)C)[oi] = (uint16_t)f2dt<BF16>(r);
+            for (int j = 0; j < CPL; ++j) {
+                const float r = epi_apply_c<PO>(acc[j][i], ein.o[i][j], ein.b[j]);
+                const size_t oi = (size_t)m * N + n0 + j;
+                if constexpr (F32) ((float *)C)[oi] = r;
+                else ((uint16_t *)C)[oi] = (uint16_t)f2dt<BF16>(r);
+            }
         }
-    }
+    });
 }
 
 struct MfPlan {
