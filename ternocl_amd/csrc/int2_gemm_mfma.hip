@@ -149,7 +149,7 @@ template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
 // DUAL: the MoE gate/up pair in one pass over A -- acc from (B, S) is the up
 // projection, acc2 from (B2, S2) the gate; C = DT(silu(gate) * DT(up)), the
 // two-launch sequence's result (up rounded to DT, then POSTOP 1) bit for bit.
-template <class Cfg, bool BF16, bool DUAL = false>
+template <class Cfg, bool BF16, bool DUAL = false, bool SHORT = false>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
                                           const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                           void *__restrict__ C, const uint16_t *__restrict__ Other,
@@ -158,7 +158,8 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
                                           const uint32_t *__restrict__ B2 = nullptr,
                                           const uint16_t *__restrict__ S2 = nullptr) {
     constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = SHORT ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int wm = (wave / Cfg::WVN) * 16 * NMB, wn = (wave % Cfg::WVN) * 16 * NCB;
     const int stages = K / BK;
 
@@ -282,6 +283,10 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // K is a multiple of 128: the stage count is even and the loop runs in
     // pairs with the register set fixed at compile time.
     constexpr uint32_t kBuf = (uint32_t)Cfg::BM * A_PITCH;  // DT elements per buffer
+    // SHORT (tiles that may end early, as an expert's last tile): a wave whose
+    // rows all lie past the tile's last row skips its MFMAs; it still stages A
+    // and meets the barriers.
+    const bool rows_live = !SHORT || wm < mrows;
     uint32_t cur = 0;  // st % 3
     auto stage = [&](int st, int par) __attribute__((always_inline)) {
         const uint16_t *abuf = lds + cur * kBuf;
@@ -328,6 +333,7 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
             } else {
                 a_frags(abuf, ks, af);
             }
+            if (!rows_live) continue;  // uniform: this wave's rows are all past the tile's last row
 #pragma unroll
             for (int cb = 0; cb < CB2; ++cb) {
                 uint32_t bf[4];
@@ -471,7 +477,7 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
                           : ARows{A_all + (size_t)(row0 + m0) * K, nullptr, 1};
     const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : mrows) * K * 2);
     const size_t bo = (size_t)e * (K / 16) * N, so = (size_t)e * (K / kGS) * N;
-    gemm_tile<Cfg, BF16, DUAL>(ar, a_bytes, mrows, B_all + bo, S_all + so, C_all, Other_all, nullptr, row0 + m0,
+    gemm_tile<Cfg, BF16, DUAL, true>(ar, a_bytes, mrows, B_all + bo, S_all + so, C_all, Other_all, nullptr, row0 + m0,
                                N, K, tn * Cfg::BN, postop, out_f32, lds, DUAL ? B2_all + bo : nullptr,
                                DUAL ? S2_all + so : nullptr);
 }
