@@ -563,39 +563,54 @@ void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, c
 
 int moe_tile_rows() { return kMoeTileRows; }
 
+// Column tile of the MoE GEMMs: the widest of 512 / 256 / 128 columns whose
+// ragged last tile idles at most 1/10 of the MFMA work.
+static int moe_bn(int N, int widest) {
+    for (int bn = widest; bn > 128; bn >>= 1)
+        if ((long)((N + bn - 1) / bn) * bn * 10 <= (long)N * 11) return bn;
+    return 128;
+}
+
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
                             int E, int G, int N, int K, int postop, int out_f32, hipStream_t st) {
-    // 128-row tiles of eight waves: 256 columns (waves of 64 x 64) unless the
-    // ragged last column tile would idle more than 1/10 of the MFMA work, then
-    // 128 (waves of 64 x 32)
-    typedef TileCfg<4, 4, 2, 4> Wide;
-    typedef TileCfg<4, 2, 2, 4> Narrow;
-    const bool wide = (long)((N + 255) / 256) * 256 * 10 <= (long)N * 11;
+    // 128-row tiles of eight waves side by side, each wave 128 rows x 64
+    // columns (the dense engine's wave shape: 0.5 LDS fragment reads and 0.25
+    // weight-word decodes per MFMA) on 512-column tiles; 128 x 32 waves on 256,
+    // or 64 x 32 waves (2 x 4) on 128
+    typedef TileCfg<8, 4, 1, 8> W512;
+    typedef TileCfg<8, 2, 1, 8> W256;
+    typedef TileCfg<4, 2, 2, 4> W128;
+    const int bn = moe_bn(N, 512);
     if (dtype == TERNOCL_BF16) {
-        if (wide) moe_launch<Wide, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
-        else moe_launch<Narrow, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        if (bn == 512) moe_launch<W512, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else if (bn == 256) moe_launch<W256, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else moe_launch<W128, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
     } else {
-        if (wide) moe_launch<Wide, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
-        else moe_launch<Narrow, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        if (bn == 512) moe_launch<W512, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else if (bn == 256) moe_launch<W256, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        else moe_launch<W128, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
     }
     return check_launch();
 }
 
 // The gate/up pair of the MoE layer in one launch: Hs = DT(silu(A x Bg) * DT(A x Bu)),
 // bit-identical to moe_gemm_run(up, postop 0) followed by moe_gemm_run(gate, postop 1).
+// Eight waves side by side, each 128 rows x 32 columns of both products (one
+// A fragment feeds four MFMAs per weight set) on 256-column tiles, or 2 x 4
+// waves of 64 x 32 on 128.
 ternocl_status moe_gate_up_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                                const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
                                int E, int G, int N, int K, hipStream_t st) {
-    typedef TileCfg<4, 4, 2, 4> Wide;
-    typedef TileCfg<4, 2, 2, 4> Narrow;
-    const bool wide = (long)((N + 255) / 256) * 256 * 10 <= (long)N * 11;
+    typedef TileCfg<8, 2, 1, 8> W256;
+    typedef TileCfg<4, 2, 2, 4> W128;
+    const bool wide = moe_bn(N, 256) == 256;
     if (dtype == TERNOCL_BF16) {
-        if (wide) moe_launch<Wide, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
-        else moe_launch<Narrow, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+        if (wide) moe_launch<W256, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+        else moe_launch<W128, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
     } else {
-        if (wide) moe_launch<Wide, false, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
-        else moe_launch<Narrow, false, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+        if (wide) moe_launch<W256, false, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
+        else moe_launch<W128, false, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
     }
     return check_launch();
 }
