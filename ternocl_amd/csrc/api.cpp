@@ -70,7 +70,6 @@ ternocl_status fwht_run(int dtype, const void *x, const int8_t *signs, void *y, 
                         int HB, int use_signs, float scale_full, float scale_tail, hipStream_t st);
 // kernels (moe.hip, int2_gemm_mfma.hip)
 int moe_tile_rows();
-size_t moe_route_lds(int E);
 ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st);
 ternocl_status moe_gather_run(const void *X, const int *perm, void *Xs, int G, int K, int topk, hipStream_t st);
 ternocl_status moe_combine_run(int dtype, const float *Y, const int *inv, const void *RW, void *O, int T,

@@ -100,14 +100,16 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
             run[x] = r;
         }
     };
-    auto place_block = [&](int b0) {
+    // dst: perm in global memory, or (one block) its copy in LDS, written out
+    // in order afterwards: the scattered 4-byte stores stay on chip
+    auto place_block = [&](int b0, int *dst) {
         const int seg0 = b0 + wave * kRouteChunks * 64;
 #pragma unroll
         for (int c = 0; c < kRouteChunks; ++c) {
             const int g = seg0 + c * 64 + lane;
             if (eid[c] >= 0 && eid[c] < E) {
                 const int p = mine[eid[c]] + loc[c];
-                perm[p] = g;
+                dst[p] = g;
                 inv[g] = p;
             } else if (g < G) {
                 inv[g] = -1;
@@ -159,9 +161,13 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
     // registers and wcnt holds its per-wave counts.  Otherwise each block is
     // loaded and ranked again, on top of the running bases.
     if (G <= kRouteBlock) {
+        int *sperm = wcnt + kRouteWaves * E;  // [meta[E]] rows
         wave_bases();
         __syncthreads();
-        place_block(0);
+        place_block(0, sperm);
+        __syncthreads();
+        const int rows = meta[E];
+        for (int i = tid; i < rows; i += kRouteThreads) perm[i] = sperm[i];
         return;
     }
     for (int b0 = 0; b0 < G; b0 += kRouteBlock) {
@@ -172,7 +178,7 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
         __syncthreads();
         wave_bases();
         __syncthreads();
-        place_block(b0);
+        place_block(b0, perm);
         __syncthreads();  // wcnt is reset for the next block
     }
 }
@@ -220,10 +226,13 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
 
 }  // namespace
 
-size_t moe_route_lds(int E) { return (size_t)(2 + kRouteWaves) * E * sizeof(int); }
+// counts, running bases and per-wave counts; with one block also perm's LDS copy
+size_t moe_route_lds(int E, int G) {
+    return ((size_t)(2 + kRouteWaves) * E + (G <= kRouteBlock ? (size_t)G : 0)) * sizeof(int);
+}
 
 ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st) {
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), moe_route_lds(E), st, ids, meta, perm, inv,
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), moe_route_lds(E, G), st, ids, meta, perm, inv,
                        G, E, moe_tile_rows());
     return check_launch();
 }
