@@ -509,12 +509,12 @@ struct GemmPlan {
 // each tile shape (larger tiles decode fewer B words and read less A per MAC;
 // eight-wave tiles keep two waves per SIMD, four-wave 256 x 256 tiles one).
 GemmPlan gemm_plan(int M, int N) {
-    static const GemmPlan cands[] = {{8, 4, 2, 4}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
-    static const double eff[] = {1.0, 0.75, 0.7, 0.88};
-    static const int per_cu[] = {1, 1, 1, 2};  // resident workgroups per CU
-    GemmPlan best = cands[3];
+    static const GemmPlan cands[] = {{8, 4, 1, 8}, {8, 4, 2, 4}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
+    static const double eff[] = {1.0, 0.99, 0.75, 0.7, 0.88};
+    static const int per_cu[] = {1, 1, 1, 1, 2};  // resident workgroups per CU
+    GemmPlan best = cands[4];
     double best_t = 1e300;
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 5; ++c) {
         const int BM = 16 * cands[c].nmb * cands[c].wvm, BN = 16 * cands[c].ncb * cands[c].wvn;
         const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
         const long slots = 256L * per_cu[c];
@@ -541,7 +541,8 @@ template <bool BF16>
 void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const void *S, void *C,
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
-    if (p.wvn == 4) gemm_launch<TileCfg<8, 4, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (p.wvn == 8) gemm_launch<TileCfg<8, 4, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.wvn == 4) gemm_launch<TileCfg<8, 4, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else if (p.nmb == 8) gemm_launch<TileCfg<8, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else if (p.ncb == 8) gemm_launch<TileCfg<4, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
