@@ -381,8 +381,10 @@ def main():
     ap.add_argument("--only-headline", action="store_true", help="skip the prefill, C1, C4 and C5 workloads")
     ap.add_argument("--probe", type=int, default=0, metavar="N",
                     help="counter-collection mode for rocprofv3 --pmc: N eager launches per GEMV shape, "
-                         "a 64 MiB device copy (the calibration kernel of known size) and N calls of the "
-                         "int8 prefill (quant_a + s8 x s2 GEMM, M=1024 K=4096 N=14336); prints one line")
+                         "a 64 MiB device copy (the calibration kernel of known size), N calls each of the "
+                         "int8 prefill (quant_a + s8 x s2 GEMM) and the fp16 upcvt prefill GEMM (M=1024 "
+                         "K=4096 N=14336), of the BITCOS GEMV (K=5376 N=21504, z = .5) and of one MoE "
+                         "prefill layer (T=2048 E=64 top-8 H=2048 I=1408); prints one line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -417,6 +419,36 @@ def main():
         for _ in range(args.probe):
             T.quant_a(dA, dSA, dAq, M, K)
             T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, None, None, M, N, K)
+        for _ in range(args.probe):  # the fp16 upcvt prefill GEMM on the same operands
+            T.int2_fp16_upcvt_gemm(dA, dB, dSB, dC, None, None, M, N, K)
+        del dA, dB, dSB, dSA, dAq, dC
+        # BITCOS GEMV M=1 K=5376 N=21504 fp16 at z = .5, one weight set
+        Kb, Nb = 5376, 21504
+        g = synth.rng(49)
+        x = dev16(torch, synth.activations(g, (1, Kb), False), False)
+        buf, _ = synth.bitcos_weights(g, Kb, Nb, 0.5)
+        dBc, dSc = dev32(torch, buf), dev16(torch, synth.scales(g, Kb, Nb, False), False)
+        ls = T.bitcos_pick_ls(1, Nb, Kb)
+        dSR = torch.zeros(max(ls - 1, 1) * Nb, dtype=torch.int32, device="cuda")
+        T.bitcos_slice_ranks(dBc, dSR, Kb, Nb, ls)
+        dCb = torch.empty((1, Nb), dtype=torch.float16, device="cuda")
+        for _ in range(args.probe):
+            T.bitcos_fp16_upcvt_gemm(x, dBc, dSc, dSR, dCb, None, None, 1, Nb, Kb, ls)
+        del x, dBc, dSc, dSR, dCb
+        # one int2 MoE prefill layer, T=2048 E=64 top-8 H=2048 I=1408 bf16
+        Tk, E, topk, H, I = 2048, 64, 8, 2048, 1408
+        g = synth.rng(55)
+        X = dev16(torch, synth.activations(g, (Tk, H), True), True)
+        ids, RW = synth.moe_routing(g, Tk, E, topk, True)
+        dids, dRW = torch.from_numpy(ids).cuda(), dev16(torch, RW, True)
+        wts = []
+        for K_, N_ in ((H, I), (H, I), (I, H)):
+            wts.append(dev32(torch, np.stack([synth.int2_weights(g, K_, N_) for _ in range(E)])))
+            wts.append(dev16(torch, np.stack([synth.scales(g, K_, N_, True) for _ in range(E)]), True))
+        dO = torch.empty((Tk, H), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(T.int2_moe_prefill_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device="cuda")
+        for _ in range(args.probe):
+            T.int2_moe_prefill(X, dids, dRW, Tk, E, topk, H, I, *wts, dO, ws)
         torch.cuda.synchronize()
         print(json.dumps({"probe": args.probe, "bytes_per_launch": {f"K{sb.K}_N{sb.N}": sb.bytes() for sb in sbs},
                           "copy_bytes": 64 << 20}), flush=True)
