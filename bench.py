@@ -329,6 +329,40 @@ def bench_c4(torch, T, synth, formats, orc):
                         "fwht_bit_exact": fwht_ok}
         del W, dB, dSR
         torch.cuda.empty_cache()
+    # the M-tiled BITCOS path (bitcos_fp16_upcvt_gemm_mt) at a prefill M: re-pack + int2 GEMM
+    Mp, z = 1024, 0.5
+    g = synth.rng(77)
+    A = synth.activations(g, (Mp, K), bf16)
+    buf, _ = synth.bitcos_weights(g, K, N, z)
+    S = synth.scales(g, K, N, bf16)
+    ls = T.bitcos_pick_ls(1, N, K)
+    dA, dB, dS = dev16(torch, A, bf16), dev32(torch, buf), dev16(torch, S, bf16)
+    dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    ws = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device="cuda")
+    dC = torch.empty((Mp, N), dtype=torch.float16, device="cuda")
+    dW2 = ws.view(torch.int32).view(K // 16, N)
+
+    def mt():
+        T.bitcos_fp16_upcvt_gemm_mt(dA, dB, dS, dSR, dC, None, None, Mp, N, K, ls, ws)
+
+    def repack():
+        T.bitcos_to_int2(dB, dSR, ls, dW2, K, N)
+    mt()
+    torch.cuda.synchronize()
+    rows = 4
+    want = formats.dt_to_f32(orc.epilogue(orc.bitcos_gold(A[:rows], buf, S, rows, K, N, bf16), None, None, 0,
+                                          False, bf16), bf16)
+    got = formats.dt_to_f32(dC[:rows].contiguous().view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
+    us = graph_time_us(torch, mt, 10)
+    r_us = graph_time_us(torch, repack, 20)
+    flops = 2.0 * Mp * N * K
+    out["prefill_m1024_z0.5"] = {"workload": "bitcos_fp16_upcvt_gemm_mt M=1024 K=5376 N=21504 fp16 z=.5: "
+                                             "re-pack to int2 + int2 prefill GEMM",
+                                 "us": round(us, 2), "TFLOPS": round(flops / us / 1e6, 1),
+                                 "mfma_frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                 "repack_us": round(r_us, 2), "parity_bad": bad, "parity_rows": rows}
     return out
 
 

@@ -162,6 +162,25 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const ui
                                               const void *S, const uint32_t *SR, int ls, void *C,
                                               const void *Other, const void *Bias, int M, int N,
                                               int K, int postop, int out_f32, void *stream);
+/* ---- BITCOS M-tiled prefill ---------------------------------------------
+ * Replaces bitcos_fp16_upcvt_gemm_mt (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:303-305):
+ * the same C as ternocl_bitcos_fp16_upcvt_gemm (within the float tolerance) for
+ * any M, with the weights streamed once instead of once per 4 rows.  One pass
+ * re-packs the BITCOS weights into the int2 format (K * N / 4 bytes of ws,
+ * ternocl_bitcos_gemm_mt_ws_bytes), then the int2 prefill GEMM engine runs on
+ * them with S as is.  SR / ls as for ternocl_bitcos_fp16_upcvt_gemm (the
+ * re-pack splits K into ls slices); the same constraints. */
+size_t ternocl_bitcos_gemm_mt_ws_bytes(int K, int N);
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const uint32_t *B,
+                                                 const void *S, const uint32_t *SR, int ls, void *C,
+                                                 const void *Other, const void *Bias, int M, int N,
+                                                 int K, int postop, int out_f32, void *ws,
+                                                 size_t ws_bytes, void *stream);
+/* The re-pack alone (bit-exact hook): W2 uint32 [K/16][N], row j of word (kp, n)
+ * in bits 2j, 2j+1 = code 0 / 1 / 3 for 0 / +1 / -1 (the int2 format of
+ * ternocl_int2_fp16_upcvt_gemm). */
+ternocl_status ternocl_bitcos_to_int2(const uint32_t *B, const uint32_t *SR, int ls, uint32_t *W2, int K,
+                                      int N, void *stream);
 /* Slice ranks of a BITCOS buffer for ls slices: SR[(s-1)*N + n] = non-zeros of
  * column n in bitmap words kp < s * ceil(K/ls) / 32 (common/bitcos.hpp:81-94). */
 ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K, int N, int ls,

@@ -186,6 +186,25 @@ def bitcos_fp16_upcvt_gemm(A, B, S, SR, C, Other, Bias, M: int, N: int, K: int, 
                                                 int(bool(out_f32)), _stream(stream)))
 
 
+def bitcos_gemm_mt_ws_bytes(K: int, N: int) -> int:
+    return lib().ternocl_bitcos_gemm_mt_ws_bytes(K, N)
+
+
+def bitcos_fp16_upcvt_gemm_mt(A, B, S, SR, C, Other, Bias, M: int, N: int, K: int, ls: int, ws,
+                              postop: int = 0, out_f32: bool = False, stream=None) -> None:
+    """bitcos_fp16_upcvt_gemm_mt (bitcos_fp16_upcvt.cl:303): any M, the weights re-packed into
+    ws (bitcos_gemm_mt_ws_bytes) and streamed once by the int2 prefill GEMM."""
+    _check(lib().ternocl_bitcos_fp16_upcvt_gemm_mt(_dtype_of(A), _ptr(A), _ptr(B), _ptr(S), _ptr(SR), ls,
+                                                   _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                                   int(bool(out_f32)), _ptr(ws), _nbytes(ws),
+                                                   _stream(stream)))
+
+
+def bitcos_to_int2(B, SR, ls: int, W2, K: int, N: int, stream=None) -> None:
+    """W2 [K/16, N] int2 words of the BITCOS weights (the M-tiled path's re-pack, test hook)."""
+    _check(lib().ternocl_bitcos_to_int2(_ptr(B), _ptr(SR), ls, _ptr(W2), K, N, _stream(stream)))
+
+
 def bitcos_slice_ranks(B, SR, K: int, N: int, ls: int, stream=None) -> None:
     """SR [ls-1, N] slice ranks of a BITCOS buffer (common/bitcos.hpp:81-94), on the device."""
     _check(lib().ternocl_bitcos_slice_ranks(_ptr(B), _ptr(SR), K, N, ls, _stream(stream)))

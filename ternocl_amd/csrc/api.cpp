@@ -65,6 +65,8 @@ ternocl_status bitcos_slice_ranks_run(const uint32_t *Bc, uint32_t *SR, int N, i
                                       hipStream_t st);
 ternocl_status bitcos_dequant_run(int dtype, const uint32_t *Bc, const void *S, void *W, int N, int K,
                                   hipStream_t st);
+ternocl_status bitcos_to_int2_run(const uint32_t *Bc, const uint32_t *SR, int ls, uint32_t *W2, int N, int K,
+                                  hipStream_t st);
 // kernels (hadamard.hip)
 ternocl_status fwht_run(int dtype, const void *x, const int8_t *signs, void *y, int rows, int K,
                         int HB, int use_signs, float scale_full, float scale_tail, hipStream_t st);
@@ -241,6 +243,44 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const ui
     if (ls > 1 && !SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR (slice ranks for ls slices) must be non-null when ls > 1");
     return bitcos_gemv_run(dtype, A, B, S, SR, ls, C, Other, Bias, M, N, K, postop, out_f32,
                            (hipStream_t)stream);
+}
+
+static ternocl_status check_bitcos_slices(int N, int K, int ls, const uint32_t *SR) {
+    if (ls < 1 || ls > bitcos_max_ls()) FAIL(TERNOCL_ERR_INVALID_ARG, "ls must be 1..16");
+    if (N < 16 || N % 16 || K < 64 || K % (64 * ls)) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need N % 16 == 0 and K % (64 * ls) == 0");
+    if (ls > 1 && !SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR (slice ranks for ls slices) must be non-null when ls > 1");
+    return TERNOCL_OK;
+}
+
+size_t ternocl_bitcos_gemm_mt_ws_bytes(int K, int N) {
+    if (K < 16 || N < 1) return 0;
+    return (size_t)(K / 16) * (size_t)N * 4;
+}
+
+ternocl_status ternocl_bitcos_to_int2(const uint32_t *B, const uint32_t *SR, int ls, uint32_t *W2, int K,
+                                      int N, void *stream) {
+    if (!B || !W2) FAIL(TERNOCL_ERR_INVALID_ARG, "B and W2 must be non-null");
+    ternocl_status s = check_bitcos_slices(N, K, ls, SR);
+    if (s != TERNOCL_OK) return s;
+    return bitcos_to_int2_run(B, SR, ls, W2, N, K, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const uint32_t *B,
+                                                 const void *S, const uint32_t *SR, int ls, void *C,
+                                                 const void *Other, const void *Bias, int M, int N,
+                                                 int K, int postop, int out_f32, void *ws,
+                                                 size_t ws_bytes, void *stream) {
+    ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
+    if (s != TERNOCL_OK) return s;
+    if ((s = check_bitcos_slices(N, K, ls, SR)) != TERNOCL_OK) return s;
+    const size_t need = ternocl_bitcos_gemm_mt_ws_bytes(K, N);
+    if (!ws || ws_bytes < need) FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_bitcos_gemm_mt_ws_bytes(K, N) bytes");
+    if (((uintptr_t)ws & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "ws must be 16-byte aligned");
+    if (need >= (1u << 31) || (size_t)M * K * 2 >= (1u << 31))
+        FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the M-tiled BITCOS path takes A and the re-packed weights below 2^31 bytes");
+    const hipStream_t st = (hipStream_t)stream;
+    if ((s = bitcos_to_int2_run(B, SR, ls, (uint32_t *)ws, N, K, st)) != TERNOCL_OK) return s;
+    return int2_gemm_mfma_run(dtype, A, (const uint32_t *)ws, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
 ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K, int N, int ls,

@@ -258,6 +258,76 @@ k_bitcos_dequant(const uint32_t *__restrict__ Bc, const uint16_t *__restrict__ S
     }
 }
 
+// Re-pack for the M-tiled path: the BITCOS weights as int2 words (row j of
+// word (kp, n) in bits 2j, 2j + 1; codes 0 / 1 / 3 = 0 / +1 / -1), so the int2
+// prefill GEMM engine runs on them.  Lane = column, wave = K slice (entering
+// the column's sign stream at SR[s-1], as the GEMV); per block of up to 8
+// bitmap words, all bitmap loads go out together, then -- the ranks known --
+// all sign-word loads, then the decode: two dependent memory round trips per
+// block.  The 256-byte table maps (nibble of presence bits, next four sign
+// bits) to the nibble's four 2-bit codes.
+__global__ void __launch_bounds__(64 * kBcMaxLs)
+k_bitcos_to_int2(const uint32_t *__restrict__ Bc, const uint32_t *__restrict__ SR, uint32_t *__restrict__ W2,
+                 int N, int K, int ls) {
+    __shared__ uint8_t lut[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+        const uint32_t m = (uint32_t)i >> 4, sgn = (uint32_t)i & 15u;
+        uint32_t r = 0, out = 0;
+        for (int j = 0; j < 4; ++j)
+            if ((m >> j) & 1u) {
+                out |= (1u | (((sgn >> r) & 1u) << 1)) << (2 * j);
+                ++r;
+            }
+        lut[i] = (uint8_t)out;
+    }
+    __syncthreads();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 64 + lane;
+    const int nc = n < N ? n : N - 1;
+    const size_t bw = (size_t)(K >> 5) * N;
+    const uint32_t *__restrict__ sg = Bc + bw + N + Bc[bw + nc];
+    const int words = K >> 5, per = words / ls, w0 = wave * per;
+    uint32_t R = wave ? SR[(size_t)(wave - 1) * N + nc] : 0u;
+    for (int b = 0; b < per; b += 8) {
+        uint32_t bm[8], r[8], lo[8], hi[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int kp = w0 + b + j < words ? w0 + b + j : words - 1;
+            const uint32_t x = Bc[(size_t)kp * N + nc];
+            bm[j] = b + j < per ? x : 0u;  // words past the slice: no rows, no signs
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            r[j] = R;
+            R += __builtin_popcount(bm[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // inside the stream or its pad words
+            lo[j] = sg[r[j] >> 5];
+            hi[j] = sg[(r[j] >> 5) + 1];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (b + j >= per) break;  // uniform
+            const uint32_t sw = __builtin_amdgcn_alignbit(hi[j], lo[j], r[j] & 31u);
+            uint32_t out[2] = {0u, 0u}, p = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t m4 = (bm[j] >> (4 * i)) & 15u;
+                const uint32_t s4 = (sw >> p) & 15u;
+                p = __builtin_popcount(m4) + p;
+                out[i >> 2] |= (uint32_t)lut[(m4 << 4) | s4] << (8 * (i & 3));
+            }
+            if (n < N) {
+                const size_t kp2 = 2 * (size_t)(w0 + b + j);
+                W2[kp2 * N + n] = out[0];
+                W2[(kp2 + 1) * N + n] = out[1];
+            }
+        }
+    }
+}
+
 template <int MR, bool BF16>
 void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
@@ -290,6 +360,12 @@ ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, con
         bc_launch_rows<true>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, st);
     else
         bc_launch_rows<false>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, st);
+    return check_launch();
+}
+
+ternocl_status bitcos_to_int2_run(const uint32_t *Bc, const uint32_t *SR, int ls, uint32_t *W2, int N, int K,
+                                  hipStream_t st) {
+    hipLaunchKernelGGL(k_bitcos_to_int2, dim3((N + 63) / 64), dim3(64 * ls), 0, st, Bc, SR, W2, N, K, ls);
     return check_launch();
 }
 

@@ -508,17 +508,29 @@ struct GemmPlan {
 // round of workgroups over the 256 CUs), weighted by the relative MAC rate of
 // each tile shape (larger tiles decode fewer B words and read less A per MAC;
 // eight-wave tiles keep two waves per SIMD, four-wave 256 x 256 tiles one).
+// Tile choice.  The 128 x 512 tile of eight 128 x 64 waves is the fastest per
+// FLOP (measured 1.1-1.2 PFLOPS at M = 1024..4096), so it is taken whenever it
+// yields at least 192 tiles (three quarters of the CUs busy in its first
+// round; at N = 21504 its second, partial round still beats the 128 x 128
+// tile).  Below that the candidates are scored by rounds x tile area /
+// throughput relative to it (measured: 256 x 256 0.94, 256 x 128 0.66, 128 x
+// 256 0.69, 128 x 128 with two workgroups per CU 0.78).
 GemmPlan gemm_plan(int M, int N) {
+    auto tiles = [&](const GemmPlan &p) {
+        const int BM = 16 * p.nmb * p.wvm, BN = 16 * p.ncb * p.wvn;
+        return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    };
+    const GemmPlan wide = {8, 4, 1, 8};
+    if (tiles(wide) >= 192) return wide;
     static const GemmPlan cands[] = {{8, 4, 1, 8}, {8, 4, 2, 4}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
-    static const double eff[] = {1.0, 0.99, 0.75, 0.7, 0.88};
+    static const double eff[] = {1.0, 0.94, 0.66, 0.69, 0.78};
     static const int per_cu[] = {1, 1, 1, 1, 2};  // resident workgroups per CU
     GemmPlan best = cands[4];
     double best_t = 1e300;
     for (int c = 0; c < 5; ++c) {
         const int BM = 16 * cands[c].nmb * cands[c].wvm, BN = 16 * cands[c].ncb * cands[c].wvn;
-        const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
         const long slots = 256L * per_cu[c];
-        const long rounds = (tiles + slots - 1) / slots;
+        const long rounds = (tiles(cands[c]) + slots - 1) / slots;
         const double t = (double)rounds * BM * BN * per_cu[c] / eff[c];
         if (t < best_t * 0.999) {
             best_t = t;

@@ -218,3 +218,107 @@ def test_bitcos_rejects_bad_ls(dev):
         T.bitcos_fp16_upcvt_gemm(A, B, S, None, C, None, None, 1, 16, 1024, ls=3)  # 1024 % 192
     with pytest.raises(T.TernoclError):
         T.bitcos_fp16_upcvt_gemm(A, B, S, None, C, None, None, 1, 16, 1024, ls=2)  # SR missing
+
+
+# ---- BITCOS M-tiled prefill (re-pack to int2 + the int2 prefill GEMM) -------------------
+
+@pytest.mark.parametrize("K,N,ls", [(256, 16, 1), (1024, 272, 4), (5376, 1040, 14), (2048, 96, 16)])
+@pytest.mark.parametrize("z", [0.0, 0.5, 1.0])
+def test_bitcos_to_int2_bit_exact(dev, orc, K, N, ls, z):
+    """The re-pack reproduces the int2 packing of the same codes bit for bit, through every
+    slice count (each slice enters its columns' sign streams at the slice ranks)."""
+    import torch
+    import ternocl_amd as T
+    print(f"bitcos to int2 K={K} N={N} ls={ls} z={z}", flush=True)
+    _, codes, _, _, _ = _bitcos_case(700 + K + N + ls, 1, K, N, z, False)
+    buf = formats.bitcos_pack(codes)
+    dB = dev_raw(buf)
+    dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    dW = torch.full((K // 16, N), -1, dtype=torch.int32, device="cuda")
+    T.bitcos_to_int2(dB, dSR if ls > 1 else None, ls, dW, K, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u32(dW), formats.pack_int2(codes))
+
+
+def _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32):
+    dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(buf), dev_dt(S, bf16), dev_dt(other, bf16)
+    dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    if out_f32:
+        dBias = torch.from_numpy(bias_f).cuda()
+        dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    else:
+        dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+        dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+    ws = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device="cuda")
+    T.bitcos_fp16_upcvt_gemm_mt(dA, dB, dS, dSR if ls > 1 else None, dC, dO, dBias, M, N, K, ls, ws,
+                                postop, out_f32)
+    torch.cuda.synchronize()
+    return dC
+
+
+MT_SHAPES = [(1, 256, 16, 1), (16, 1024, 272, 4), (64, 5376, 1024, 7), (130, 2048, 528, 8),
+             (257, 1536, 96, 6), (1024, 5376, 256, 14)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ls", MT_SHAPES)
+def test_bitcos_gemm_mt_parity(dev, orc, M, K, N, ls, bf16):
+    """Ragged M (1, 130, 257), the reference's M >= 64 prefill range, and the C4 K."""
+    import torch
+    import ternocl_amd as T
+    print(f"bitcos mt M={M} K={K} N={N} ls={ls} bf16={bf16}", flush=True)
+    A, codes, S, other, bias_f = _bitcos_case(5000 + M + K + N, M, K, N, 0.5, bf16)
+    buf = formats.bitcos_pack(codes)
+    dC = _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False)
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 0, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_bitcos_gemm_mt_epilogues(dev, orc, postop, out_f32):
+    import torch
+    import ternocl_amd as T
+    M, K, N, ls, bf16 = 96, 1024, 272, 4, True
+    A, codes, S, other, bias_f = _bitcos_case(80 + postop, M, K, N, 0.3, bf16)
+    buf = formats.bitcos_pack(codes)
+    dC = _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32)
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, postop, out_f32)
+    got = dC.cpu().numpy() if out_f32 else formats.dt_to_f32(host_u16(dC), bf16)
+    ref = want if out_f32 else formats.dt_to_f32(want, bf16)
+    bad, dmax = allclose_report(got, ref)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+def test_bitcos_gemm_mt_matches_gemv_path(dev, orc):
+    """The M-tiled path and the row-block GEMV path agree (both within tolerance of the gold),
+    and the M-tiled path is deterministic."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, ls, bf16 = 24, 5376, 512, 14, False
+    A, codes, S, other, bias_f = _bitcos_case(31, M, K, N, 0.7, bf16)
+    buf = formats.bitcos_pack(codes)
+    a = host_u16(_bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 5, False))
+    b = host_u16(_bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 5, False))
+    bad, dmax = allclose_report(formats.dt_to_f32(a, bf16), formats.dt_to_f32(b, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+    again = host_u16(_bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 5, False))
+    assert np.array_equal(a, again)
+
+
+def test_bitcos_gemm_mt_rejects_small_workspace(dev):
+    import torch
+    import ternocl_amd as T
+    M, K, N = 32, 1024, 64
+    A = torch.zeros((M, K), dtype=torch.float16, device="cuda")
+    B = torch.zeros(K // 32 * N + N + 8, dtype=torch.int32, device="cuda")
+    S = torch.zeros((K // 128, N), dtype=torch.float16, device="cuda")
+    C = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    small = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N) - 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(T.TernoclError):
+        T.bitcos_fp16_upcvt_gemm_mt(A, B, S, None, C, None, None, M, N, K, 1, small)
+    with pytest.raises(T.TernoclError):
+        T.bitcos_fp16_upcvt_gemm_mt(A, B, S, None, C, None, None, M, N, K, 1, None)
