@@ -1,0 +1,140 @@
+"""PyTorch custom operators over the C ABI: ``torch.ops.ternocl.*``.
+
+A serving framework calls the library through these: each operator allocates
+its outputs (and, where the C ABI takes one, its workspace) with torch on the
+inputs' device, launches on torch's current stream, and has a fake (meta)
+implementation, so the operators trace under ``torch.compile`` and run inside
+captured CUDA/HIP graphs.  They add nothing to the arithmetic: every call is
+one call of the ``ternocl_amd`` function of the same name, which raises if the
+native library is missing (there is no CPU fallback).
+
+    import ternocl_amd.torch_ops  # registers the operators
+    C = torch.ops.ternocl.int2_gemm(A, B, S, None, None, 0, False)
+
+Operators (the reference kernels they stand for, as in the C ABI):
+  int2_gemm         int2_fp16_upcvt_gemm{,_mt}            (int2_fp16_upcvt.cl:196, :341)
+  quant_a           quant_a                               (int2_int8_dpas.cl:105)
+  int2_int8_gemm    int2_int8_gemm_mt, upfront quant      (int2_int8_dpas.cl:316)
+  bitcos_gemm       bitcos_fp16_upcvt_gemv / _gemm_mt     (bitcos_fp16_upcvt.cl:179, :303)
+  fwht              hadamard_fwht                         (hadamard_fwht.cl:63)
+  moe_prefill       the int2 MoE prefill layer            (int2_moe/prefill.cpp:268-279)
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+import ternocl_amd as T
+
+__all__ = ["int2_gemm", "quant_a", "int2_int8_gemm", "bitcos_gemm", "fwht", "moe_prefill"]
+
+
+def _out_dtype(A: torch.Tensor, out_f32: bool) -> torch.dtype:
+    return torch.float32 if out_f32 else A.dtype
+
+
+@torch.library.custom_op("ternocl::int2_gemm", mutates_args=())
+def int2_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, other: Optional[torch.Tensor],
+              bias: Optional[torch.Tensor], postop: int, out_f32: bool) -> torch.Tensor:
+    """C [M, N] = ct(epi(A x dequant(B, S))); B int32 [K/16, N], S [K/128, N] in A's dtype."""
+    M, K = A.shape
+    N = B.shape[1]
+    C = torch.empty((M, N), dtype=_out_dtype(A, out_f32), device=A.device)
+    T.int2_fp16_upcvt_gemm(A, B, S, C, other, bias, M, N, K, postop, out_f32)
+    return C
+
+
+@int2_gemm.register_fake
+def _(A, B, S, other, bias, postop, out_f32):
+    return A.new_empty((A.shape[0], B.shape[1]), dtype=_out_dtype(A, out_f32))
+
+
+@torch.library.custom_op("ternocl::quant_a", mutates_args=())
+def quant_a(A: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(SA [K/128, ldsa(M)] in A's dtype, Aq int8 [M, K]) of A [M, K]."""
+    M, K = A.shape
+    SA = torch.empty((K // 128, T.ldsa(M)), dtype=A.dtype, device=A.device)
+    Aq = torch.empty((M, K), dtype=torch.int8, device=A.device)
+    T.quant_a(A, SA, Aq, M, K)
+    return SA, Aq
+
+
+@quant_a.register_fake
+def _(A):
+    M, K = A.shape
+    # ldsa(M) = (M + 31) & ~31 (LDSA of int2_int8_dpas.cl:58), computed here without the library
+    return A.new_empty((K // 128, (M + 31) // 32 * 32)), A.new_empty((M, K), dtype=torch.int8)
+
+
+@torch.library.custom_op("ternocl::int2_int8_gemm", mutates_args=())
+def int2_int8_gemm(Aq: torch.Tensor, SA: torch.Tensor, B: torch.Tensor, SB: torch.Tensor,
+                   other: Optional[torch.Tensor], bias: Optional[torch.Tensor], postop: int,
+                   out_f32: bool) -> torch.Tensor:
+    """C [M, N] of the s8 x s2 prefill on quant_a's (SA, Aq); SB [K/128, N] sets the dtype."""
+    M, K = Aq.shape
+    N = B.shape[1]
+    C = torch.empty((M, N), dtype=_out_dtype(SB, out_f32), device=Aq.device)
+    T.int2_int8_gemm(None, Aq, SA, B, SB, C, other, bias, M, N, K, postop, out_f32)
+    return C
+
+
+@int2_int8_gemm.register_fake
+def _(Aq, SA, B, SB, other, bias, postop, out_f32):
+    return SB.new_empty((Aq.shape[0], B.shape[1]), dtype=_out_dtype(SB, out_f32))
+
+
+@torch.library.custom_op("ternocl::bitcos_gemm", mutates_args=())
+def bitcos_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, SR: Optional[torch.Tensor], ls: int,
+                N: int, other: Optional[torch.Tensor], bias: Optional[torch.Tensor], postop: int,
+                out_f32: bool) -> torch.Tensor:
+    """C [M, N] of the BITCOS weights B (the common/bitcos.hpp buffer, int32) with slice ranks SR
+    for ls slices.  M >= 16 takes the M-tiled path (a workspace of the re-packed weights is
+    allocated per call), smaller M the GEMV."""
+    M, K = A.shape
+    C = torch.empty((M, N), dtype=_out_dtype(A, out_f32), device=A.device)
+    if M >= 16:
+        ws = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device=A.device)
+        T.bitcos_fp16_upcvt_gemm_mt(A, B, S, SR, C, other, bias, M, N, K, ls, ws, postop, out_f32)
+    else:
+        T.bitcos_fp16_upcvt_gemm(A, B, S, SR, C, other, bias, M, N, K, ls, postop, out_f32)
+    return C
+
+
+@bitcos_gemm.register_fake
+def _(A, B, S, SR, ls, N, other, bias, postop, out_f32):
+    return A.new_empty((A.shape[0], N), dtype=_out_dtype(A, out_f32))
+
+
+@torch.library.custom_op("ternocl::fwht", mutates_args=())
+def fwht(x: torch.Tensor, signs: Optional[torch.Tensor], HB: int) -> torch.Tensor:
+    """y [rows, K] = DT(SCALE * H_HB(signs * x)) blockwise; signs int8 [K] or None."""
+    rows, K = x.shape
+    y = torch.empty_like(x)
+    T.hadamard_fwht(x, signs, y, rows, K, HB, signs is not None)
+    return y
+
+
+@fwht.register_fake
+def _(x, signs, HB):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("ternocl::moe_prefill", mutates_args=())
+def moe_prefill(X: torch.Tensor, ids: torch.Tensor, RW: torch.Tensor, E: int, Bg: torch.Tensor,
+                Sg: torch.Tensor, Bu: torch.Tensor, Su: torch.Tensor, Bd: torch.Tensor,
+                Sd: torch.Tensor) -> torch.Tensor:
+    """O [T, H] of one int2 MoE layer: X [T, H], ids int32 [T, topk], RW [T, topk] in X's dtype,
+    experts stacked: Bg / Bu int32 [E, H/16, I], Bd int32 [E, I/16, H], scales alike."""
+    Tk, H = X.shape
+    topk = ids.shape[1]
+    I = Bg.shape[2]
+    O = torch.empty((Tk, H), dtype=X.dtype, device=X.device)
+    ws = torch.empty(T.int2_moe_prefill_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device=X.device)
+    T.int2_moe_prefill(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
+    return O
+
+
+@moe_prefill.register_fake
+def _(X, ids, RW, E, Bg, Sg, Bu, Su, Bd, Sd):
+    return torch.empty_like(X)
