@@ -404,6 +404,47 @@ def bench_c5(torch, T, synth, formats, orc):
             "check_rel_err_4_tokens": rel, "check_pass": rel < 1e-2}
 
 
+def bench_c6(torch, T, synth, formats, orc):
+    """int2 MoE decode layer at the reference driver's default problem (int2_moe/main.cpp:6):
+    T=1 E=128 top-8, H=2048 I=768, bf16.  Rate = the weight bytes the layer must stream (the
+    topk experts' gate, up and down B and S) / time; weight sets rotated past the caches like
+    the reference's --sets."""
+    Tk, E, topk, H, I, bf16 = 1, 128, 8, 2048, 768, True
+    g = synth.rng(66)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+
+    def experts(K, N):
+        return (np.stack([synth.int2_weights(g, K, N) for _ in range(E)]),
+                np.stack([synth.scales(g, K, N, bf16) for _ in range(E)]))
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = experts(H, I), experts(H, I), experts(I, H)
+    layer_bytes = sum(a.nbytes for a in (Bg, Sg, Bu, Su, Bd, Sd))
+    streamed = layer_bytes * len(np.unique(ids)) // E  # the distinct experts touched (int2_moe/main.cpp:322-328)
+    sets, W = rotation(torch, [dev32(torch, Bg), dev16(torch, Sg, bf16), dev32(torch, Bu), dev16(torch, Su, bf16),
+                               dev32(torch, Bd), dev16(torch, Sd, bf16)], layer_bytes)
+    dX, dRW = dev16(torch, X, bf16), dev16(torch, RW, bf16)
+    dids = torch.from_numpy(ids).cuda()
+    dO = torch.empty((Tk, H), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(T.int2_moe_decode_ws_bytes(Tk, topk, H, I), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def call():
+        bg, sg, bu, su, bd, sd = W[it[0] % sets]
+        it[0] += 1
+        T.int2_moe_decode(dX, dids, dRW, Tk, E, topk, H, I, bg, sg, bu, su, bd, sd, dO, ws)
+    call()
+    torch.cuda.synchronize()
+    got = formats.dt_to_f32(dO.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    ref = orc.moe_ref_tokens(X, ids, RW, 0, Tk, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16, round_up=False)
+    rel = float(np.abs(got - ref).max() / np.abs(ref).max())
+    us = graph_time_us(torch, call, 2 * sets)
+    gbs = streamed / us / 1e3
+    return {"workload": "int2 MoE decode layer T=1 E=128 top-8 H=2048 I=768 bf16 (gate/up, silu*up, down, combine)",
+            "value": round(gbs, 1), "unit": "GB/s", "us": round(us, 2), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "streamed_weight_bytes": int(streamed), "layers_rotated": sets,
+            "check_rel_err": rel, "check_pass": rel < 1e-2}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -561,6 +602,8 @@ def main():
         extra["c4"] = bench_c4(torch, T, synth, formats, orc)
         torch.cuda.empty_cache()
         extra["c5"] = bench_c5(torch, T, synth, formats, orc)
+        torch.cuda.empty_cache()
+        extra["c6"] = bench_c6(torch, T, synth, formats, orc)
         torch.cuda.empty_cache()
 
     traffic = None

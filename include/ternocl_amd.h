@@ -250,6 +250,23 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
                                         const uint32_t *Bd, const void *Sd, void *O, void *ws,
                                         size_t ws_bytes, void *stream);
 
+/* ---- int2 MoE decode layer ------------------------------------------------
+ * Replaces int2_moe_gate_up + int2_moe_down + int2_moe_reduce
+ * (int2_moe/int2_moe.cl:61-133, the sequence of int2_moe/main.cpp:226-261): for
+ * every assignment g = t * topk + j with expert e = ids[g],
+ *   Hs[g] = DT(silu(X[t] . Bg[e]) * (X[t] . Bu[e]))   (fp32 products, one rounding)
+ *   O[t]  = DT(sum_j RW[g] * (Hs[g] . Bd[e]))          (fp32, j order)
+ * The weight GEMVs run on the fp8 x fp4 decode engine, one launch for gate and up,
+ * one for down.  Same tensors as ternocl_int2_moe_prefill (X DT [T, H], ids int32
+ * [T, topk], RW DT [T, topk], experts stacked); an id outside [0, E) contributes
+ * nothing.  ws: ternocl_int2_moe_decode_ws_bytes() bytes, 256-byte aligned;
+ * T * topk < 32768, H and I multiples of 128, X 16-byte aligned. */
+size_t ternocl_int2_moe_decode_ws_bytes(int T, int topk, int H, int I);
+ternocl_status ternocl_int2_moe_decode(int dtype, const void *X, const int *ids, const void *RW, int T,
+                                       int E, int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                       const uint32_t *Bu, const void *Su, const uint32_t *Bd,
+                                       const void *Sd, void *O, void *ws, size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -229,11 +229,14 @@ def moe_combine(Y, inv, RW, T, topk, N, bf16: bool):
     return O
 
 
-def moe_ref_tokens(X, ids, RW, T0, T1, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16: bool):
+def moe_ref_tokens(X, ids, RW, T0, T1, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16: bool,
+                   round_up: bool = True):
+    """round_up: the prefill check (up rounded to DT first, int2_moe/prefill.cpp:306);
+    False: the decode check (int2_moe/main.cpp:280)."""
     O = np.empty((T1 - T0, H), np.float64)
     orc().orc_moe_ref_tokens(int(bf16), _p(_u16(X)), _p(np.ascontiguousarray(ids, np.int32)),
                              _p(_u16(RW)), T0, T1, topk, H, I, _p(_u32(Bg)), _p(_u16(Sg)),
-                             _p(_u32(Bu)), _p(_u16(Su)), _p(_u32(Bd)), _p(_u16(Sd)), _p(O))
+                             _p(_u32(Bu)), _p(_u16(Su)), _p(_u32(Bd)), _p(_u16(Sd)), _p(O), int(round_up))
     return O
 
 

@@ -458,11 +458,13 @@ static inline float moe_w(int bf16, const uint32_t *B, const uint16_t *S, int K,
 }
 
 /* int2_moe/prefill.cpp:291-315: double-precision reference of tokens
- * [T0, T1): O[(t - T0) * H + n]. */
+ * [T0, T1): O[(t - T0) * H + n].  round_up = 1: the up product is rounded to DT
+ * before silu(gate) * up (the prefill check); 0: it is not (the decode check,
+ * int2_moe/main.cpp:276-281). */
 void orc_moe_ref_tokens(int bf16, const uint16_t *X, const int *ids, const uint16_t *RW, int T0,
                         int T1, int topk, int H, int I, const uint32_t *Bg, const uint16_t *Sg,
                         const uint32_t *Bu, const uint16_t *Su, const uint32_t *Bd,
-                        const uint16_t *Sd, double *O) {
+                        const uint16_t *Sd, double *O, int round_up) {
 #pragma omp parallel for schedule(dynamic, 1)
     for (int t = T0; t < T1; ++t) {
         double *o = O + (size_t)(t - T0) * H;
@@ -477,7 +479,7 @@ void orc_moe_ref_tokens(int bf16, const uint16_t *X, const int *ids, const uint1
                     sg += x * moe_w(bf16, Bg, Sg, H, I, e, k, n);
                     su += x * moe_w(bf16, Bu, Su, H, I, e, k, n);
                 }
-                const float up = orc_tof(orc_fromf((float)su, bf16), bf16);
+                const double up = round_up ? (double)orc_tof(orc_fromf((float)su, bf16), bf16) : su;
                 h[n] = orc_tof(orc_fromf((float)(sg / (1.0 + exp(-sg)) * up), bf16), bf16);
             }
             for (int n = 0; n < H; ++n) {

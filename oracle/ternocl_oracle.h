@@ -83,7 +83,7 @@ void orc_moe_combine(int bf16, const float *Y, const int *inv, const uint16_t *R
 void orc_moe_ref_tokens(int bf16, const uint16_t *X, const int *ids, const uint16_t *RW, int T0,
                         int T1, int topk, int H, int I, const uint32_t *Bg, const uint16_t *Sg,
                         const uint32_t *Bu, const uint16_t *Su, const uint32_t *Bd,
-                        const uint16_t *Sd, double *O);
+                        const uint16_t *Sd, double *O, int round_up);
 
 #ifdef __cplusplus
 }

@@ -270,3 +270,18 @@ def int2_moe_prefill(X, ids, RW, T: int, E: int, topk: int, H: int, I: int, Bg, 
     _check(lib().ternocl_int2_moe_prefill(_dtype_of(X), _ptr(X), _ptr(ids), _ptr(RW), T, E, topk, H, I,
                                           _ptr(Bg), _ptr(Sg), _ptr(Bu), _ptr(Su), _ptr(Bd), _ptr(Sd), _ptr(O),
                                           _ptr(ws), _nbytes(ws), _stream(stream)))
+
+
+# ---- int2 MoE decode (int2_moe/int2_moe.cl) -------------------------------------
+
+def int2_moe_decode_ws_bytes(T: int, topk: int, H: int, I: int) -> int:
+    return lib().ternocl_int2_moe_decode_ws_bytes(T, topk, H, I)
+
+
+def int2_moe_decode(X, ids, RW, T: int, E: int, topk: int, H: int, I: int, Bg, Sg, Bu, Su, Bd, Sd, O,
+                    ws, stream=None) -> None:
+    """One MoE decode layer: gate/up GEMVs with silu * up, down GEMVs, weighted sum over the
+    topk experts (int2_moe/int2_moe.cl:61-133, main.cpp:226-261)."""
+    _check(lib().ternocl_int2_moe_decode(_dtype_of(X), _ptr(X), _ptr(ids), _ptr(RW), T, E, topk, H, I,
+                                         _ptr(Bg), _ptr(Sg), _ptr(Bu), _ptr(Su), _ptr(Bd), _ptr(Sd), _ptr(O),
+                                         _ptr(ws), _nbytes(ws), _stream(stream)))

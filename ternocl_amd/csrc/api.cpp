@@ -84,6 +84,11 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
                                int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                                const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
                                void *O, void *ws, hipStream_t st);
+size_t moe_decode_ws_bytes(int T, int topk, int H, int I);
+ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                              int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                              const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                              void *O, void *ws, hipStream_t st);
 // kernels (misc.hip)
 ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st);
 
@@ -387,6 +392,29 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
     if (!ws || ws_bytes < moe_ws_layout(T, E, topk, H, I).total)
         FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_prefill_ws_bytes() bytes");
     return moe_prefill_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws, (hipStream_t)stream);
+}
+
+size_t ternocl_int2_moe_decode_ws_bytes(int T, int topk, int H, int I) {
+    if (T < 1 || topk < 1 || H < 1 || I < 1) return 0;
+    return moe_decode_ws_bytes(T, topk, H, I);
+}
+
+ternocl_status ternocl_int2_moe_decode(int dtype, const void *X, const int *ids, const void *RW, int T,
+                                       int E, int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                       const uint32_t *Bu, const void *Su, const uint32_t *Bd,
+                                       const void *Sd, void *O, void *ws, size_t ws_bytes, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!X || !ids || !RW || !Bg || !Sg || !Bu || !Su || !Bd || !Sd || !O)
+        FAIL(TERNOCL_ERR_INVALID_ARG, "X, ids, RW, the six weight tensors and O must be non-null");
+    if (T < 1 || E < 1 || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need T, E, topk >= 1");
+    if (H % 128 || I % 128) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "H and I must be multiples of 128");
+    if ((size_t)T * topk > 32767) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "T * topk must be below 32768 (decode)");
+    if (((uintptr_t)X & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "X must be 16-byte aligned");
+    if (!ws || ws_bytes < moe_decode_ws_bytes(T, topk, H, I))
+        FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_decode_ws_bytes() bytes");
+    if (((uintptr_t)ws & 255) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "ws must be 256-byte aligned");
+    return moe_decode_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

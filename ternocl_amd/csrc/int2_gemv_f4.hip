@@ -294,12 +294,24 @@ __device__ __forceinline__ int f4_loads_after_barrier() {
 // long-K shapes, whose activation staging is the bulk of the VALU work), else 8.
 __host__ __device__ constexpr int f4_max_waves(int mr, int cpl) { return mr == 1 && cpl == 1 ? 16 : 8; }
 
-template <int MR, int CPL, int GPW, bool BF16>
+// Grouped mode (the MoE decode GEMVs, int2_moe/int2_moe.cl:61-174): row v =
+// blockIdx.y of the launch is pair g = v mod G of weight set v / G (set 1 =
+// B2 / S2) with expert e = ids[g] of the stacked experts [E][K/16][N] /
+// [E][K/128][N], activation row g / adiv of A (rows of K), and writes fp32 row
+// v of C.  A pair whose expert id lies outside [0, E) writes zeros.
+struct F4Group {
+    const int *ids;
+    int G, E, adiv;
+    const uint32_t *B2;
+    const uint16_t *S2;
+};
+
+template <int MR, int CPL, int GPW, bool BF16, bool GRP = false>
 __global__ void __launch_bounds__(64 * f4_max_waves(MR, CPL))
 k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ S, void *__restrict__ C,
                const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
-               int K, int postop, int out_f32, int swz) {
+               int K, int postop, int out_f32, int swz, F4Group grp = F4Group{}) {
     constexpr int RS = kF4RowStride, RR = RS * MR, P = f4_pieces(BF16);
     static_assert(RR <= 16, "too many MFMA rows");
     extern __shared__ uint8_t lds8[];
@@ -315,6 +327,21 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         strip = (((qq >> 1) << 3) + x) * 2 + (qq & 1);
     }
     const int n0 = strip * 16 * CPL + CPL * c;
+    if constexpr (GRP) {  // (uniform per workgroup: no wave returns alone)
+        const int v = blockIdx.y, set = v >= grp.G ? 1 : 0, g = v - set * grp.G;
+        const int e = grp.ids[g];
+        float *crow = (float *)C + (size_t)v * N;
+        if (e < 0 || e >= grp.E) {
+            if (wave == 0 && q == 0)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) crow[n0 + j] = 0.0f;
+            return;
+        }
+        A += (size_t)(g / grp.adiv) * K;
+        B = (set ? grp.B2 : B) + (size_t)e * (K / 16) * N;
+        S = (set ? grp.S2 : S) + (size_t)e * (K / kGS) * N;
+        C = crow;
+    }
     constexpr int WB = f4_window_bytes(RR, GPW);
     const int nbuf = windows > 1 ? 2 : 1;
     uint8_t *wlds = lds8 + (size_t)wave * nbuf * WB;
@@ -529,6 +556,33 @@ hipError_t f4_launch(const F4Plan &p, const void *A, const uint32_t *B, const vo
     }
 }
 
+template <int CPL, int GPW, bool BF16>
+hipError_t f4_group_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
+                             int rows, int N, int K, const F4Group &grp, hipStream_t st) {
+    const int strips = N / (16 * CPL);
+    hipLaunchKernelGGL((k_int2_gemv_f4<1, CPL, GPW, BF16, true>), dim3(strips, rows), dim3(64 * p.waves), p.lds,
+                       st, (const uint16_t *)A, B, (const uint16_t *)S, C, nullptr, nullptr, 1, N, K, 0, 1, 0,
+                       grp);
+    return hipGetLastError();
+}
+
+template <bool BF16>
+hipError_t f4_group_launch(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C, int rows,
+                           int N, int K, const F4Group &grp, hipStream_t st) {
+    if (p.cpl == 2) {
+        switch (p.gpw) {
+        case 1: return f4_group_launch_t<2, 1, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+        case 2: return f4_group_launch_t<2, 2, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+        default: return f4_group_launch_t<2, 4, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+        }
+    }
+    switch (p.gpw) {
+    case 1: return f4_group_launch_t<1, 1, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+    case 2: return f4_group_launch_t<1, 2, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+    default: return f4_group_launch_t<1, 4, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+    }
+}
+
 // Decode hook: the two fp4 dwords the kernel builds from each word,
 // D[word][0] = rows 0, 2, .., 14, D[word][1] = rows 1, 3, .., 15 (e2m1 2v).
 __global__ void k_int2_f4_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, size_t words) {
@@ -597,6 +651,27 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
     }
     const hipError_t e = bf16 ? f4_launch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st)
                               : f4_launch<false>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return launch_status(e);
+}
+
+// The grouped GEMVs of the MoE decode: C fp32 [rows][N], rows = G (one weight
+// set) or 2G (B / S for pairs 0..G-1, B2 / S2 for G..2G-1); A rows of K, row
+// g / adiv for pair g; experts ids[g] of [E][K/16][N] weights.  Tiles: the
+// automatic M = 1 tile with at most 4 groups per wave and 1 or 2 columns per lane.
+ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, int G, int E, int adiv,
+                                      const uint32_t *B, const void *S, const uint32_t *B2, const void *S2,
+                                      float *C, int rows, int N, int K, hipStream_t st) {
+    F4Plan p = f4_plan(dtype == TERNOCL_BF16, 1, N, K, 0, 0, 0);
+    if (p.cpl > 2 || p.gpw > 4 || p.waves > 8) {
+        p = f4_plan(dtype == TERNOCL_BF16, 1, N, K, 8, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw);
+    }
+    if (N % (16 * p.cpl) || p.lds > kF4MaxLds) {
+        set_error("grouped GEMV: N must be a multiple of 16 and the tile must fit in LDS");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    const F4Group grp{ids, G, E, adiv, B2, (const uint16_t *)S2};
+    const hipError_t e = dtype == TERNOCL_BF16 ? f4_group_launch<true>(p, A, B, S, C, rows, N, K, grp, st)
+                                               : f4_group_launch<false>(p, A, B, S, C, rows, N, K, grp, st);
     return launch_status(e);
 }
 

@@ -210,9 +210,10 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
     float s[4] = {0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < topk; ++j) {
         const int g = t * topk + j;
-        if (inv[g] < 0) continue;  // a dropped assignment (expert id out of range)
+        const int row = inv ? inv[g] : g;  // no inv: Y in assignment order (the decode layer)
+        if (row < 0) continue;  // a dropped assignment (expert id out of range)
         const float w = dt2f<BF16>(RW[g]);
-        const float4 y = *(const float4 *)(Y + (size_t)inv[g] * N + n);
+        const float4 y = *(const float4 *)(Y + (size_t)row * N + n);
         s[0] += w * y.x;
         s[1] += w * y.y;
         s[2] += w * y.z;
@@ -222,6 +223,17 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
     o.x = f2dt<BF16>(s[0]) | (f2dt<BF16>(s[1]) << 16);
     o.y = f2dt<BF16>(s[2]) | (f2dt<BF16>(s[3]) << 16);
     *(uint2 *)(O + (size_t)t * N + n) = o;
+}
+
+// The decode layer's gate/up product, int2_moe/int2_moe.cl:95:
+// Hs[g, n] = DT(a * sigmoid(a) * u), a = GU[g, n] (gate, fp32), u = GU[G + g, n] (up, fp32).
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+k_moe_silu_mul(const float *__restrict__ GU, uint16_t *__restrict__ Hs, int count) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const float a = GU[i], u = GU[(size_t)count + i];
+    Hs[i] = (uint16_t)f2dt<BF16>(a * sigmoid_ref(a) * u);
 }
 
 }  // namespace
@@ -282,6 +294,43 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
     if ((s = moe_gate_up_run(dtype, meta, X, perm, topk, Bu, Su, Bg, Sg, Hs, E, G, I, H, st)) != TERNOCL_OK) return s;
     if ((s = moe_gemm_run(dtype, meta, Hs, nullptr, 1, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK) return s;
     return moe_combine_run(dtype, Y, inv, RW, O, T, topk, H, st);
+}
+
+// ---- MoE decode layer (int2_moe/int2_moe.cl, the sequence of int2_moe/main.cpp:226-261) ----
+ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, int G, int E, int adiv,
+                                      const uint32_t *B, const void *S, const uint32_t *B2, const void *S2,
+                                      float *C, int rows, int N, int K, hipStream_t st);  // int2_gemv_f4.hip
+
+// Workspace: GU fp32 [2G][I] | Hs DT [G][I] | Y fp32 [G][H], each 256-byte aligned.
+size_t moe_decode_ws_bytes(int T, int topk, int H, int I) {
+    const size_t G = (size_t)T * topk;
+    return align_up(2 * G * I * 4, 256) + align_up(G * I * 2, 256) + align_up(G * H * 4, 256);
+}
+
+// gate and up: one grouped GEMV launch over 2G rows (fp32); Hs = DT(silu(gate) * up);
+// down: one grouped GEMV over G rows (fp32 Y, row g = assignment g); combine:
+// O[t] = DT(sum_j RW[g] * Y[g]) in j order (the reference's down * rw + reduce).
+ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                              int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                              const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                              void *O, void *ws, hipStream_t st) {
+    const int G = T * topk;
+    uint8_t *b = (uint8_t *)ws;
+    float *GU = (float *)b;
+    uint16_t *Hs = (uint16_t *)(b + align_up((size_t)2 * G * I * 4, 256));
+    float *Y = (float *)((uint8_t *)Hs + align_up((size_t)G * I * 2, 256));
+    ternocl_status s;
+    if ((s = int2_gemv_f4_group_run(dtype, X, ids, G, E, topk, Bg, Sg, Bu, Su, GU, 2 * G, I, H, st)) != TERNOCL_OK)
+        return s;
+    const int count = G * I;
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL(k_moe_silu_mul<true>, dim3((count + 255) / 256), dim3(256), 0, st, GU, Hs, count);
+    else
+        hipLaunchKernelGGL(k_moe_silu_mul<false>, dim3((count + 255) / 256), dim3(256), 0, st, GU, Hs, count);
+    if ((s = check_launch()) != TERNOCL_OK) return s;
+    if ((s = int2_gemv_f4_group_run(dtype, Hs, ids, G, E, 1, Bd, Sd, nullptr, nullptr, Y, G, H, I, st)) != TERNOCL_OK)
+        return s;
+    return moe_combine_run(dtype, Y, nullptr, RW, O, T, topk, H, st);
 }
 
 }  // namespace tcl

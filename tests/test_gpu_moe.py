@@ -245,3 +245,109 @@ def test_moe_layer_equals_stage_composition(dev, orc, bf16, I):
     T.int2_moe_combine(Y, inv, dev_dt(RW, bf16), O, Tk, topk, H)
     torch.cuda.synchronize()
     assert np.array_equal(got, host_u16(O))
+
+
+# ---- the decode layer (int2_moe/int2_moe.cl, int2_moe/main.cpp) ----------------------
+
+def _decode(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16, ws_bytes=None):
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    dO = torch.full((Tk, H), 7.0, dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    n = T.int2_moe_decode_ws_bytes(Tk, topk, H, I) if ws_bytes is None else ws_bytes
+    ws = torch.full((n,), 0x7f, dtype=torch.uint8, device="cuda")
+    T.int2_moe_decode(dev_dt(X, bf16), _ints(ids), dev_dt(RW, bf16), Tk, E, topk, H, I,
+                      dev_raw(Bg), dev_dt(Sg, bf16), dev_raw(Bu), dev_dt(Su, bf16), dev_raw(Bd),
+                      dev_dt(Sd, bf16), dO, ws)
+    torch.cuda.synchronize()
+    return host_u16(dO)
+
+
+def _oracle_decode(orc, X, ids, RW, Tk, topk, H, I, W, bf16):
+    """The decode layer from the oracle's int2 gold, stage by stage: fp32 gate and up per
+    assignment, h = DT(silu(gate) * up), fp32 down of h, then the weighted combine in slot order
+    (assignment g = t * topk + j, int2_moe/main.cpp:263-289)."""
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    G = Tk * topk
+    Y = np.zeros((G, H), np.float32)
+    for g in range(G):
+        e, x = int(ids[g]), X[g // topk: g // topk + 1]
+        gate = orc.int2_gold(x, Bg[e], Sg[e], 1, H, I, bf16).astype(np.float64)
+        up = orc.int2_gold(x, Bu[e], Su[e], 1, H, I, bf16).astype(np.float64)
+        h = formats.f32_to_dt((gate / (1.0 + np.exp(-gate)) * up).astype(np.float32), bf16)
+        Y[g] = orc.int2_gold(h, Bd[e], Sd[e], 1, I, H, bf16)[0]
+    return orc.moe_combine(Y, np.arange(G, dtype=np.int32), RW, Tk, topk, H, bf16)
+
+
+def _decode_case(seed, Tk, E, topk, H, I, bf16):
+    g = synth.rng(seed)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+    return X, ids, RW, _weights(g, E, H, I, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("Tk,E,topk,H,I", [(1, 8, 2, 256, 384), (2, 16, 4, 512, 256), (5, 6, 3, 384, 640),
+                                          (3, 32, 8, 1024, 512)])
+def test_moe_decode_matches_oracle(dev, orc, bf16, Tk, E, topk, H, I):
+    """Every output within 1e-3 + 1e-2 |ref| of the oracle's stage composition, and the
+    reference's own check (rel < 1e-2 of the double-precision layer, int2_moe/main.cpp:263-294)."""
+    import torch
+    import ternocl_amd as T
+    print(f"moe decode T={Tk} E={E} topk={topk} H={H} I={I} bf16={bf16}", flush=True)
+    X, ids, RW, W = _decode_case(100 + Tk * E + H, Tk, E, topk, H, I, bf16)
+    got = formats.dt_to_f32(_decode(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16), bf16)
+    want = formats.dt_to_f32(_oracle_decode(orc, X, ids, RW, Tk, topk, H, I, W, bf16), bf16)
+    bad, dmax = allclose_report(got, want)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    ref = orc.moe_ref_tokens(X, ids, RW, 0, Tk, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16, round_up=False)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    assert rel < 1e-2, rel
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_moe_decode_reference_default_shape(dev, orc, bf16):
+    """The reference driver's default problem (int2_moe/main.cpp:6): T=1, E=128, top-8,
+    H=2048, I=768; two runs bit-identical."""
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H, I = 1, 128, 8, 2048, 768
+    X, ids, RW, W = _decode_case(77, Tk, E, topk, H, I, bf16)
+    out = _decode(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16)
+    got = formats.dt_to_f32(out, bf16)
+    bad, dmax = allclose_report(got, formats.dt_to_f32(_oracle_decode(orc, X, ids, RW, Tk, topk, H, I, W, bf16),
+                                                       bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    ref = orc.moe_ref_tokens(X, ids, RW, 0, Tk, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16, round_up=False)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-2
+    assert np.array_equal(out, _decode(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16))
+
+
+def test_moe_decode_out_of_range_ids_add_nothing(dev, orc):
+    """An id outside [0, E) contributes zero: the layer equals the oracle's with that slot's
+    weight set to 0 (the prefill route drops such ids the same way)."""
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H, I, bf16 = 4, 12, 4, 256, 256, True
+    X, ids, RW, W = _decode_case(9, Tk, E, topk, H, I, bf16)
+    bad_ids = ids.copy()
+    bad_ids[[1, 6, 7, 12]] = [-1, E, E + 100, -5]
+    got = formats.dt_to_f32(_decode(T, torch, X, bad_ids, RW, Tk, E, topk, H, I, W, bf16), bf16)
+    ok_ids, rw0 = ids.copy(), RW.copy()
+    ok_ids[[1, 6, 7, 12]] = 0
+    rw0[[1, 6, 7, 12]] = 0
+    want = formats.dt_to_f32(_oracle_decode(orc, X, ok_ids, rw0, Tk, topk, H, I, W, bf16), bf16)
+    bad, dmax = allclose_report(got, want)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+def test_moe_decode_rejects_bad_arguments(dev):
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H, I, bf16 = 2, 4, 2, 256, 256, False
+    X, ids, RW, W = _decode_case(3, Tk, E, topk, H, I, bf16)
+    need = T.int2_moe_decode_ws_bytes(Tk, topk, H, I)
+    with pytest.raises(T.TernoclError):
+        _decode(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16, ws_bytes=need - 256)
+    with pytest.raises(T.TernoclError):
+        _decode(T, torch, X[:, :192], ids, RW, Tk, E, topk, 192, I, W, bf16)

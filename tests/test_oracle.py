@@ -335,6 +335,7 @@ def test_moe_ref_tokens_vs_dense(orc):
     Su = np.stack([synth.scales(g, H, I, False) for _ in range(E)])
     Sd = np.stack([synth.scales(g, I, H, False) for _ in range(E)])
     O = orc.moe_ref_tokens(X, ids, RW, 0, T, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, False)
+    Od = orc.moe_ref_tokens(X, ids, RW, 0, T, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, False, round_up=False)
 
     def W(B, S, K):
         return formats.unpack_int2(B, K).astype(np.float64) * np.repeat(formats.dt_to_f32(S, False), 128, axis=0)
@@ -349,3 +350,7 @@ def test_moe_ref_tokens_vs_dense(orc):
             h = sg / (1 + np.exp(-sg)) * su
             o += (h @ W(Bd[e], Sd[e], I)) * rw[t * topk + j]
         assert np.allclose(O[t], o, rtol=2e-2, atol=2e-3 * np.abs(o).max())
+        # the decode check (up not rounded): the same within its one DT rounding of h
+        assert np.allclose(Od[t], o, rtol=2e-2, atol=2e-3 * np.abs(o).max())
+    # and the two modes differ only through up's rounding: tiny, but not zero
+    assert 0 < np.abs(Od - O).max() <= 2e-2 * np.abs(O).max()
