@@ -445,6 +445,51 @@ def bench_c6(torch, T, synth, formats, orc):
             "check_rel_err": rel, "check_pass": rel < 1e-2}
 
 
+def bench_c7(torch, T, synth, formats, orc):
+    """s8 x s2 decode GEMV (int2_int8_gemv, QMODE 0 and 1) at M=1 on the GEMV workload shapes,
+    bf16, weight sets rotated: quant_a on its own and the GEMV, rates on the reference
+    byte model with the int8 activations and their scales in place of the DT activations."""
+    out = {}
+    for i, (K, N) in enumerate(SHAPES):
+        M, bf16 = 1, True
+        g = synth.rng(700 + i)
+        A = synth.activations(g, (M, K), bf16)
+        B, SB = synth.int2_weights(g, K, N), synth.scales(g, K, N, bf16)
+        set_bytes = B.nbytes + SB.nbytes
+        sets, W = rotation(torch, [dev32(torch, B), dev16(torch, SB, bf16)], set_bytes)
+        dA = dev16(torch, A, bf16)
+        dSA = torch.empty((K // 128, T.ldsa(M)), dtype=torch.bfloat16, device="cuda")
+        dAq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        dC = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        T.quant_a(dA, dSA, dAq, M, K)
+        it = [0]
+
+        def upfront():
+            b, sb = W[it[0] % sets]
+            it[0] += 1
+            T.int2_int8_gemm(None, dAq, dSA, b, sb, dC, None, None, M, N, K)
+
+        def in_gemv():
+            b, sb = W[it[0] % sets]
+            it[0] += 1
+            T.int2_int8_gemm(dA, None, dSA, b, sb, dC, None, None, M, N, K)
+        upfront()
+        torch.cuda.synchronize()
+        want = orc.int8_gold(A, B, orc.scale_a(A, M, K, bf16), SB, M, K, N, bf16)
+        got = formats.dt_to_f32(dC.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+        d = np.abs(got - want)
+        bad = int((d > 1e-3 + 1e-2 * np.abs(want)).sum())
+        q_us = graph_time_us(torch, lambda: T.quant_a(dA, dSA, None, M, K), 50)
+        u_us = graph_time_us(torch, upfront, 2 * sets)
+        i_us = graph_time_us(torch, in_gemv, 2 * sets)
+        nbytes = M * K + (K // 128) * M * 2 + K * N / 4 + (K // 128) * N * 2 + M * N * 2
+        out[f"m1_k{K}_n{N}"] = {"gemv_us": round(u_us, 2), "gemv_GB/s": round(nbytes / u_us / 1e3, 1),
+                                "hbm_frac": round(nbytes / u_us / 1e3 / HBM_PEAK_GBS, 4),
+                                "in_gemv_quant_us": round(i_us, 2), "quant_a_scales_only_us": round(q_us, 2),
+                                "parity_bad": bad, "layers_rotated": sets}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -604,6 +649,8 @@ def main():
         extra["c5"] = bench_c5(torch, T, synth, formats, orc)
         torch.cuda.empty_cache()
         extra["c6"] = bench_c6(torch, T, synth, formats, orc)
+        torch.cuda.empty_cache()
+        extra["int8_gemv"] = bench_c7(torch, T, synth, formats, orc)
         torch.cuda.empty_cache()
 
     traffic = None

@@ -40,6 +40,11 @@ ternocl_status int2_mfma_decode_run(int dtype, const uint32_t *B, uint32_t *D, i
                                     hipStream_t st);
 // kernels (int2_gemv_f4.hip)
 bool int2_gemv_f4_supports(int M, int N, const void *A);
+bool int2_int8_gemv_supports(int M, int N, int K, const void *A, const int8_t *Aq);
+ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                  const uint32_t *B, const void *SB, void *C, const void *Other,
+                                  const void *Bias, int M, int N, int K, int postop, int out_f32,
+                                  hipStream_t st);
 ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                 const void *Other, const void *Bias, int M, int N, int K, int postop,
                                 int out_f32, int waves, int cpl, int gpw, hipStream_t st);
@@ -227,6 +232,9 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
     if (!Aq && !A) FAIL(TERNOCL_ERR_INVALID_ARG, "Aq (upfront quantization) or A (in-GEMM quantization) must be non-null");
     ternocl_status s = check_gemm_common(dtype, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
+    if (int2_int8_gemv_supports(M, N, K, A, Aq))  // decode: the fp8 x fp4 block-scaled GEMV
+        return int2_int8_gemv_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
+                                  (hipStream_t)stream);
     return int2_int8_gemm_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
                               (hipStream_t)stream);
 }

@@ -75,6 +75,17 @@ __device__ __forceinline__ void f4_decode(uint32_t w, uint32_t &d0, uint32_t &d1
     d1 = w & 0xCCCCCCCCu;
 }
 
+// The s8 x s2 contract's decode (the int8 modes): code 2 reads as -2, the
+// nibble 1110 (e2m1 -4.0 = 2 * -2); codes 0, 1, 3 as in f4_decode.  Bit 2r+1
+// of t is set where row r holds code 2 (b1 = 1, b0 = 0).
+__device__ __forceinline__ void f4_decode_s2(uint32_t w, uint32_t &d0, uint32_t &d1) {
+    f4_decode(w, d0, d1);
+    const uint32_t t = w & ~(w << 1);
+    const uint32_t me = t & 0x22222222u, mo = t & 0x88888888u;  // even rows, odd rows
+    d0 |= me | (me << 1);
+    d1 |= (mo >> 1) | (mo >> 2);
+}
+
 // E8M0 exponent (biased, 1..254) of the scale that maps a block whose
 // largest magnitude has fp32 biased exponent e into [1, 2): 2^(e - 127).
 __device__ __forceinline__ uint32_t f4_scale_exp(uint32_t maxbits) {
@@ -123,20 +134,33 @@ __host__ __device__ constexpr int f4_window_bytes(int rr, int gpw) { return (gpw
 // A[m, 128 g + 8u .. + 7] of row m < MR, window group gl < GPW, u < 16; task
 // idx = (m * GPW + gl) * 16 + u; lane takes idx = lane + 64 t.  A quad of
 // lanes holds one 32-activation block (u = 4b .. 4b + 3).
-template <int MR, int GPW, bool BF16> struct F4Stage {
-    static constexpr int P = f4_pieces(BF16), RS = kF4RowStride, RR = RS * MR;
+// QM (the int8 modes of the s8 x s2 GEMV): 0 = DT activations; 1 = int8 Aq
+// (8 bytes per task); 2 = DT activations quantized here with SA[g, m] exactly
+// as quant_a does (q = sat(rne(a * sa)), NaN -> 0).  An int8 value takes 2
+// pieces, exactly: |q| <= 127 puts the block scale at <= 2^6, piece 0 keeps q's
+// top 4 bits, and the residual is an integer of magnitude <= 2^(e_q - 4) <= 4,
+// a multiple of s/16 that e4m3 holds.
+template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
+    static constexpr int P = QM ? 2 : f4_pieces(BF16), RS = kF4RowStride, RR = RS * MR;
     static constexpr int T = MR * GPW * 16, TPL = (T + 63) / 64;
     uint4 raw[TPL];
+    uint32_t sar[QM ? TPL : 1];
     // Unconditional loads (row and group clamped into range): a load under a
     // branch is waited for at the branch's end.
     __device__ __forceinline__ void load(const uint16_t *__restrict__ A, int M, int K, int groups, int g0,
-                                         int lane) {
+                                         int lane, const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
 #pragma unroll
         for (int t = 0; t < TPL; ++t) {
             const int idx = lane + 64 * t, u = idx & 15, mg = idx >> 4;
             const int m = mg / GPW, gl = mg % GPW;
             const int mc = m < M ? m : M - 1, g = g0 + gl < groups ? g0 + gl : groups - 1;
-            raw[t] = *(const uint4 *)(A + (size_t)mc * K + (size_t)g * kGS + 8 * u);
+            if constexpr (QM == 1) {
+                const uint2 v = *(const uint2 *)((const int8_t *)A + (size_t)mc * K + (size_t)g * kGS + 8 * u);
+                raw[t] = make_uint4(v.x, v.y, 0u, 0u);
+            } else {
+                raw[t] = *(const uint4 *)(A + (size_t)mc * K + (size_t)g * kGS + 8 * u);
+            }
+            if constexpr (QM != 0) sar[t] = SA[(size_t)g * ldsa + mc];
         }
     }
     __device__ __forceinline__ void store(uint8_t *data, int lane) const {
@@ -147,16 +171,36 @@ template <int MR, int GPW, bool BF16> struct F4Stage {
             const bool live = idx < T;
             const uint32_t w[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
             float f[8];
+            if constexpr (QM == 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f[2 * i] = dt2f<BF16>(w[i] & 0xffffu);
-                f[2 * i + 1] = dt2f<BF16>(w[i] >> 16);
+                for (int i = 0; i < 8; ++i) f[i] = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3)));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f[2 * i] = dt2f<BF16>(w[i] & 0xffffu);
+                    f[2 * i + 1] = dt2f<BF16>(w[i] >> 16);
+                }
+            }
+            if constexpr (QM == 2) {
+                const float sa = dt2f<BF16>(sar[t]);  // quant_a's scale, as the quantization uses it
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {  // the product is exact; |a * sa| <= 127.06
+                    const float pq = f[i] * sa;
+                    f[i] = pq == pq ? fminf(fmaxf(__builtin_rintf(pq), -128.0f), 127.0f) : 0.0f;
+                }
             }
             float r[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) r[i] = f[i];
             const int row0 = (gl * RR + RS * m) * 128 + f4_byte_off(u);
             const int srow0 = GPW * RR * 128 + (gl * RR + RS * m) * 4 + (u >> 2);
+            if constexpr (QM != 0) {
+                // 1 / SA[g, m] for the fold, in the scale slot of piece row
+                // RS m + 2, which the two int8 pieces leave unused
+                const float sa = dt2f<BF16>(sar[t]);
+                if (live && u == 0)
+                    *(float *)(data + GPW * RR * 128 + (gl * RR + RS * m + 2) * 4) = sa != 0.0f ? 1.0f / sa : 0.0f;
+            }
             uint32_t se = 0;
 #pragma unroll
             for (int p = 0; p < P; ++p) {
@@ -226,6 +270,7 @@ template <int CPL, int GPW> struct F4Slab {
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
             const int g = g0w + gi < groups ? g0w + gi : groups - 1;
+
 #pragma unroll
             for (int t = 0; t < 2; ++t) w[gi][t].load(B + ((size_t)g * 8 + 2 * q + t) * N + n0);
             if constexpr (CPL == 4) {
@@ -306,13 +351,18 @@ struct F4Group {
     const uint16_t *S2;
 };
 
-template <int MR, int CPL, int GPW, bool BF16, bool GRP = false>
+// QM != 0: the s8 x s2 GEMV (int2_int8_dpas.cl:213-215): S is SB, SA [K/128]
+// [ldsa] the activation scales, A int8 (QM 1) or DT quantized while staged (QM
+// 2); per group and column acc += float(dot) * (SB * (1 / SA)), the int32 dot
+// exact (piece rows 4m, 4m + 1 sum to 2 dot).
+template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0>
 __global__ void __launch_bounds__(64 * f4_max_waves(MR, CPL))
 k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ S, void *__restrict__ C,
                const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
-               int K, int postop, int out_f32, int swz, F4Group grp = F4Group{}) {
-    constexpr int RS = kF4RowStride, RR = RS * MR, P = f4_pieces(BF16);
+               int K, int postop, int out_f32, int swz, F4Group grp = F4Group{},
+               const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
+    constexpr int RS = kF4RowStride, RR = RS * MR, P = QM ? 2 : f4_pieces(BF16);
     static_assert(RR <= 16, "too many MFMA rows");
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
@@ -347,8 +397,8 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     uint8_t *wlds = lds8 + (size_t)wave * nbuf * WB;
     const int rho = c & (RR - 1);  // A row (piece row) this lane feeds; rows >= RR are don't-care
 
-    F4Stage<MR, GPW, BF16> st;
-    st.load(A, M, K, groups, wave * GPW, lane);
+    F4Stage<MR, GPW, BF16, QM> st;
+    st.load(A, M, K, groups, wave * GPW, lane, SA, ldsa);
     int after = f4_loads_after_barrier();
     F4Slab<CPL, GPW> cur;
     cur.load(B + after, S + after, N, groups, wave * GPW, q, n0);
@@ -356,7 +406,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     ein.load(Other, Bias, postop, out_f32, M, N, q, n0, wave == 0);
     st.store(wlds, lane);
 
-    constexpr int ROWS = P;  // live result rows of lane q: the pieces of row m = q
+    constexpr int ROWS = QM ? 1 : P;  // accumulators per column: the pieces of row m = q, or their sum
     float acc[CPL][ROWS];
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -369,7 +419,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         const bool more = win + 1 < windows;
         F4Slab<CPL, GPW> nxt;
         if (more) {
-            st.load(A, M, K, groups, (win + 1) * gw + wave * GPW, lane);
+            st.load(A, M, K, groups, (win + 1) * gw + wave * GPW, lane, SA, ldsa);
             after = f4_loads_after_barrier();
             nxt.load(B + after, S + after, N, groups, (win + 1) * gw + wave * GPW, q, n0);
         }
@@ -382,17 +432,30 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             const int sa = buf[GPW * RR * 128 + (gi * RR + rho) * 4 + q];
             const v8i_t av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                               (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            float inv = 0.0f;  // int8 modes: 1 / SA[g, m] of row m = q (clamped into the rows staged)
+            if constexpr (QM != 0)
+                inv = *(const float *)(buf + GPW * RR * 128 + (gi * RR + RS * (q < MR ? q : MR - 1) + 2) * 4);
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 uint32_t d0, d1, e0, e1;
-                f4_decode(cur.w[gi][0].v[j], d0, d1);
-                f4_decode(cur.w[gi][1].v[j], e0, e1);
+                if constexpr (QM != 0) {
+                    f4_decode_s2(cur.w[gi][0].v[j], d0, d1);
+                    f4_decode_s2(cur.w[gi][1].v[j], e0, e1);
+                } else {
+                    f4_decode(cur.w[gi][0].v[j], d0, d1);
+                    f4_decode(cur.w[gi][1].v[j], e0, e1);
+                }
                 const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
                 const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                     av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa, 0, 127);
                 const float s = dt2f<BF16>(cur.scale(gi, j));
+                if constexpr (QM != 0) {
+                    const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
+                    acc[j][0] += dot * (s * inv);
+                } else {
 #pragma unroll
-                for (int i = 0; i < ROWS; ++i) acc[j][i] = d[i] * s + acc[j][i];
+                    for (int i = 0; i < ROWS; ++i) acc[j][i] = d[i] * s + acc[j][i];
+                }
             }
         }
         if (more) {
@@ -409,10 +472,14 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     float out[CPL][OPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        float t = acc[j][0];
+        if constexpr (QM != 0) {
+            out[j][0] = acc[j][0];
+        } else {
+            float t = acc[j][0];
 #pragma unroll
-        for (int i = 1; i < P; ++i) t += acc[j][i];
-        out[j][0] = t * 0.5f;
+            for (int i = 1; i < P; ++i) t += acc[j][i];
+            out[j][0] = t * 0.5f;
+        }
     }
     const bool live = q < QV;
     if (W > 1) {
@@ -583,6 +650,59 @@ hipError_t f4_group_launch(const F4Plan &p, const void *A, const uint32_t *B, co
     }
 }
 
+// The s8 x s2 GEMV launches: QM 1 (A = Aq, int8) or 2 (A = DT, quantized
+// while staged); tiles of <= 2 columns per lane and <= 4 groups per wave.
+template <int MR, int CPL, int GPW, bool BF16, int QM>
+hipError_t f4q_launch_t(const F4Plan &p, const void *A, const void *SA, int ldsa, const uint32_t *B,
+                        const void *S, void *C, const void *Other, const void *Bias, int M, int N, int K,
+                        int postop, int out_f32, hipStream_t st) {
+    const int strips = N / (16 * CPL);
+    const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
+    hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QM>), dim3(strips), dim3(64 * p.waves), p.lds,
+                       st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N,
+                       K, postop, out_f32, swz, F4Group{}, (const uint16_t *)SA, ldsa);
+    return hipGetLastError();
+}
+
+template <int MR, bool BF16, int QM>
+hipError_t f4q_launch_m(const F4Plan &p, const void *A, const void *SA, int ldsa, const uint32_t *B,
+                        const void *S, void *C, const void *Other, const void *Bias, int M, int N, int K,
+                        int postop, int out_f32, hipStream_t st) {
+#define TCL_F4Q(CPL, GPW) \
+    return f4q_launch_t<MR, CPL, GPW, BF16, QM>(p, A, SA, ldsa, B, S, C, Other, Bias, M, N, K, postop, out_f32, st)
+    switch (p.cpl * 10 + p.gpw) {
+    case 11: TCL_F4Q(1, 1);
+    case 12: TCL_F4Q(1, 2);
+    case 14: TCL_F4Q(1, 4);
+    case 21: TCL_F4Q(2, 1);
+    case 22: TCL_F4Q(2, 2);
+    case 24: TCL_F4Q(2, 4);
+    default: return hipErrorInvalidValue;
+    }
+#undef TCL_F4Q
+}
+
+template <bool BF16, int QM>
+hipError_t f4q_launch(const F4Plan &p, const void *A, const void *SA, int ldsa, const uint32_t *B, const void *S,
+                      void *C, const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
+                      hipStream_t st) {
+    switch (p.mr) {
+    case 1: return f4q_launch_m<1, BF16, QM>(p, A, SA, ldsa, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 2: return f4q_launch_m<2, BF16, QM>(p, A, SA, ldsa, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    default: return f4q_launch_m<4, BF16, QM>(p, A, SA, ldsa, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    }
+}
+
+// The s8 x s2 GEMV's tile: the automatic one (<= 2 columns per lane, <= 4
+// groups per wave; 16 waves only with 1 column per lane and M = 1, which the
+// kernel's launch bounds allow).
+F4Plan f4q_plan(int M, int N, int K) {
+    F4Plan p = f4_plan(false, M, N, K, 0, 0, 0);
+    if (p.cpl > 2 || p.gpw > 4)
+        p = f4_plan(false, M, N, K, p.waves, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw);
+    return p;
+}
+
 // Decode hook: the two fp4 dwords the kernel builds from each word,
 // D[word][0] = rows 0, 2, .., 14, D[word][1] = rows 1, 3, .., 15 (e2m1 2v).
 __global__ void k_int2_f4_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, size_t words) {
@@ -651,6 +771,37 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
     }
     const hipError_t e = bf16 ? f4_launch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st)
                               : f4_launch<false>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return launch_status(e);
+}
+
+// Whether the s8 x s2 GEMV takes a call: M <= 4; N a multiple of 16 (32 when
+// the tile takes 2 columns per lane); Aq 8-byte or A 16-byte aligned; C,
+// Other and Bias byte offsets below 2^31.
+bool int2_int8_gemv_supports(int M, int N, int K, const void *A, const int8_t *Aq) {
+    if (M < 1 || M > kF4MaxM || N % 16 || (size_t)M * N * 4 >= 0x7ff00000u) return false;
+    if (Aq ? ((uintptr_t)Aq & 7) != 0 : ((uintptr_t)A & 15) != 0) return false;
+    const F4Plan p = f4q_plan(M, N, K);
+    return N % (16 * p.cpl) == 0 && p.lds <= kF4MaxLds;
+}
+
+ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                  const uint32_t *B, const void *SB, void *C, const void *Other,
+                                  const void *Bias, int M, int N, int K, int postop, int out_f32,
+                                  hipStream_t st) {
+    if (!int2_int8_gemv_supports(M, N, K, A, Aq)) {
+        set_error("the s8 x s2 GEMV takes M <= 4, N % 16 == 0 and aligned activations");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    const F4Plan p = f4q_plan(M, N, K);
+    const int ldsa = (M + 31) & ~31;
+    const bool bf16 = dtype == TERNOCL_BF16;
+    hipError_t e;
+    if (Aq)
+        e = bf16 ? f4q_launch<true, 1>(p, Aq, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+                 : f4q_launch<false, 1>(p, Aq, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else
+        e = bf16 ? f4q_launch<true, 2>(p, A, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+                 : f4q_launch<false, 2>(p, A, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
     return launch_status(e);
 }
 

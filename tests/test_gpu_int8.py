@@ -232,3 +232,72 @@ def test_int8_gemm_in_gemm_quantization(dev, orc, M, K, N, bf16):
     want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, 5, False)
     bad, dmax = allclose_report(formats.dt_to_f32(host_u16(ig), bf16), formats.dt_to_f32(want, bf16))
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+# ---- M <= 4: the s8 x s2 decode GEMV (int2_int8_dpas.cl:213-215) ------------------
+
+DECODE_SHAPES = [(1, 128, 16), (1, 4096, 14336), (2, 14336, 4096), (3, 2048, 1040), (4, 4096, 4096),
+                 (4, 256, 48), (1, 5376, 21504)]
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 16), (1, 14336, 1024), (2, 4096, 4096), (3, 1024, 48), (4, 2048, 12288)])
+def test_int8_gemv_group_dots_exact(dev, M, K, N):
+    """With SA = SB = 1 and fp32 output the GEMV returns sum_k Aq * v exactly (integers below
+    2^24): the int8 pieces, the two's-complement decode of every code (2 = -2) and the k
+    order, checked bit for bit over the whole int8 range."""
+    import torch
+    import ternocl_amd as T
+    print(f"int8 gemv exact dots M={M} K={K} N={N}", flush=True)
+    g = synth.rng(600 + M * K + N)
+    Aq = g.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = g.integers(0, 2**32, size=(K // 16, N), dtype=np.uint32)
+    one = formats.f32_to_dt(np.ones(1, np.float32), False)[0]
+    SA = np.full((K // 128, T.ldsa(M)), one, np.uint16)
+    SB = np.full((K // 128, N), one, np.uint16)
+    dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    T.int2_int8_gemm(None, torch.from_numpy(Aq).cuda(), dev_dt(SA, False), dev_raw(B), dev_dt(SB, False), dC,
+                     None, None, M, N, K, 0, True)
+    torch.cuda.synchronize()
+    shifts = np.arange(16, dtype=np.uint32) * 2
+    codes = ((B[:, None, :] >> shifts[None, :, None]) & 3).astype(np.int64).reshape(K, N)
+    v = np.where(codes >= 2, codes - 4, codes)
+    want = Aq.astype(np.int64) @ v
+    assert np.array_equal(dC.cpu().numpy(), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", DECODE_SHAPES)
+def test_int8_gemv_parity(dev, orc, M, K, N, bf16):
+    """M <= 4 against the oracle's s8 x s2 gold within 1e-3 + 1e-2 |ref|, the reference
+    driver's A ~ U[-5, 5] and every code; the in-GEMV quantization (QMODE 1) gives the upfront
+    mode's C bit for bit."""
+    import torch
+    import ternocl_amd as T
+    print(f"int8 gemv M={M} K={K} N={N} bf16={bf16}", flush=True)
+    A, B, SB, other, bias_f = _int8_case(5000 + M + N, M, K, N, bf16, ref_dist=True, all_codes=True)
+    dA, dSA, dAq = _quant(T, torch, A, M, K, bf16)
+    dB, dSB = dev_raw(B), dev_dt(SB, bf16)
+    up = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+    ig = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+    T.int2_int8_gemm(None, dAq, dSA, dB, dSB, up, None, None, M, N, K, 0, False)
+    T.int2_int8_gemm(dA, None, dSA, dB, dSB, ig, None, None, M, N, K, 0, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(up), host_u16(ig))
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, 0, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(up), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_int8_gemv_epilogues(dev, orc, bf16, postop, out_f32):
+    import torch
+    import ternocl_amd as T
+    M, K, N = 2, 1024, 528
+    A, B, SB, other, bias_f = _int8_case(70 + postop, M, K, N, bf16)
+    got = _int8_run(T, torch, A, B, SB, other, bias_f, M, K, N, bf16, postop, out_f32)
+    got = got.cpu().numpy() if out_f32 else host_u16(got)
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, postop, out_f32)
+    bad, dmax = allclose_report(_as_f32(got, out_f32, bf16), _as_f32(want, out_f32, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
