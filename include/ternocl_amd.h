@@ -135,7 +135,10 @@ ternocl_status ternocl_quant_a(int dtype, const void *A, void *SA, int8_t *Aq, i
  * quant_a's for every finite input, so both modes give identical C.
  * SB: DT [K/128, N]; B, C, Other, Bias, postop and out_f32 as
  * ternocl_int2_fp16_upcvt_gemm.  Any M >= 1; the A operand (M*K elements of
- * Aq or A) and B must each be below 2^31 bytes. */
+ * Aq or A) and B must each be below 2^31 bytes.  M <= 4 with N % 16 == 0 (Aq
+ * 8-byte or A 16-byte aligned) runs the decode GEMV (the reference's
+ * int2_int8_gemv): the same exact group dot products and the same fold, with
+ * the groups of a column summed in a different order than the tile GEMM. */
 ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                       const uint32_t *B, const void *SB, void *C,
                                       const void *Other, const void *Bias, int M, int N, int K,
