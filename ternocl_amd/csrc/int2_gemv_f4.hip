@@ -140,11 +140,16 @@ __host__ __device__ constexpr int f4_window_bytes(int rr, int gpw) { return (gpw
 // pieces, exactly: |q| <= 127 puts the block scale at <= 2^6, piece 0 keeps q's
 // top 4 bits, and the residual is an integer of magnitude <= 2^(e_q - 4) <= 4,
 // a multiple of s/16 that e4m3 holds.
+// QM 3 (the MoE decode's down GEMV): A is fp32, gate rows, with the up rows
+// ldsa floats further; the activation is h = DT(gate * sigmoid(gate) * up),
+// the reference's rounding point (int2_moe/int2_moe.cl:95).
 template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
-    static constexpr int P = QM ? 2 : f4_pieces(BF16), RS = kF4RowStride, RR = RS * MR;
+    static constexpr bool I8 = QM == 1 || QM == 2;
+    static constexpr int P = I8 ? 2 : f4_pieces(BF16), RS = kF4RowStride, RR = RS * MR;
     static constexpr int T = MR * GPW * 16, TPL = (T + 63) / 64;
-    uint4 raw[TPL];
-    uint32_t sar[QM ? TPL : 1];
+    uint4 raw[QM == 3 ? 1 : TPL];
+    float4 gu[QM == 3 ? TPL : 1][4];  // QM 3: gate 8, up 8
+    uint32_t sar[I8 ? TPL : 1];
     // Unconditional loads (row and group clamped into range): a load under a
     // branch is waited for at the branch's end.
     __device__ __forceinline__ void load(const uint16_t *__restrict__ A, int M, int K, int groups, int g0,
@@ -154,13 +159,19 @@ template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
             const int idx = lane + 64 * t, u = idx & 15, mg = idx >> 4;
             const int m = mg / GPW, gl = mg % GPW;
             const int mc = m < M ? m : M - 1, g = g0 + gl < groups ? g0 + gl : groups - 1;
-            if constexpr (QM == 1) {
+            if constexpr (QM == 3) {
+                const float *ga = (const float *)A + (size_t)mc * K + (size_t)g * kGS + 8 * u;
+                gu[t][0] = *(const float4 *)ga;
+                gu[t][1] = *(const float4 *)(ga + 4);
+                gu[t][2] = *(const float4 *)(ga + ldsa);
+                gu[t][3] = *(const float4 *)(ga + ldsa + 4);
+            } else if constexpr (QM == 1) {
                 const uint2 v = *(const uint2 *)((const int8_t *)A + (size_t)mc * K + (size_t)g * kGS + 8 * u);
                 raw[t] = make_uint4(v.x, v.y, 0u, 0u);
             } else {
                 raw[t] = *(const uint4 *)(A + (size_t)mc * K + (size_t)g * kGS + 8 * u);
             }
-            if constexpr (QM != 0) sar[t] = SA[(size_t)g * ldsa + mc];
+            if constexpr (I8) sar[t] = SA[(size_t)g * ldsa + mc];
         }
     }
     __device__ __forceinline__ void store(uint8_t *data, int lane) const {
@@ -169,9 +180,17 @@ template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
             const int idx = lane + 64 * t, u = idx & 15, mg = idx >> 4;
             const int m = mg / GPW, gl = mg % GPW;
             const bool live = idx < T;
-            const uint32_t w[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
+            const uint32_t w[4] = {raw[QM == 3 ? 0 : t].x, raw[QM == 3 ? 0 : t].y, raw[QM == 3 ? 0 : t].z,
+                                   raw[QM == 3 ? 0 : t].w};
             float f[8];
-            if constexpr (QM == 1) {
+            if constexpr (QM == 3) {
+                const float ga[8] = {gu[t][0].x, gu[t][0].y, gu[t][0].z, gu[t][0].w,
+                                     gu[t][1].x, gu[t][1].y, gu[t][1].z, gu[t][1].w};
+                const float ua[8] = {gu[t][2].x, gu[t][2].y, gu[t][2].z, gu[t][2].w,
+                                     gu[t][3].x, gu[t][3].y, gu[t][3].z, gu[t][3].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] = dt2f<BF16>(f2dt<BF16>(ga[i] * sigmoid_ref(ga[i]) * ua[i]));
+            } else if constexpr (QM == 1) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) f[i] = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3)));
             } else {
@@ -194,7 +213,7 @@ template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
             for (int i = 0; i < 8; ++i) r[i] = f[i];
             const int row0 = (gl * RR + RS * m) * 128 + f4_byte_off(u);
             const int srow0 = GPW * RR * 128 + (gl * RR + RS * m) * 4 + (u >> 2);
-            if constexpr (QM != 0) {
+            if constexpr (I8) {
                 // 1 / SA[g, m] for the fold, in the scale slot of piece row
                 // RS m + 2, which the two int8 pieces leave unused
                 const float sa = dt2f<BF16>(sar[t]);
@@ -344,32 +363,44 @@ __host__ __device__ constexpr int f4_max_waves(int mr, int cpl) { return mr == 1
 // B2 / S2) with expert e = ids[g] of the stacked experts [E][K/16][N] /
 // [E][K/128][N], activation row g / adiv of A (rows of K), and writes fp32 row
 // v of C.  A pair whose expert id lies outside [0, E) writes zeros.
+// DS (the decode layer's down launch with its weighted sum, the reference's
+// int2_moe_down_sum, int2_moe/int2_moe.cl:133-174): workgroup (strip,
+// token t), wave j = slot j: its own GEMV over all of K for pair g = t topk + j
+// (expert ids[g], activation row g of the QM 3 staging); wave 0 then writes
+// O[t] = DT(sum_j RW[g] * y_j) in slot order (fp32 products and sums, no
+// contraction, as k_moe_combine).  A slot whose id lies outside [0, E)
+// streams expert 0 and contributes y = 0.
 struct F4Group {
     const int *ids;
     int G, E, adiv;
     const uint32_t *B2;
     const uint16_t *S2;
+    int topk;
+    const uint16_t *RW;
+    uint16_t *O;
 };
 
 // QM != 0: the s8 x s2 GEMV (int2_int8_dpas.cl:213-215): S is SB, SA [K/128]
 // [ldsa] the activation scales, A int8 (QM 1) or DT quantized while staged (QM
 // 2); per group and column acc += float(dot) * (SB * (1 / SA)), the int32 dot
 // exact (piece rows 4m, 4m + 1 sum to 2 dot).
-template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0>
+template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0, bool DS = false>
 __global__ void __launch_bounds__(64 * f4_max_waves(MR, CPL))
 k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ S, void *__restrict__ C,
                const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
                int K, int postop, int out_f32, int swz, F4Group grp = F4Group{},
                const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
-    constexpr int RS = kF4RowStride, RR = RS * MR, P = QM ? 2 : f4_pieces(BF16);
+    constexpr bool I8 = QM == 1 || QM == 2;
+    constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
     static_assert(RR <= 16, "too many MFMA rows");
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int groups = K / kGS;
-    const int gw = W * GPW;
+    const int gw = DS ? GPW : W * GPW;   // groups per window (DS: each wave covers all of K)
+    const int g0w = DS ? 0 : wave * GPW;  // this wave's first group of a window
     const int windows = (groups + gw - 1) / gw;
     int strip = blockIdx.x;
     if (swz) {  // strips 2j, 2j+1 (sharing 128-byte lines) on the same XCD
@@ -377,7 +408,16 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         strip = (((qq >> 1) << 3) + x) * 2 + (qq & 1);
     }
     const int n0 = strip * 16 * CPL + CPL * c;
-    if constexpr (GRP) {  // (uniform per workgroup: no wave returns alone)
+    bool dead = false;  // DS: this wave's slot has no expert
+    if constexpr (DS) {
+        const int g = blockIdx.y * grp.topk + wave;
+        int e = grp.ids[g];
+        dead = e < 0 || e >= grp.E;
+        e = dead ? 0 : e;
+        A = (const uint16_t *)((const float *)A + (size_t)g * K);
+        B += (size_t)e * (K / 16) * N;
+        S += (size_t)e * (K / kGS) * N;
+    } else if constexpr (GRP) {  // (uniform per workgroup: no wave returns alone)
         const int v = blockIdx.y, set = v >= grp.G ? 1 : 0, g = v - set * grp.G;
         const int e = grp.ids[g];
         float *crow = (float *)C + (size_t)v * N;
@@ -387,7 +427,10 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 for (int j = 0; j < CPL; ++j) crow[n0 + j] = 0.0f;
             return;
         }
-        A += (size_t)(g / grp.adiv) * K;
+        if constexpr (QM == 3)
+            A = (const uint16_t *)((const float *)A + (size_t)g * K);
+        else
+            A += (size_t)(g / grp.adiv) * K;
         B = (set ? grp.B2 : B) + (size_t)e * (K / 16) * N;
         S = (set ? grp.S2 : S) + (size_t)e * (K / kGS) * N;
         C = crow;
@@ -398,15 +441,15 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int rho = c & (RR - 1);  // A row (piece row) this lane feeds; rows >= RR are don't-care
 
     F4Stage<MR, GPW, BF16, QM> st;
-    st.load(A, M, K, groups, wave * GPW, lane, SA, ldsa);
+    st.load(A, M, K, groups, g0w, lane, SA, ldsa);
     int after = f4_loads_after_barrier();
     F4Slab<CPL, GPW> cur;
-    cur.load(B + after, S + after, N, groups, wave * GPW, q, n0);
+    cur.load(B + after, S + after, N, groups, g0w, q, n0);
     F4EpiIn<MR, CPL, BF16> ein;  // behind the weights: waited for only at the epilogue
     ein.load(Other, Bias, postop, out_f32, M, N, q, n0, wave == 0);
     st.store(wlds, lane);
 
-    constexpr int ROWS = QM ? 1 : P;  // accumulators per column: the pieces of row m = q, or their sum
+    constexpr int ROWS = I8 ? 1 : P;  // accumulators per column: the pieces of row m = q, or their sum
     float acc[CPL][ROWS];
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -419,13 +462,13 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         const bool more = win + 1 < windows;
         F4Slab<CPL, GPW> nxt;
         if (more) {
-            st.load(A, M, K, groups, (win + 1) * gw + wave * GPW, lane, SA, ldsa);
+            st.load(A, M, K, groups, (win + 1) * gw + g0w, lane, SA, ldsa);
             after = f4_loads_after_barrier();
-            nxt.load(B + after, S + after, N, groups, (win + 1) * gw + wave * GPW, q, n0);
+            nxt.load(B + after, S + after, N, groups, (win + 1) * gw + g0w, q, n0);
         }
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
-            const int g = win * gw + wave * GPW + gi;
+            const int g = win * gw + g0w + gi;
             if (g >= groups) break;  // uniform across the wave
             const uint8_t *row = buf + (gi * RR + rho) * 128 + 32 * q;
             const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
@@ -433,12 +476,12 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             const v8i_t av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                               (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
             float inv = 0.0f;  // int8 modes: 1 / SA[g, m] of row m = q (clamped into the rows staged)
-            if constexpr (QM != 0)
+            if constexpr (I8)
                 inv = *(const float *)(buf + GPW * RR * 128 + (gi * RR + RS * (q < MR ? q : MR - 1) + 2) * 4);
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 uint32_t d0, d1, e0, e1;
-                if constexpr (QM != 0) {
+                if constexpr (I8) {
                     f4_decode_s2(cur.w[gi][0].v[j], d0, d1);
                     f4_decode_s2(cur.w[gi][1].v[j], e0, e1);
                 } else {
@@ -449,7 +492,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                     av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa, 0, 127);
                 const float s = dt2f<BF16>(cur.scale(gi, j));
-                if constexpr (QM != 0) {
+                if constexpr (I8) {
                     const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
                     acc[j][0] += dot * (s * inv);
                 } else {
@@ -472,7 +515,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     float out[CPL][OPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        if constexpr (QM != 0) {
+        if constexpr (I8) {
             out[j][0] = acc[j][0];
         } else {
             float t = acc[j][0];
@@ -482,6 +525,26 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         }
     }
     const bool live = q < QV;
+    if constexpr (DS) {  // y_j of every slot, then wave 0's weighted sum in slot order
+        float *red = (float *)(lds8 + (size_t)nbuf * W * WB);  // [W][CPL][16]
+        if (live)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) red[(wave * CPL + j) * 16 + c] = dead ? 0.0f : out[j][0];
+        __syncthreads();
+        if (wave != 0 || !live) return;
+        const int t = blockIdx.y;
+        float sum[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) sum[j] = 0.0f;
+        for (int w2 = 0; w2 < W; ++w2) {
+            const float rw = dt2f<BF16>(grp.RW[t * grp.topk + w2]);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) sum[j] = __fadd_rn(sum[j], __fmul_rn(rw, red[(w2 * CPL + j) * 16 + c]));
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) grp.O[(size_t)t * N + n0 + j] = (uint16_t)f2dt<BF16>(sum[j]);
+        return;
+    }
     if (W > 1) {
         float *red = (float *)(lds8 + (size_t)nbuf * W * WB);  // [W-1][CPL][QV*16][OPL]
         constexpr int JS = QV * 16 * OPL;
@@ -623,30 +686,32 @@ hipError_t f4_launch(const F4Plan &p, const void *A, const uint32_t *B, const vo
     }
 }
 
-template <int CPL, int GPW, bool BF16>
+// QM 3: the down GEMV of the decode layer (A = fp32 gate rows, up rows
+// up_off floats further).  DS: one workgroup per (strip, token), a wave per slot.
+template <int CPL, int GPW, bool BF16, int QM, bool DS>
 hipError_t f4_group_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
-                             int rows, int N, int K, const F4Group &grp, hipStream_t st) {
+                             int rows, int N, int K, const F4Group &grp, int up_off, hipStream_t st) {
     const int strips = N / (16 * CPL);
-    hipLaunchKernelGGL((k_int2_gemv_f4<1, CPL, GPW, BF16, true>), dim3(strips, rows), dim3(64 * p.waves), p.lds,
-                       st, (const uint16_t *)A, B, (const uint16_t *)S, C, nullptr, nullptr, 1, N, K, 0, 1, 0,
-                       grp);
+    hipLaunchKernelGGL((k_int2_gemv_f4<1, CPL, GPW, BF16, true, QM, DS>), dim3(strips, rows), dim3(64 * p.waves),
+                       p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, nullptr, nullptr, 1, N, K, 0, 1,
+                       0, grp, nullptr, up_off);
     return hipGetLastError();
 }
 
-template <bool BF16>
+template <bool BF16, int QM, bool DS>
 hipError_t f4_group_launch(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C, int rows,
-                           int N, int K, const F4Group &grp, hipStream_t st) {
-    if (p.cpl == 2) {
+                           int N, int K, const F4Group &grp, int up_off, hipStream_t st) {
+    if (!DS && p.cpl == 2) {
         switch (p.gpw) {
-        case 1: return f4_group_launch_t<2, 1, BF16>(p, A, B, S, C, rows, N, K, grp, st);
-        case 2: return f4_group_launch_t<2, 2, BF16>(p, A, B, S, C, rows, N, K, grp, st);
-        default: return f4_group_launch_t<2, 4, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+        case 1: return f4_group_launch_t<2, 1, BF16, QM, DS>(p, A, B, S, C, rows, N, K, grp, up_off, st);
+        case 2: return f4_group_launch_t<2, 2, BF16, QM, DS>(p, A, B, S, C, rows, N, K, grp, up_off, st);
+        default: return f4_group_launch_t<2, 4, BF16, QM, DS>(p, A, B, S, C, rows, N, K, grp, up_off, st);
         }
     }
     switch (p.gpw) {
-    case 1: return f4_group_launch_t<1, 1, BF16>(p, A, B, S, C, rows, N, K, grp, st);
-    case 2: return f4_group_launch_t<1, 2, BF16>(p, A, B, S, C, rows, N, K, grp, st);
-    default: return f4_group_launch_t<1, 4, BF16>(p, A, B, S, C, rows, N, K, grp, st);
+    case 1: return f4_group_launch_t<1, 1, BF16, QM, DS>(p, A, B, S, C, rows, N, K, grp, up_off, st);
+    case 2: return f4_group_launch_t<1, 2, BF16, QM, DS>(p, A, B, S, C, rows, N, K, grp, up_off, st);
+    default: return f4_group_launch_t<1, 4, BF16, QM, DS>(p, A, B, S, C, rows, N, K, grp, up_off, st);
     }
 }
 
@@ -809,20 +874,55 @@ ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, co
 // set) or 2G (B / S for pairs 0..G-1, B2 / S2 for G..2G-1); A rows of K, row
 // g / adiv for pair g; experts ids[g] of [E][K/16][N] weights.  Tiles: the
 // automatic M = 1 tile with at most 4 groups per wave and 1 or 2 columns per lane.
-ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, int G, int E, int adiv,
+static F4Plan f4_group_plan(int N, int K) {
+    F4Plan p = f4_plan(false, 1, N, K, 0, 0, 0);
+    if (p.cpl > 2 || p.gpw > 4 || p.waves > 8) p = f4_plan(false, 1, N, K, 8, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw);
+    return p;
+}
+
+// The down launch with the weighted sum (DS): topk waves (<= 16), one column
+// per lane, each wave's groups in windows of up to 4.
+static F4Plan f4_down_sum_plan(int K, int topk) {
+    const int groups = K / kGS;
+    F4Plan p;
+    p.mr = 1;
+    p.cpl = 1;
+    p.waves = topk;
+    p.gpw = groups >= 3 ? 4 : groups;
+    const int windows = (groups + p.gpw - 1) / p.gpw;
+    p.lds = (size_t)(windows > 1 ? 2 : 1) * topk * f4_window_bytes(kF4RowStride, p.gpw) + (size_t)topk * 16 * 4;
+    return p;
+}
+
+// The decode layer's grouped GEMVs (fp32 weights of the MoE experts [E][K/16][N]):
+// mode 0, gate/up: C [2G][N] = rows of X (row g / topk for pair g) times gate
+//   (rows < G) or up (B2 / S2, rows >= G) of expert ids[g];
+// mode 1, down: C [G][N] = h times down, h = DT(silu(gate) * up) staged from
+//   the fp32 rows A = mode 0's C;
+// mode 2, down with the weighted sum (topk <= 16): O [T][N] directly.
+ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, int G, int E, int topk,
                                       const uint32_t *B, const void *S, const uint32_t *B2, const void *S2,
-                                      float *C, int rows, int N, int K, hipStream_t st) {
-    F4Plan p = f4_plan(dtype == TERNOCL_BF16, 1, N, K, 0, 0, 0);
-    if (p.cpl > 2 || p.gpw > 4 || p.waves > 8) {
-        p = f4_plan(dtype == TERNOCL_BF16, 1, N, K, 8, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw);
-    }
-    if (N % (16 * p.cpl) || p.lds > kF4MaxLds) {
-        set_error("grouped GEMV: N must be a multiple of 16 and the tile must fit in LDS");
+                                      float *C, int N, int K, const void *RW, void *O, int mode,
+                                      hipStream_t st) {
+    const bool bf16 = dtype == TERNOCL_BF16;
+    const F4Plan p = mode == 2 ? f4_down_sum_plan(K, topk) : f4_group_plan(N, K);
+    if (N % (16 * p.cpl) || p.lds > kF4MaxLds || (mode == 2 && (topk < 1 || topk > 16))) {
+        set_error("grouped GEMV: N must be a multiple of 16, the tile must fit in LDS, topk <= 16 for the fused sum");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
-    const F4Group grp{ids, G, E, adiv, B2, (const uint16_t *)S2};
-    const hipError_t e = dtype == TERNOCL_BF16 ? f4_group_launch<true>(p, A, B, S, C, rows, N, K, grp, st)
-                                               : f4_group_launch<false>(p, A, B, S, C, rows, N, K, grp, st);
+    const F4Group grp{ids, G, E, mode == 0 ? topk : 1, B2, (const uint16_t *)S2, topk, (const uint16_t *)RW,
+                      (uint16_t *)O};
+    const int up_off = G * K;  // modes 1, 2: floats from a gate row to its up row
+    hipError_t e;
+    if (mode == 0)
+        e = bf16 ? f4_group_launch<true, 0, false>(p, A, B, S, C, 2 * G, N, K, grp, 0, st)
+                 : f4_group_launch<false, 0, false>(p, A, B, S, C, 2 * G, N, K, grp, 0, st);
+    else if (mode == 1)
+        e = bf16 ? f4_group_launch<true, 3, false>(p, A, B, S, C, G, N, K, grp, up_off, st)
+                 : f4_group_launch<false, 3, false>(p, A, B, S, C, G, N, K, grp, up_off, st);
+    else
+        e = bf16 ? f4_group_launch<true, 3, true>(p, A, B, S, C, G / topk, N, K, grp, up_off, st)
+                 : f4_group_launch<false, 3, true>(p, A, B, S, C, G / topk, N, K, grp, up_off, st);
     return launch_status(e);
 }
 

@@ -225,17 +225,6 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
     *(uint2 *)(O + (size_t)t * N + n) = o;
 }
 
-// The decode layer's gate/up product, int2_moe/int2_moe.cl:95:
-// Hs[g, n] = DT(a * sigmoid(a) * u), a = GU[g, n] (gate, fp32), u = GU[G + g, n] (up, fp32).
-template <bool BF16>
-__global__ void __launch_bounds__(256)
-k_moe_silu_mul(const float *__restrict__ GU, uint16_t *__restrict__ Hs, int count) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= count) return;
-    const float a = GU[i], u = GU[(size_t)count + i];
-    Hs[i] = (uint16_t)f2dt<BF16>(a * sigmoid_ref(a) * u);
-}
-
 }  // namespace
 
 // counts, running bases and per-wave counts; with one block also perm's LDS copy
@@ -297,19 +286,24 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
 }
 
 // ---- MoE decode layer (int2_moe/int2_moe.cl, the sequence of int2_moe/main.cpp:226-261) ----
-ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, int G, int E, int adiv,
+// (int2_gemv_f4.hip)
+ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, int G, int E, int topk,
                                       const uint32_t *B, const void *S, const uint32_t *B2, const void *S2,
-                                      float *C, int rows, int N, int K, hipStream_t st);  // int2_gemv_f4.hip
+                                      float *C, int N, int K, const void *RW, void *O, int mode,
+                                      hipStream_t st);
 
-// Workspace: GU fp32 [2G][I] | Hs DT [G][I] | Y fp32 [G][H], each 256-byte aligned.
+// Workspace: gate/up fp32 [2G][I] | Y fp32 [G][H] (used when topk > 16), each
+// 256-byte aligned.
 size_t moe_decode_ws_bytes(int T, int topk, int H, int I) {
     const size_t G = (size_t)T * topk;
-    return align_up(2 * G * I * 4, 256) + align_up(G * I * 2, 256) + align_up(G * H * 4, 256);
+    return align_up(2 * G * I * 4, 256) + align_up(G * H * 4, 256);
 }
 
-// gate and up: one grouped GEMV launch over 2G rows (fp32); Hs = DT(silu(gate) * up);
-// down: one grouped GEMV over G rows (fp32 Y, row g = assignment g); combine:
-// O[t] = DT(sum_j RW[g] * Y[g]) in j order (the reference's down * rw + reduce).
+// (1) One grouped GEMV over 2G rows: gate and up of every pair, fp32.
+// (2) topk <= 16: one launch per (column strip, token), a wave per slot: down
+//     of h = DT(silu(gate) * up) (formed while staging), then
+//     O[t] = DT(sum_j RW[g] * y_g) in slot order (the reference's down_sum);
+//     topk > 16: the down GEMV into Y (fp32) and the weighted-sum kernel.
 ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
                               int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                               const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
@@ -317,18 +311,16 @@ ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const vo
     const int G = T * topk;
     uint8_t *b = (uint8_t *)ws;
     float *GU = (float *)b;
-    uint16_t *Hs = (uint16_t *)(b + align_up((size_t)2 * G * I * 4, 256));
-    float *Y = (float *)((uint8_t *)Hs + align_up((size_t)G * I * 2, 256));
+    float *Y = (float *)(b + align_up((size_t)2 * G * I * 4, 256));
     ternocl_status s;
-    if ((s = int2_gemv_f4_group_run(dtype, X, ids, G, E, topk, Bg, Sg, Bu, Su, GU, 2 * G, I, H, st)) != TERNOCL_OK)
+    if ((s = int2_gemv_f4_group_run(dtype, X, ids, G, E, topk, Bg, Sg, Bu, Su, GU, I, H, nullptr, nullptr, 0,
+                                    st)) != TERNOCL_OK)
         return s;
-    const int count = G * I;
-    if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL(k_moe_silu_mul<true>, dim3((count + 255) / 256), dim3(256), 0, st, GU, Hs, count);
-    else
-        hipLaunchKernelGGL(k_moe_silu_mul<false>, dim3((count + 255) / 256), dim3(256), 0, st, GU, Hs, count);
-    if ((s = check_launch()) != TERNOCL_OK) return s;
-    if ((s = int2_gemv_f4_group_run(dtype, Hs, ids, G, E, 1, Bd, Sd, nullptr, nullptr, Y, G, H, I, st)) != TERNOCL_OK)
+    if (topk <= 16)
+        return int2_gemv_f4_group_run(dtype, GU, ids, G, E, topk, Bd, Sd, nullptr, nullptr, nullptr, H, I, RW, O,
+                                      2, st);
+    if ((s = int2_gemv_f4_group_run(dtype, GU, ids, G, E, topk, Bd, Sd, nullptr, nullptr, Y, H, I, nullptr,
+                                    nullptr, 1, st)) != TERNOCL_OK)
         return s;
     return moe_combine_run(dtype, Y, nullptr, RW, O, T, topk, H, st);
 }

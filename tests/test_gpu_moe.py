@@ -286,10 +286,11 @@ def _decode_case(seed, Tk, E, topk, H, I, bf16):
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("Tk,E,topk,H,I", [(1, 8, 2, 256, 384), (2, 16, 4, 512, 256), (5, 6, 3, 384, 640),
-                                          (3, 32, 8, 1024, 512)])
+                                          (3, 32, 8, 1024, 512), (2, 20, 16, 256, 128), (2, 24, 20, 256, 256)])
 def test_moe_decode_matches_oracle(dev, orc, bf16, Tk, E, topk, H, I):
     """Every output within 1e-3 + 1e-2 |ref| of the oracle's stage composition, and the
-    reference's own check (rel < 1e-2 of the double-precision layer, int2_moe/main.cpp:263-294)."""
+    reference's own check (rel < 1e-2 of the double-precision layer, int2_moe/main.cpp:263-294).
+    topk <= 16 takes the fused down-and-sum launch, topk = 20 the down GEMV and the sum kernel."""
     import torch
     import ternocl_amd as T
     print(f"moe decode T={Tk} E={E} topk={topk} H={H} I={I} bf16={bf16}", flush=True)
