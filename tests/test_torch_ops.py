@@ -34,6 +34,7 @@ def test_ops_registered_and_fake_shapes():
     Bd = torch.empty((E, I // 16, H), dtype=torch.int32, device="meta")
     Sd = torch.empty((E, I // 128, H), dtype=torch.bfloat16, device="meta")
     assert ops.moe_prefill(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd).shape == (M, H)
+    assert ops.moe_decode(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd).shape == (M, H)
 
 
 @pytest.mark.gpu
@@ -87,3 +88,36 @@ def test_ops_match_direct_calls(dev, orc):
     T.hadamard_fwht(x, None, y2, 2, 1024, 512, False)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Tk,decode", [(40, False), (3, True)])
+def test_moe_ops_match_direct_calls(dev, Tk, decode):
+    """moe_prefill / moe_decode give the direct C-ABI calls' bits."""
+    import numpy as np
+    import ternocl_amd as T
+    import ternocl_amd.torch_ops  # noqa: F401
+    from ternocl_amd import synth
+    from tests.gpu_util import dev_dt, dev_raw, host_u16
+    E, topk, H, I, bf16 = 6, 2, 256, 128, True
+    g = synth.rng(91 + Tk)
+    X = dev_dt(synth.activations(g, (Tk, H), bf16), bf16)
+    ids_np, RW_np = synth.moe_routing(g, Tk, E, topk, bf16)
+    ids = torch.from_numpy(ids_np.reshape(Tk, topk)).cuda()
+    RW = dev_dt(RW_np.reshape(Tk, topk), bf16)
+
+    def experts(K, N):
+        return (dev_raw(np.stack([synth.int2_weights(g, K, N) for _ in range(E)])),
+                dev_dt(np.stack([synth.scales(g, K, N, bf16) for _ in range(E)]), bf16))
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = experts(H, I), experts(H, I), experts(I, H)
+    op = torch.ops.ternocl.moe_decode if decode else torch.ops.ternocl.moe_prefill
+    got = op(X, ids, RW, E, Bg, Sg, Bu, Su, Bd, Sd)
+    O = torch.empty_like(X)
+    if decode:
+        ws = torch.empty(T.int2_moe_decode_ws_bytes(Tk, topk, H, I), dtype=torch.uint8, device="cuda")
+        T.int2_moe_decode(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
+    else:
+        ws = torch.empty(T.int2_moe_prefill_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device="cuda")
+        T.int2_moe_prefill(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(got), host_u16(O))
