@@ -398,10 +398,25 @@ def bench_c5(torch, T, synth, formats, orc):
     us = graph_time_us(torch, call, 10)
     flops = 2.0 * Tk * topk * (2.0 * H * I + I * H)  # int2_moe/prefill.cpp:350
     tf = flops / us / 1e6
+    # the same layer on the s8 x s2 GEMM (int2_moe_prefill_int8.cl, QMODE 1)
+    ws8 = torch.empty(T.int2_moe_prefill_int8_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device="cuda")
+
+    def call8():
+        bg, sg, bu, su, bd, sd = W[it[0] % sets]
+        it[0] += 1
+        T.int2_moe_prefill_int8(dX, dids, dRW, Tk, E, topk, H, I, bg, sg, bu, su, bd, sd, dO, ws8)
+    call8()
+    torch.cuda.synchronize()
+    got8 = formats.dt_to_f32(dO.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    rel8 = float(np.abs(got8[:4] - ref).max() / np.abs(ref).max())
+    us8 = graph_time_us(torch, call8, 10)
     return {"workload": "int2 MoE prefill layer T=2048 E=64 top-8 H=2048 I=1408 bf16 (route, up, gate, down, combine)",
             "value": round(tf, 1), "unit": "TFLOPS", "us": round(us, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
             "peak": BF16_PEAK_TFLOPS, "layers_rotated": sets, "layer_weight_bytes": int(layer_bytes),
-            "check_rel_err_4_tokens": rel, "check_pass": rel < 1e-2}
+            "check_rel_err_4_tokens": rel, "check_pass": rel < 1e-2,
+            "int8": {"us": round(us8, 2), "TOPS": round(flops / us8 / 1e6, 1),
+                     "mfma_frac": round(flops / us8 / 1e6 / I8_PEAK_TOPS, 4), "peak": I8_PEAK_TOPS,
+                     "check_rel_err_4_tokens": rel8, "check_pass": rel8 < 5e-2}}
 
 
 def bench_c6(torch, T, synth, formats, orc):

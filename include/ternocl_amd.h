@@ -253,6 +253,24 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
                                         const uint32_t *Bd, const void *Sd, void *O, void *ws,
                                         size_t ws_bytes, void *stream);
 
+/* Replaces the int8 MoE prefill (int2_moe/int2_moe_prefill_int8.cl:1-191, the
+ * sequence of int2_moe/prefill.cpp:243-279 run with --int8 1): route, gather
+ * the token rows into expert order, quant_a scales of the gathered rows
+ * (ternocl_quant_a semantics, G rows), up = s8 x s2 per expert segment (POSTOP
+ * 0), h = silu(gate) * up (POSTOP 1, Other = up), quant_a scales of h, down
+ * (fp32), combine; every GEMM quantizes its rows while staging them, the
+ * reference's QMODE 1 (its QMODE 0 gives the same int8 values).  Arguments as
+ * ternocl_int2_moe_prefill; ws >= ternocl_int2_moe_prefill_int8_ws_bytes(T,
+ * E, topk, H, I) bytes, 256-byte aligned.  The gathered rows (T topk H 4
+ * bytes) and each expert's packed weights must be below 2^31 bytes.  The
+ * reference's pass rule for this layer is rel < 5e-2 (prefill.cpp:318). */
+size_t ternocl_int2_moe_prefill_int8_ws_bytes(int T, int E, int topk, int H, int I);
+ternocl_status ternocl_int2_moe_prefill_int8(int dtype, const void *X, const int *ids, const void *RW,
+                                             int T, int E, int topk, int H, int I, const uint32_t *Bg,
+                                             const void *Sg, const uint32_t *Bu, const void *Su,
+                                             const uint32_t *Bd, const void *Sd, void *O, void *ws,
+                                             size_t ws_bytes, void *stream);
+
 /* ---- int2 MoE decode layer ------------------------------------------------
  * Replaces int2_moe_gate_up + int2_moe_down + int2_moe_reduce
  * (int2_moe/int2_moe.cl:61-133, the sequence of int2_moe/main.cpp:226-261): for

@@ -27,7 +27,7 @@ __all__ = [
     "bitcos_fp16_upcvt_gemm", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
     "moe_tile_rows", "int2_moe_route", "int2_moe_gather", "int2_moe_gemm", "int2_moe_combine",
-    "int2_moe_prefill_ws_bytes", "int2_moe_prefill",
+    "int2_moe_prefill_ws_bytes", "int2_moe_prefill", "int2_moe_prefill_int8_ws_bytes", "int2_moe_prefill_int8",
 ]
 
 FP16, BF16 = 0, 1
@@ -270,6 +270,19 @@ def int2_moe_prefill(X, ids, RW, T: int, E: int, topk: int, H: int, I: int, Bg, 
     _check(lib().ternocl_int2_moe_prefill(_dtype_of(X), _ptr(X), _ptr(ids), _ptr(RW), T, E, topk, H, I,
                                           _ptr(Bg), _ptr(Sg), _ptr(Bu), _ptr(Su), _ptr(Bd), _ptr(Sd), _ptr(O),
                                           _ptr(ws), _nbytes(ws), _stream(stream)))
+
+
+def int2_moe_prefill_int8_ws_bytes(T: int, E: int, topk: int, H: int, I: int) -> int:
+    return lib().ternocl_int2_moe_prefill_int8_ws_bytes(T, E, topk, H, I)
+
+
+def int2_moe_prefill_int8(X, ids, RW, T: int, E: int, topk: int, H: int, I: int, Bg, Sg, Bu, Su, Bd, Sd, O,
+                          ws, stream=None) -> None:
+    """One MoE prefill layer on the s8 x s2 GEMM: route, gather, quant_a, up, gate (silu * up),
+    quant_a, down, combine (int2_moe/int2_moe_prefill_int8.cl, QMODE 1)."""
+    _check(lib().ternocl_int2_moe_prefill_int8(_dtype_of(X), _ptr(X), _ptr(ids), _ptr(RW), T, E, topk, H, I,
+                                               _ptr(Bg), _ptr(Sg), _ptr(Bu), _ptr(Su), _ptr(Bd), _ptr(Sd),
+                                               _ptr(O), _ptr(ws), _nbytes(ws), _stream(stream)))
 
 
 # ---- int2 MoE decode (int2_moe/int2_moe.cl) -------------------------------------

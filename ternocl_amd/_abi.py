@@ -49,6 +49,8 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_int2_moe_combine": (I, [I, P, P, P, P, I, I, I, P]),
     "ternocl_int2_moe_prefill_ws_bytes": (Z, [I, I, I, I, I]),
     "ternocl_int2_moe_prefill": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
+    "ternocl_int2_moe_prefill_int8_ws_bytes": (Z, [I, I, I, I, I]),
+    "ternocl_int2_moe_prefill_int8": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
     "ternocl_int2_moe_decode_ws_bytes": (Z, [I, I, I, I]),
     "ternocl_int2_moe_decode": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
 }

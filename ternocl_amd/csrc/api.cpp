@@ -89,6 +89,12 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
                                int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                                const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
                                void *O, void *ws, hipStream_t st);
+MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I);  // moe.hip
+ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                                    int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                    const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                                    void *O, void *ws, hipStream_t st);
+int int8_moe_tile_rows();  // int2_int8.hip
 size_t moe_decode_ws_bytes(int T, int topk, int H, int I);
 ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
                               int topk, int H, int I, const uint32_t *Bg, const void *Sg,
@@ -400,6 +406,32 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
     if (!ws || ws_bytes < moe_ws_layout(T, E, topk, H, I).total)
         FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_prefill_ws_bytes() bytes");
     return moe_prefill_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws, (hipStream_t)stream);
+}
+
+size_t ternocl_int2_moe_prefill_int8_ws_bytes(int T, int E, int topk, int H, int I) {
+    if (T < 1 || E < 1 || topk < 1 || H < 1 || I < 1) return 0;
+    return moe_i8_ws_layout(T, E, topk, H, I).total;
+}
+
+ternocl_status ternocl_int2_moe_prefill_int8(int dtype, const void *X, const int *ids, const void *RW,
+                                             int T, int E, int topk, int H, int I, const uint32_t *Bg,
+                                             const void *Sg, const uint32_t *Bu, const void *Su,
+                                             const uint32_t *Bd, const void *Sd, void *O, void *ws,
+                                             size_t ws_bytes, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!X || !ids || !RW || !Bg || !Sg || !Bu || !Su || !Bd || !Sd || !O)
+        FAIL(TERNOCL_ERR_INVALID_ARG, "X, ids, RW, the six weight tensors and O must be non-null");
+    if (T < 1 || E < 1 || E > kMoeMaxExperts || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need T, topk >= 1 and 1 <= E <= 512");
+    if (H % 128 || I % 128) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "H and I must be multiples of 128");
+    if (int8_moe_tile_rows() != moe_tile_rows()) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "int8 tile rows differ from the route's");
+    const size_t G = (size_t)T * topk;
+    if (G * H * 4 >= (1u << 31) || G * I * 2 >= (1u << 31) || (size_t)(H / 16) * I * 4 >= (1u << 31))
+        FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the gathered rows and each expert's weights must be below 2^31 bytes");
+    if (!ws || ws_bytes < moe_i8_ws_layout(T, E, topk, H, I).total)
+        FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_prefill_int8_ws_bytes() bytes");
+    return moe_prefill_int8_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws,
+                                (hipStream_t)stream);
 }
 
 size_t ternocl_int2_moe_decode_ws_bytes(int T, int topk, int H, int I) {

@@ -199,6 +199,10 @@ namespace tcl {
 struct MoeWs {
     size_t meta, perm, inv, h, y, total;
 };
+// The int8 MoE prefill layer's workspace (byte offsets, each 256-byte aligned).
+struct MoeI8Ws {
+    size_t meta, perm, inv, xs, sa1, u, h, sa2, y, total;
+};
 // Records the HIP error text for ternocl_last_error() and maps it to a status.
 ternocl_status launch_status(hipError_t e);
 ternocl_status check_launch();

@@ -352,3 +352,80 @@ def test_moe_decode_rejects_bad_arguments(dev):
         _decode(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16, ws_bytes=need - 256)
     with pytest.raises(T.TernoclError):
         _decode(T, torch, X[:, :192], ids, RW, Tk, E, topk, 192, I, W, bf16)
+
+
+# ---- the int8 prefill layer (int2_moe/int2_moe_prefill_int8.cl, QMODE 1) ----------------
+
+def _layer_int8(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16):
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    dO = torch.zeros((Tk, H), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    ws = torch.empty(T.int2_moe_prefill_int8_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device="cuda")
+    T.int2_moe_prefill_int8(dev_dt(X, bf16), _ints(ids), dev_dt(RW, bf16), Tk, E, topk, H, I,
+                            dev_raw(Bg), dev_dt(Sg, bf16), dev_raw(Bu), dev_dt(Su, bf16), dev_raw(Bd),
+                            dev_dt(Sd, bf16), dO, ws)
+    torch.cuda.synchronize()
+    return host_u16(dO)
+
+
+def _oracle_layer_int8(orc, X, ids, RW, Tk, E, topk, H, I, W, bf16, rpt):
+    """The int8 layer from the oracle's stages: expert-sorted rows, per-row quant_a scales,
+    the s8 x s2 gold for up, gate (POSTOP 1 on up) and down (fp32), the combine."""
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    G = Tk * topk
+    meta, perm, inv = orc.moe_route(ids, E, rpt)
+    Xs = X[perm // topk]
+    Y = np.zeros((G, H), np.float32)
+    for e in range(E):
+        r0, r1 = int(meta[e]), int(meta[e + 1])
+        if r0 == r1:
+            continue
+        Me, Xe = r1 - r0, Xs[r0:r1]
+        SAx = orc.scale_a(Xe, Me, H, bf16)
+        U = orc.epilogue(orc.int8_gold(Xe, Bu[e], SAx, Su[e], Me, H, I, bf16), None, None, 0, False, bf16)
+        Hs = orc.epilogue(orc.int8_gold(Xe, Bg[e], SAx, Sg[e], Me, H, I, bf16), U, None, 1, False, bf16)
+        SAh = orc.scale_a(Hs, Me, I, bf16)
+        Y[r0:r1] = orc.epilogue(orc.int8_gold(Hs, Bd[e], SAh, Sd[e], Me, I, H, bf16), None, None, 0, True, bf16)
+    return orc.moe_combine(Y, inv, RW, Tk, topk, H, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("Tk,E,topk,H,I", [(96, 8, 2, 256, 384), (300, 6, 3, 512, 256), (7, 16, 4, 384, 128)])
+def test_moe_int8_layer_matches_oracle(dev, orc, bf16, Tk, E, topk, H, I):
+    """Within 1e-3 + 1e-2 |ref| of the oracle's s8 x s2 stage composition, and the reference's
+    own int8 check on the first tokens (rel < 5e-2 of the double-precision layer,
+    int2_moe/prefill.cpp:288-319)."""
+    import torch
+    import ternocl_amd as T
+    print(f"moe int8 layer T={Tk} E={E} topk={topk} H={H} I={I} bf16={bf16}", flush=True)
+    g = synth.rng(300 + Tk + E)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+    W = _weights(g, E, H, I, bf16)
+    got = formats.dt_to_f32(_layer_int8(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16), bf16)
+    want = formats.dt_to_f32(_oracle_layer_int8(orc, X, ids, RW, Tk, E, topk, H, I, W, bf16, T.moe_tile_rows()),
+                             bf16)
+    bad, dmax = allclose_report(got, want)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    n = min(Tk, 8)
+    ref = orc.moe_ref_tokens(X, ids, RW, 0, n, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16)
+    assert np.abs(got[:n] - ref).max() / np.abs(ref).max() < 5e-2
+
+
+def test_moe_int8_layer_workload_shape(dev, orc):
+    """T=2048 tokens, 64 experts, top-8, H=2048, I=1408, bf16: the reference's int8 check on the
+    first tokens (rel < 5e-2), every output finite, two runs bit-identical."""
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H, I, bf16 = 2048, 64, 8, 2048, 1408, True
+    g = synth.rng(2026)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+    W = _weights(g, E, H, I, bf16)
+    out = _layer_int8(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16)
+    got = formats.dt_to_f32(out, bf16)
+    assert np.isfinite(got).all()
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    ref = orc.moe_ref_tokens(X, ids, RW, 0, 4, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16)
+    assert np.abs(got[:4] - ref).max() / np.abs(ref).max() < 5e-2
+    assert np.array_equal(out, _layer_int8(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16))
