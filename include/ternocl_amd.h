@@ -255,11 +255,11 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
 
 /* Replaces the int8 MoE prefill (int2_moe/int2_moe_prefill_int8.cl:1-191, the
  * sequence of int2_moe/prefill.cpp:243-279 run with --int8 1): route, gather
- * the token rows into expert order, quant_a scales of the gathered rows
+ * the token rows into expert order, quant_a of the gathered rows
  * (ternocl_quant_a semantics, G rows), up = s8 x s2 per expert segment (POSTOP
  * 0), h = silu(gate) * up (POSTOP 1, Other = up), quant_a scales of h, down
- * (fp32), combine; every GEMM quantizes its rows while staging them, the
- * reference's QMODE 1 (its QMODE 0 gives the same int8 values).  Arguments as
+ * (fp32), combine; quant_a writes the int8 rows once (the reference's QMODE 0,
+ * whose int8 values its QMODE 1 reproduces).  Arguments as
  * ternocl_int2_moe_prefill; ws >= ternocl_int2_moe_prefill_int8_ws_bytes(T,
  * E, topk, H, I) bytes, 256-byte aligned.  The gathered rows (T topk H 4
  * bytes) and each expert's packed weights must be below 2^31 bytes.  The

@@ -459,25 +459,37 @@ static hipError_t int8_gemm_launch(int dtype, const void *Asrc, const void *SA, 
     return hipGetLastError();
 }
 
-// The int8 MoE prefill's grouped GEMM (in-GEMM quantization of the DT rows A
-// [G][K] with SA [K/128][ldsa(G)]); grid: an upper bound of the row tiles
-// (each expert's ragged tail adds at most one) times the column blocks.
-ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const void *SA, const uint32_t *B,
-                                 const void *SB, void *C, const void *Other, int E, int G, int N, int K,
-                                 int postop, int out_f32, hipStream_t st) {
+// The int8 MoE prefill's grouped GEMM on the expert-sorted rows: Aq [G][K]
+// int8 from quant_a (upfront), or, Aq NULL, the DT rows A quantized while
+// staged; SA [K/128][ldsa(G)].  Grid: an upper bound of the row tiles (each
+// expert's ragged tail adds at most one) times the column blocks.
+template <bool QA>
+static hipError_t int8_moe_launch(int dtype, const int *meta, const void *Asrc, const void *SA, const uint32_t *B,
+                                  const void *SB, void *C, const void *Other, int E, int G, int N, int K,
+                                  int postop, int out_f32, hipStream_t st) {
     typedef QTile<4, 4, 2, 2> TC;
     const int ntn = (N + TC::BN - 1) / TC::BN;
     const int max_tiles = (G + TC::BM - 1) / TC::BM + E;
     const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
     if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, true, true>), grid, block, 0, st, A, (const uint16_t *)SA, B,
-                           (const uint16_t *)SB, C, (const uint16_t *)Other, nullptr, G, N, K, postop, out_f32,
-                           meta, E);
-    else
-        hipLaunchKernelGGL((k_int2_int8_gemm<TC, false, true, true>), grid, block, 0, st, A, (const uint16_t *)SA,
+        hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, QA, true>), grid, block, 0, st, Asrc, (const uint16_t *)SA,
                            B, (const uint16_t *)SB, C, (const uint16_t *)Other, nullptr, G, N, K, postop, out_f32,
                            meta, E);
-    return check_launch();
+    else
+        hipLaunchKernelGGL((k_int2_int8_gemm<TC, false, QA, true>), grid, block, 0, st, Asrc, (const uint16_t *)SA,
+                           B, (const uint16_t *)SB, C, (const uint16_t *)Other, nullptr, G, N, K, postop, out_f32,
+                           meta, E);
+    return hipGetLastError();
+}
+
+ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
+                                 const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G, int N,
+                                 int K, int postop, int out_f32, hipStream_t st) {
+    const hipError_t e = Aq ? int8_moe_launch<false>(dtype, meta, Aq, SA, B, SB, C, Other, E, G, N, K, postop,
+                                                     out_f32, st)
+                            : int8_moe_launch<true>(dtype, meta, A, SA, B, SB, C, Other, E, G, N, K, postop,
+                                                    out_f32, st);
+    return launch_status(e);
 }
 
 int int8_moe_tile_rows() { return QTile<4, 4, 2, 2>::BM; }

@@ -289,12 +289,13 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
 // int2_moe/prefill.cpp:243-279 with --int8 1) ----
 // (int2_int8.hip)
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st);
-ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const void *SA, const uint32_t *B,
-                                 const void *SB, void *C, const void *Other, int E, int G, int N, int K,
-                                 int postop, int out_f32, hipStream_t st);
+ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
+                                 const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G, int N,
+                                 int K, int postop, int out_f32, hipStream_t st);
 
 // Workspace: meta | perm | inv | Xs DT [G][H] | SA1 [H/128][ldsa(G)] | U DT [G][I] |
-// Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H], each 256-byte aligned.
+// Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [G][H] | Hq int8
+// [G][I], each 256-byte aligned.
 MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     const size_t G = (size_t)T * topk, lda = ((size_t)G + 31) & ~(size_t)31;
     MoeI8Ws w;
@@ -308,14 +309,17 @@ MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     w.h = o;    o = align_up(o + G * I * 2, 256);
     w.sa2 = o;  o = align_up(o + (size_t)(I / 128) * lda * 2, 256);
     w.y = o;    o = align_up(o + G * H * 4, 256);
+    w.xq = o;   o = align_up(o + G * H, 256);
+    w.hq = o;   o = align_up(o + G * I, 256);
     w.total = o;
     return w;
 }
 
-// route; gather the token rows into expert order; SA1 of the gathered rows
-// (quant_a, scales only); up = s8 x s2 (POSTOP 0); h = silu(gate) * up
-// (POSTOP 1, Other = up); SA2 of h; Y = s8 x s2 down (fp32); combine.  Each
-// GEMM quantizes its rows while staging them (the reference's QMODE 1).
+// route; gather the token rows into expert order; quant_a of the gathered
+// rows (SA1, Xq); up = s8 x s2 (POSTOP 0); h = silu(gate) * up (POSTOP 1,
+// Other = up); quant_a of h (SA2, Hq); Y = s8 x s2 down (fp32); combine.  The
+// int8 rows are written once (the reference's QMODE 0 with WRITE_Q); its
+// QMODE 1, quantizing in each GEMM, gives the same int8 values.
 ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
                                     int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                                     const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
@@ -325,15 +329,19 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
     int *meta = (int *)(b + w.meta), *perm = (int *)(b + w.perm), *inv = (int *)(b + w.inv);
     void *Xs = b + w.xs, *SA1 = b + w.sa1, *U = b + w.u, *Hs = b + w.h, *SA2 = b + w.sa2;
     float *Y = (float *)(b + w.y);
+    int8_t *Xq = (int8_t *)(b + w.xq), *Hq = (int8_t *)(b + w.hq);
     const int G = T * topk;
     ternocl_status s;
     if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
     if ((s = moe_gather_run(X, perm, Xs, G, H, topk, st)) != TERNOCL_OK) return s;
-    if ((s = quant_a_run(dtype, Xs, SA1, nullptr, G, H, st)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Xs, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Xs, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK) return s;
-    if ((s = quant_a_run(dtype, Hs, SA2, nullptr, G, I, st)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Hs, SA2, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK) return s;
+    if ((s = quant_a_run(dtype, Xs, SA1, Xq, G, H, st)) != TERNOCL_OK) return s;
+    if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK)
+        return s;
+    if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK)
+        return s;
+    if ((s = quant_a_run(dtype, Hs, SA2, Hq, G, I, st)) != TERNOCL_OK) return s;
+    if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Hq, SA2, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK)
+        return s;
     return moe_combine_run(dtype, Y, inv, RW, O, T, topk, H, st);
 }
 
