@@ -254,10 +254,10 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
                                         size_t ws_bytes, void *stream);
 
 /* Replaces the int8 MoE prefill (int2_moe/int2_moe_prefill_int8.cl:1-191, the
- * sequence of int2_moe/prefill.cpp:243-279 run with --int8 1): route, gather
+ * sequence of int2_moe/prefill.cpp:243-279 run with --int8 0): route, gather
  * the token rows into expert order, quant_a of the gathered rows
  * (ternocl_quant_a semantics, G rows), up = s8 x s2 per expert segment (POSTOP
- * 0), h = silu(gate) * up (POSTOP 1, Other = up), quant_a scales of h, down
+ * 0), h = silu(gate) * up (POSTOP 1, Other = up), quant_a of h, down
  * (fp32), combine; quant_a writes the int8 rows once (the reference's QMODE 0,
  * whose int8 values its QMODE 1 reproduces).  Arguments as
  * ternocl_int2_moe_prefill; ws >= ternocl_int2_moe_prefill_int8_ws_bytes(T,
