@@ -71,3 +71,30 @@ def test_status_strings():
 def test_ws_bytes_query():
     import ternocl_amd as T
     assert T.int2_gemm_ws_bytes(1, 14336, 4096) == 0  # the GEMV keeps no scratch
+
+
+@pytest.mark.parametrize("entry", ["ternocl_int2_moe_prefill", "ternocl_int2_moe_prefill_int8",
+                                   "ternocl_int2_moe_decode"])
+def test_moe_layer_host_validation(entry):
+    """The MoE layer entries reject bad arguments on the host, before any device call (the
+    pointers here are never dereferenced): a null weight, H % 128 != 0, a short workspace, and
+    for the decode layer T * topk >= 32768."""
+    import ctypes
+    import ternocl_amd as T
+    L = T.lib()
+    fn = getattr(L, entry)
+    ws_q = {"ternocl_int2_moe_prefill": lambda Tk, E, k, H, I: L.ternocl_int2_moe_prefill_ws_bytes(Tk, E, k, H, I),
+            "ternocl_int2_moe_prefill_int8": lambda Tk, E, k, H, I: L.ternocl_int2_moe_prefill_int8_ws_bytes(Tk, E, k, H, I),
+            "ternocl_int2_moe_decode": lambda Tk, E, k, H, I: L.ternocl_int2_moe_decode_ws_bytes(Tk, k, H, I)}[entry]
+    p = ctypes.c_void_p(4096)
+
+    def call(Tk=4, E=8, k=2, H=256, I=256, Bd=p, ws_bytes=None):
+        need = ws_q(Tk, E, k, H, I)
+        return fn(1, p, p, p, Tk, E, k, H, I, p, p, p, p, Bd, p, p, p, need if ws_bytes is None else ws_bytes, None)
+    assert ws_q(4, 8, 2, 256, 256) > 0
+    assert call(Bd=None) == 1  # TERNOCL_ERR_INVALID_ARG
+    assert call(H=192) == 2  # TERNOCL_ERR_UNSUPPORTED_SHAPE
+    assert call(ws_bytes=ws_q(4, 8, 2, 256, 256) - 1) == 3  # TERNOCL_ERR_WORKSPACE
+    assert L.ternocl_last_error().decode()
+    if entry == "ternocl_int2_moe_decode":
+        assert call(Tk=4096, k=8) == 2
