@@ -55,7 +55,8 @@ ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, c
                                   int postop, int out_f32, hipStream_t st);
 ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (int2_int8.hip)
-ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st);
+ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
+                           const int *perm = nullptr, int topk = 1, const int *nrows = nullptr);
 ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,

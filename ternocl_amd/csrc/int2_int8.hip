@@ -55,13 +55,17 @@ __host__ __device__ constexpr int ldsa_of(int M) { return (M + 31) & ~31; }
 template <bool BF16>
 __global__ void __launch_bounds__(256)
 k_quant_a(const uint16_t *__restrict__ A, uint16_t *__restrict__ SA, int8_t *__restrict__ Aq, int M,
-          int K) {
+          int K, const int *__restrict__ perm = nullptr, int topk = 1, const int *__restrict__ nrows = nullptr) {
     const int cpr = K >> 3;  // 8-element chunks per row (a multiple of 16)
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     // the 16 chunks of a group are 16 aligned consecutive threads: they leave together
     if (t >= (size_t)M * cpr) return;
     const int m = (int)(t / cpr), c = (int)(t - (size_t)m * cpr);
-    const uint4 v = *(const uint4 *)(A + (size_t)m * K + 8 * (size_t)c);
+    // perm (the MoE layer): row m of the output is row perm[m] / topk of A, for
+    // the *nrows rows the route kept (perm past them is not written)
+    if (perm && m >= *nrows) return;
+    const int src = perm ? perm[m] / topk : m;
+    const uint4 v = *(const uint4 *)(A + (size_t)src * K + 8 * (size_t)c);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     float a[8];
 #pragma unroll
@@ -432,15 +436,19 @@ __global__ void k_int2_s8_decode(const uint32_t *__restrict__ B, uint32_t *__res
 
 }  // namespace
 
-ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st) {
+// perm non-NULL (the int8 MoE layer): output row m < *nrows quantizes row
+// perm[m] / topk of A, the gather fused into the quantization (rows past
+// *nrows, the dropped assignments, are not written).
+ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
+                           const int *perm, int topk, const int *nrows) {
     const size_t threads = (size_t)M * (K / 8);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     if (dtype == TERNOCL_BF16)
         hipLaunchKernelGGL(k_quant_a<true>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)A,
-                           (uint16_t *)SA, Aq, M, K);
+                           (uint16_t *)SA, Aq, M, K, perm, topk, nrows);
     else
         hipLaunchKernelGGL(k_quant_a<false>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)A,
-                           (uint16_t *)SA, Aq, M, K);
+                           (uint16_t *)SA, Aq, M, K, perm, topk, nrows);
     return check_launch();
 }
 

@@ -288,12 +288,13 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
 // ---- int8 MoE prefill layer (int2_moe/int2_moe_prefill_int8.cl, QMODE 1; the sequence of
 // int2_moe/prefill.cpp:243-279 with --int8 1) ----
 // (int2_int8.hip)
-ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st);
+ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
+                           const int *perm = nullptr, int topk = 1, const int *nrows = nullptr);
 ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
                                  const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G, int N,
                                  int K, int postop, int out_f32, hipStream_t st);
 
-// Workspace: meta | perm | inv | Xs DT [G][H] | SA1 [H/128][ldsa(G)] | U DT [G][I] |
+// Workspace: meta | perm | inv | SA1 [H/128][ldsa(G)] | U DT [G][I] |
 // Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [G][H] | Hq int8
 // [G][I], each 256-byte aligned.
 MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
@@ -303,7 +304,6 @@ MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     w.meta = o; o = align_up(o + (size_t)(2 * E + 2) * 4, 256);
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
-    w.xs = o;   o = align_up(o + G * H * 2, 256);
     w.sa1 = o;  o = align_up(o + (size_t)(H / 128) * lda * 2, 256);
     w.u = o;    o = align_up(o + G * I * 2, 256);
     w.h = o;    o = align_up(o + G * I * 2, 256);
@@ -315,8 +315,8 @@ MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     return w;
 }
 
-// route; gather the token rows into expert order; quant_a of the gathered
-// rows (SA1, Xq); up = s8 x s2 (POSTOP 0); h = silu(gate) * up (POSTOP 1,
+// route; quant_a of the token rows in expert order (SA1, Xq: the gather
+// fused into the quantization); up = s8 x s2 (POSTOP 0); h = silu(gate) * up (POSTOP 1,
 // Other = up); quant_a of h (SA2, Hq); Y = s8 x s2 down (fp32); combine.  The
 // int8 rows are written once (the reference's QMODE 0 with WRITE_Q); its
 // QMODE 1, quantizing in each GEMM, gives the same int8 values.
@@ -327,14 +327,13 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
     const MoeI8Ws w = moe_i8_ws_layout(T, E, topk, H, I);
     char *b = (char *)ws;
     int *meta = (int *)(b + w.meta), *perm = (int *)(b + w.perm), *inv = (int *)(b + w.inv);
-    void *Xs = b + w.xs, *SA1 = b + w.sa1, *U = b + w.u, *Hs = b + w.h, *SA2 = b + w.sa2;
+    void *SA1 = b + w.sa1, *U = b + w.u, *Hs = b + w.h, *SA2 = b + w.sa2;
     float *Y = (float *)(b + w.y);
     int8_t *Xq = (int8_t *)(b + w.xq), *Hq = (int8_t *)(b + w.hq);
     const int G = T * topk;
     ternocl_status s;
     if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
-    if ((s = moe_gather_run(X, perm, Xs, G, H, topk, st)) != TERNOCL_OK) return s;
-    if ((s = quant_a_run(dtype, Xs, SA1, Xq, G, H, st)) != TERNOCL_OK) return s;
+    if ((s = quant_a_run(dtype, X, SA1, Xq, G, H, st, perm, topk, meta + E)) != TERNOCL_OK) return s;
     if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK)
         return s;
     if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK)

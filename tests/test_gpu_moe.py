@@ -429,3 +429,41 @@ def test_moe_int8_layer_workload_shape(dev, orc):
     ref = orc.moe_ref_tokens(X, ids, RW, 0, 4, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16)
     assert np.abs(got[:4] - ref).max() / np.abs(ref).max() < 5e-2
     assert np.array_equal(out, _layer_int8(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16))
+
+
+def test_moe_int8_layer_out_of_range_ids_add_nothing(dev, orc):
+    """Ids outside [0, E) are dropped by the route: the int8 layer equals the oracle's
+    composition with those slots' weights set to 0 (the kept rows route the same way)."""
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H, I, bf16 = 64, 8, 2, 256, 256, True
+    g = synth.rng(44)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+    W = _weights(g, E, H, I, bf16)
+    drop = np.array([1, 6, 7, 40, 101])
+    bad_ids = ids.copy()
+    bad_ids[drop] = [-1, E, E + 9, -3, E]
+    got = formats.dt_to_f32(_layer_int8(T, torch, X, bad_ids, RW, Tk, E, topk, H, I, W, bf16), bf16)
+    (Bg, Sg), (Bu, Su), (Bd, Sd) = W
+    G = Tk * topk
+    keep = np.setdiff1d(np.arange(G), drop)
+    meta, pm, _ = orc.moe_route(bad_ids[keep], E, T.moe_tile_rows())
+    Xs = X[keep[pm] // topk]
+    Y = np.zeros((G, H), np.float32)
+    for e in range(E):
+        r0, r1 = int(meta[e]), int(meta[e + 1])
+        if r0 == r1:
+            continue
+        Me, Xe = r1 - r0, Xs[r0:r1]
+        SAx = orc.scale_a(Xe, Me, H, bf16)
+        U = orc.epilogue(orc.int8_gold(Xe, Bu[e], SAx, Su[e], Me, H, I, bf16), None, None, 0, False, bf16)
+        Hs = orc.epilogue(orc.int8_gold(Xe, Bg[e], SAx, Sg[e], Me, H, I, bf16), U, None, 1, False, bf16)
+        SAh = orc.scale_a(Hs, Me, I, bf16)
+        Y[keep[pm[r0:r1]]] = orc.epilogue(orc.int8_gold(Hs, Bd[e], SAh, Sd[e], Me, I, H, bf16), None, None, 0,
+                                          True, bf16)
+    rw0 = RW.copy()
+    rw0[drop] = 0
+    want = formats.dt_to_f32(orc.moe_combine(Y, np.arange(G, dtype=np.int32), rw0, Tk, topk, H, bf16), bf16)
+    bad, dmax = allclose_report(got, want)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
