@@ -19,6 +19,7 @@ Operators (the reference kernels they stand for, as in the C ABI):
   fwht              hadamard_fwht                         (hadamard_fwht.cl:63)
   moe_prefill       the int2 MoE prefill layer            (int2_moe/prefill.cpp:268-279)
   moe_decode        the int2 MoE decode layer             (int2_moe/int2_moe.cl:61-174)
+  moe_prefill_int8  the int8 MoE prefill layer            (int2_moe/int2_moe_prefill_int8.cl)
 """
 from __future__ import annotations
 
@@ -28,7 +29,7 @@ import torch
 
 import ternocl_amd as T
 
-__all__ = ["int2_gemm", "quant_a", "int2_int8_gemm", "bitcos_gemm", "fwht", "moe_prefill", "moe_decode"]
+__all__ = ["int2_gemm", "quant_a", "int2_int8_gemm", "bitcos_gemm", "fwht", "moe_prefill", "moe_decode", "moe_prefill_int8"]
 
 
 def _out_dtype(A: torch.Tensor, out_f32: bool) -> torch.dtype:
@@ -157,5 +158,24 @@ def moe_decode(X: torch.Tensor, ids: torch.Tensor, RW: torch.Tensor, E: int, Bg:
 
 
 @moe_decode.register_fake
+def _(X, ids, RW, E, Bg, Sg, Bu, Su, Bd, Sd):
+    return torch.empty_like(X)
+
+
+@torch.library.custom_op("ternocl::moe_prefill_int8", mutates_args=())
+def moe_prefill_int8(X: torch.Tensor, ids: torch.Tensor, RW: torch.Tensor, E: int, Bg: torch.Tensor,
+                     Sg: torch.Tensor, Bu: torch.Tensor, Su: torch.Tensor, Bd: torch.Tensor,
+                     Sd: torch.Tensor) -> torch.Tensor:
+    """O [T, H] of one MoE prefill layer on the s8 x s2 GEMM; arguments as moe_prefill."""
+    Tk, H = X.shape
+    topk = ids.shape[1]
+    I = Bg.shape[2]
+    O = torch.empty((Tk, H), dtype=X.dtype, device=X.device)
+    ws = torch.empty(T.int2_moe_prefill_int8_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device=X.device)
+    T.int2_moe_prefill_int8(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
+    return O
+
+
+@moe_prefill_int8.register_fake
 def _(X, ids, RW, E, Bg, Sg, Bu, Su, Bd, Sd):
     return torch.empty_like(X)

@@ -35,6 +35,7 @@ def test_ops_registered_and_fake_shapes():
     Sd = torch.empty((E, I // 128, H), dtype=torch.bfloat16, device="meta")
     assert ops.moe_prefill(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd).shape == (M, H)
     assert ops.moe_decode(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd).shape == (M, H)
+    assert ops.moe_prefill_int8(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd).shape == (M, H)
 
 
 @pytest.mark.gpu
@@ -91,9 +92,9 @@ def test_ops_match_direct_calls(dev, orc):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("Tk,decode", [(40, False), (3, True)])
+@pytest.mark.parametrize("Tk,decode", [(40, False), (3, True), (40, "int8")])
 def test_moe_ops_match_direct_calls(dev, Tk, decode):
-    """moe_prefill / moe_decode give the direct C-ABI calls' bits."""
+    """moe_prefill / moe_decode / moe_prefill_int8 give the direct C-ABI calls' bits."""
     import numpy as np
     import ternocl_amd as T
     import ternocl_amd.torch_ops  # noqa: F401
@@ -110,10 +111,14 @@ def test_moe_ops_match_direct_calls(dev, Tk, decode):
         return (dev_raw(np.stack([synth.int2_weights(g, K, N) for _ in range(E)])),
                 dev_dt(np.stack([synth.scales(g, K, N, bf16) for _ in range(E)]), bf16))
     (Bg, Sg), (Bu, Su), (Bd, Sd) = experts(H, I), experts(H, I), experts(I, H)
-    op = torch.ops.ternocl.moe_decode if decode else torch.ops.ternocl.moe_prefill
+    op = {False: torch.ops.ternocl.moe_prefill, True: torch.ops.ternocl.moe_decode,
+          "int8": torch.ops.ternocl.moe_prefill_int8}[decode]
     got = op(X, ids, RW, E, Bg, Sg, Bu, Su, Bd, Sd)
     O = torch.empty_like(X)
-    if decode:
+    if decode == "int8":
+        ws = torch.empty(T.int2_moe_prefill_int8_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device="cuda")
+        T.int2_moe_prefill_int8(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
+    elif decode:
         ws = torch.empty(T.int2_moe_decode_ws_bytes(Tk, topk, H, I), dtype=torch.uint8, device="cuda")
         T.int2_moe_decode(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
     else:
