@@ -263,6 +263,14 @@ def bench_c3(torch, T, synth, formats, orc):
     got = formats.dt_to_f32(dC[:rows].contiguous().view(torch.int16).cpu().numpy().view(np.uint16), bf16)
     bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
     Aq_ok = bool(np.array_equal(dAq[:rows].cpu().numpy(), orc.quant_a(A[:rows], SA, rows, K, bf16)))
+    # the fp16 upcvt GEMM on the same operands, checked on the same rows
+    it[0] = 0
+    upcvt()
+    torch.cuda.synchronize()
+    want_u = formats.dt_to_f32(orc.epilogue(orc.int2_gold(A[:rows], B, SB, rows, K, N, bf16), None, None, 0,
+                                            False, bf16), bf16)
+    got_u = formats.dt_to_f32(dC[:rows].contiguous().view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    bad_u = int((np.abs(got_u - want_u) > 1e-3 + 1e-2 * np.abs(want_u)).sum())
     us = graph_time_us(torch, call, 40)
     q_us = graph_time_us(torch, quant, 40)
     g_us = graph_time_us(torch, gemm, 40)
@@ -275,7 +283,8 @@ def bench_c3(torch, T, synth, formats, orc):
             "gemm_TOPS": round(ops / g_us / 1e6, 1), "weight_sets": sets,
             "parity_bad": bad, "parity_rows": rows, "quant_bit_exact": Aq_ok,
             "upcvt_fp16_gemm": {"us": round(u_us, 2), "TFLOPS": round(ops / u_us / 1e6, 1),
-                                "mfma_frac": round(ops / u_us / 1e6 / BF16_PEAK_TFLOPS, 4)}}
+                                "mfma_frac": round(ops / u_us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                "parity_bad": bad_u, "parity_rows": rows}}
 
 
 def bench_c4(torch, T, synth, formats, orc):

@@ -18,6 +18,10 @@
  *   C    : DT [M, N], or fp32 with out_f32
  *   Other: DT [M, N]   (postop 1, 2, 5)     Bias: C's type [N] (postop 3, 5)
  * Constraints: N % 16 == 0, K % 128 == 0, M >= 1 (ragged M is fine).
+ * The MFMA GEMMs (prefill, grouped MoE) address their operands with 32-bit
+ * buffer offsets: packed weights (K * N / 4 bytes per matrix) and activation
+ * rows stay below 2^31 bytes, or the entry returns TERNOCL_ERR_UNSUPPORTED_SHAPE.
+ * The fp16 prefill GEMM (M > 16) forms 2 * S in fp16: it takes |S| < 32768.
  *
  * Epilogue (postop), applied to the fp32 accumulator before the output cast,
  * as common/epilogue.clh:27-37 and common/epilogue.hpp:98-115:
@@ -219,12 +223,16 @@ ternocl_status ternocl_hadamard_fwht(int dtype, const void *x, const int8_t *sig
  * each expert in the expert-sorted order, then row-tile offsets [E+1..2E+1]
  * (tiles of ternocl_moe_tile_rows() rows); perm int [G] sorted row -> g;
  * inv int [G] = perm^-1.  Rows of an expert are in assignment order (stable,
- * deterministic).  An id outside [0, E) drops its assignment (inv = -1).
+ * deterministic).  An id outside [0, E) drops its assignment (inv = -1); the
+ * rows past the kept ones, perm[meta[E] .. G), are set to -1.
  * 1 <= E <= 512. */
 int ternocl_moe_tile_rows(void);
 ternocl_status ternocl_int2_moe_route(const int *ids, int *meta, int *perm, int *inv, int G, int E,
                                       void *stream);
-/* Gather (int2_moe_prefill.cl:63-70): Xs[p] = X[perm[p] / topk], rows of K DT. */
+/* Gather (int2_moe_prefill.cl:63-70): Xs[p] = X[perm[p] / topk], rows of K DT,
+ * for p < G; a row whose perm[p] is negative (a dropped assignment, as the
+ * route leaves it) is written as zeros.  Every non-negative perm[p] must be
+ * below T * topk for the T rows of X. */
 ternocl_status ternocl_int2_moe_gather(int dtype, const void *X, const int *perm, void *Xs, int G,
                                        int K, int topk, void *stream);
 /* Grouped GEMM (int2_moe_prefill.cl:72-141): for every sorted row p of expert e,

@@ -19,8 +19,10 @@
  *                           float64 product within fp32 rounding.
  *   orc_int2_dequant        closed form (+s, s^0x8000, 0), exhaustive over codes.
  *   orc_epilogue            bit-identical to the compiled epilogue_ref for
- *                           postop 0..4 x {DT, fp32}; postop 5 (bias + residual)
- *                           is an extension: parity unpinned against the reference.
+ *                           postop 0..4 x {DT, fp32}; postop 5 (bias + residual,
+ *                           no single reference postop) bit-identical to the
+ *                           compiled epilogue_ref run twice: postop 3 into fp32,
+ *                           then postop 2 into the output type.
  *   orc_scale_a/quant_a     bit-identical to the compiled compute_scale_a and the
  *                           lrintf quantization for finite products; closed-form
  *                           checks (RTE ties, saturation, FLT_EPSILON floor).

@@ -114,6 +114,9 @@ using namespace tcl;
         return (code);           \
     } while (0)
 
+// Operands the MFMA GEMMs address through 32-bit buffer offsets stay below this.
+constexpr size_t kMaxBufBytes = (size_t)1 << 31;
+
 static ternocl_status check_dtype(int dtype) {
     if (dtype != TERNOCL_FP16 && dtype != TERNOCL_BF16) FAIL(TERNOCL_ERR_INVALID_ARG, "dtype must be TERNOCL_FP16 or TERNOCL_BF16");
     return TERNOCL_OK;
@@ -172,9 +175,13 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
     (void)ws; (void)ws_bytes;
     const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0};
     if (t.engine < 0 || t.engine > 4) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..4");
-    if (t.engine == 3 || (M > 16 && t.engine == 0))
+    if (t.engine == 3 || (M > 16 && t.engine == 0)) {
+        // the GEMM addresses the packed weights with 32-bit buffer offsets
+        if ((size_t)(K / 16) * (size_t)N * 4 >= kMaxBufBytes)
+            FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the prefill GEMM takes packed weights (K * N / 4 bytes) below 2^31 bytes");
         return int2_gemm_mfma_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32,
                                   (hipStream_t)stream);
+    }
     if (M <= 16) {
         // automatic: the fp8 x fp4 engine where it applies, else the bf16/fp16 MFMA GEMV
         if (t.engine == 4 || (t.engine == 0 && int2_gemv_f4_supports(M, N, A)))
@@ -296,7 +303,7 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const
     const size_t need = ternocl_bitcos_gemm_mt_ws_bytes(K, N);
     if (!ws || ws_bytes < need) FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_bitcos_gemm_mt_ws_bytes(K, N) bytes");
     if (((uintptr_t)ws & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "ws must be 16-byte aligned");
-    if (need >= (1u << 31) || (size_t)M * K * 2 >= (1u << 31))
+    if (need >= kMaxBufBytes || (size_t)M * K * 2 >= kMaxBufBytes)
         FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the M-tiled BITCOS path takes A and the re-packed weights below 2^31 bytes");
     const hipStream_t st = (hipStream_t)stream;
     if ((s = bitcos_to_int2_run(B, SR, ls, (uint32_t *)ws, N, K, st)) != TERNOCL_OK) return s;
@@ -375,6 +382,8 @@ ternocl_status ternocl_int2_moe_gemm(int dtype, const int *meta, const void *A_a
     if (!meta) FAIL(TERNOCL_ERR_INVALID_ARG, "meta must be non-null");
     if (postop == 3 || postop == 5) FAIL(TERNOCL_ERR_INVALID_ARG, "the MoE GEMM has no bias: postop 0, 1, 2 or 4");
     if (E < 1 || E > kMoeMaxExperts || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need 1 <= E <= 512 and topk >= 1");
+    if ((size_t)(perm ? G / topk : G) * (size_t)K * 2 >= kMaxBufBytes || (size_t)(K / 16) * (size_t)N * 4 >= kMaxBufBytes)
+        FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the A rows and each expert's packed weights must be below 2^31 bytes");
     return moe_gemm_run(dtype, meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop,
                         out_f32, (hipStream_t)stream);
 }
@@ -404,6 +413,13 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
         FAIL(TERNOCL_ERR_INVALID_ARG, "X, ids, RW, the six weight tensors and O must be non-null");
     if (T < 1 || E < 1 || E > kMoeMaxExperts || topk < 1) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need T, topk >= 1 and 1 <= E <= 512");
     if (H % 128 || I % 128) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "H and I must be multiples of 128");
+    {
+        const size_t G = (size_t)T * topk;
+        if ((size_t)T * H * 2 >= kMaxBufBytes || G * I * 2 >= kMaxBufBytes ||
+            (size_t)(H / 16) * I * 4 >= kMaxBufBytes || (size_t)(I / 16) * H * 4 >= kMaxBufBytes)
+            FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE,
+                 "X (T * H * 2 bytes), the expert-sorted rows (T * topk * I * 2) and each expert's packed weights must be below 2^31 bytes");
+    }
     if (!ws || ws_bytes < moe_ws_layout(T, E, topk, H, I).total)
         FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_prefill_ws_bytes() bytes");
     return moe_prefill_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws, (hipStream_t)stream);
@@ -427,7 +443,8 @@ ternocl_status ternocl_int2_moe_prefill_int8(int dtype, const void *X, const int
     if (H % 128 || I % 128) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "H and I must be multiples of 128");
     if (int8_moe_tile_rows() != moe_tile_rows()) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "int8 tile rows differ from the route's");
     const size_t G = (size_t)T * topk;
-    if (G * H * 4 >= (1u << 31) || G * I * 2 >= (1u << 31) || (size_t)(H / 16) * I * 4 >= (1u << 31))
+    if (G * H * 4 >= kMaxBufBytes || G * I * 2 >= kMaxBufBytes || (size_t)(H / 16) * I * 4 >= kMaxBufBytes ||
+        (size_t)(I / 16) * H * 4 >= kMaxBufBytes)
         FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the gathered rows and each expert's weights must be below 2^31 bytes");
     if (!ws || ws_bytes < moe_i8_ws_layout(T, E, topk, H, I).total)
         FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_prefill_int8_ws_bytes() bytes");

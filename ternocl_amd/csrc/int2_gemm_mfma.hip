@@ -5,10 +5,11 @@
 //
 //   C[m,n] = ct(epi(sum_k A[m,k] * w(k,n))),  w(k,n) = code(k,n) * S[k/128, n]
 //
-// Tiling: a workgroup of 4 waves (2 x 2) computes a BM x BN tile of C, each
-// wave a (16 NMB) x (16 NCB) block as NMB x NCB v_mfma_f32_16x16x32_{f16,bf16}
-// tiles whose fp32 accumulators stay in registers (AGPRs for the large tiles)
-// over all of K.  K advances in LDS stages of 64 (two MFMA k-steps of 32).
+// Tiling: a workgroup computes a BM x BN tile of C, 128 x 512 (eight waves
+// side by side, each 128 x 64) or 128 x 128 (2 x 2 waves of 64 x 64); a wave's
+// outputs are 32 x 32 blocks of v_mfma_f32_32x32x16_{f16,bf16} whose fp32
+// accumulators stay in registers over all of K.  K advances in LDS stages of
+// 64 (four MFMA k-steps of 16).
 //   * A (DT, row-major) goes global -> registers -> LDS once per workgroup and
 //     stage, each 16-element chunk stored in the order 0,8,1,9,...,7,15, so the
 //     MFMA A fragment of lane (row, q) -- pairs (4h+i, 4h+i+8) of one chunk --
@@ -504,40 +505,22 @@ struct GemmPlan {
     int nmb, ncb, wvm, wvn;
 };
 
-// Fewest idle MFMA slots over the machine (ragged tiles and the last partial
-// round of workgroups over the 256 CUs), weighted by the relative MAC rate of
-// each tile shape (larger tiles decode fewer B words and read less A per MAC;
-// eight-wave tiles keep two waves per SIMD, four-wave 256 x 256 tiles one).
-// Tile choice.  The 128 x 512 tile of eight 128 x 64 waves is the fastest per
-// FLOP (measured 1.1-1.2 PFLOPS at M = 1024..4096), so it is taken whenever it
-// yields at least 192 tiles (three quarters of the CUs busy in its first
-// round; at N = 21504 its second, partial round still beats the 128 x 128
-// tile).  Below that the candidates are scored by rounds x tile area /
-// throughput relative to it (measured: 256 x 256 0.94, 256 x 128 0.66, 128 x
-// 256 0.69, 128 x 128 with two workgroups per CU 0.78).
+// Tile choice between the two shapes the engine compiles.  The 128 x 512 tile
+// of eight 128 x 64 waves is the fastest per FLOP (measured 1.1-1.2 PFLOPS at
+// M = 1024..4096), so it is taken whenever it yields at least 192 tiles (three
+// quarters of the CUs busy in its first round; at N = 21504 its second,
+// partial round still beats the 128 x 128 tile).  Below that the 128 x 128
+// tile of 2 x 2 waves, two resident workgroups per CU (measured at 0.78 of
+// the wide tile's MAC rate), wins while all of its tiles fit in one round of
+// 512; past that one round of the wide tile is shorter.  (Scoring 256 x 256,
+// 256 x 128 and 128 x 256 tiles the same way never selects them: a shape
+// small enough to run any of them in one round runs the 128 x 128 tile in
+// one round too, and the 256 x 256 tile is slower per FLOP than the wide one.)
 GemmPlan gemm_plan(int M, int N) {
-    auto tiles = [&](const GemmPlan &p) {
-        const int BM = 16 * p.nmb * p.wvm, BN = 16 * p.ncb * p.wvn;
-        return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    };
-    const GemmPlan wide = {8, 4, 1, 8};
-    if (tiles(wide) >= 192) return wide;
-    static const GemmPlan cands[] = {{8, 4, 1, 8}, {8, 4, 2, 4}, {8, 4, 2, 2}, {4, 8, 2, 2}, {4, 4, 2, 2}};
-    static const double eff[] = {1.0, 0.94, 0.66, 0.69, 0.78};
-    static const int per_cu[] = {1, 1, 1, 1, 2};  // resident workgroups per CU
-    GemmPlan best = cands[4];
-    double best_t = 1e300;
-    for (int c = 0; c < 5; ++c) {
-        const int BM = 16 * cands[c].nmb * cands[c].wvm, BN = 16 * cands[c].ncb * cands[c].wvn;
-        const long slots = 256L * per_cu[c];
-        const long rounds = (tiles(cands[c]) + slots - 1) / slots;
-        const double t = (double)rounds * BM * BN * per_cu[c] / eff[c];
-        if (t < best_t * 0.999) {
-            best_t = t;
-            best = cands[c];
-        }
-    }
-    return best;
+    auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
+    const GemmPlan wide = {8, 4, 1, 8}, square = {4, 4, 2, 2};
+    if (tiles(128, 512) >= 192) return wide;
+    return tiles(128, 128) <= 512 ? square : wide;
 }
 
 template <class Cfg, bool BF16>
@@ -554,9 +537,6 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
     if (p.wvn == 8) gemm_launch<TileCfg<8, 4, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.wvn == 4) gemm_launch<TileCfg<8, 4, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.nmb == 8) gemm_launch<TileCfg<8, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.ncb == 8) gemm_launch<TileCfg<4, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 

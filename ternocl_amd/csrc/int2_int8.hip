@@ -61,9 +61,9 @@ k_quant_a(const uint16_t *__restrict__ A, uint16_t *__restrict__ SA, int8_t *__r
     // the 16 chunks of a group are 16 aligned consecutive threads: they leave together
     if (t >= (size_t)M * cpr) return;
     const int m = (int)(t / cpr), c = (int)(t - (size_t)m * cpr);
-    // perm (the MoE layer): row m of the output is row perm[m] / topk of A, for
-    // the *nrows rows the route kept (perm past them is not written)
-    if (perm && m >= *nrows) return;
+    // nrows (the MoE layer): only the *nrows rows the route kept are read and
+    // written; perm: row m of the output is row perm[m] / topk of A
+    if (nrows && m >= *nrows) return;
     const int src = perm ? perm[m] / topk : m;
     const uint4 v = *(const uint4 *)(A + (size_t)src * K + 8 * (size_t)c);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -436,9 +436,10 @@ __global__ void k_int2_s8_decode(const uint32_t *__restrict__ B, uint32_t *__res
 
 }  // namespace
 
-// perm non-NULL (the int8 MoE layer): output row m < *nrows quantizes row
-// perm[m] / topk of A, the gather fused into the quantization (rows past
-// *nrows, the dropped assignments, are not written).
+// nrows non-NULL (the int8 MoE layer): only rows m < *nrows are quantized and
+// written (rows past it belong to dropped assignments); perm non-NULL: output
+// row m quantizes row perm[m] / topk of A, the gather fused into the
+// quantization.
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
                            const int *perm, int topk, const int *nrows) {
     const size_t threads = (size_t)M * (K / 8);

@@ -54,6 +54,7 @@ __global__ void __launch_bounds__(kRouteThreads)
 k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict__ perm,
             int *__restrict__ inv, int G, int E, int rpt) {
     extern __shared__ int sh[];
+    __shared__ int s_rows;  // kept assignments (meta[E])
     int *cnt = sh, *run = sh + E, *wcnt = sh + 2 * E;  // wcnt [kRouteWaves][E]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const unsigned long long below = (1ull << lane) - 1ull;
@@ -153,6 +154,7 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
         if (lane == 0) {
             meta[E] = r0;
             meta[2 * E + 1] = t0;
+            s_rows = r0;
         }
     }
     __syncthreads();
@@ -166,8 +168,9 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
         __syncthreads();
         place_block(0, sperm);
         __syncthreads();
-        const int rows = meta[E];
+        const int rows = s_rows;
         for (int i = tid; i < rows; i += kRouteThreads) perm[i] = sperm[i];
+        for (int i = rows + tid; i < G; i += kRouteThreads) perm[i] = -1;  // dropped assignments
         return;
     }
     for (int b0 = 0; b0 < G; b0 += kRouteBlock) {
@@ -181,15 +184,22 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
         place_block(b0, perm);
         __syncthreads();  // wcnt is reset for the next block
     }
+    for (int i = s_rows + tid; i < G; i += kRouteThreads) perm[i] = -1;  // dropped assignments
 }
 
-// Xs[p] = X[perm[p] / topk] (rows of K DT), one workgroup per row
+// Xs[p] = X[perm[p] / topk] (rows of K DT), one workgroup per row; a row whose
+// perm is negative (past the kept rows: the route writes -1 there) is zeroed
 __global__ void __launch_bounds__(256)
 k_moe_gather(const uint16_t *__restrict__ X, const int *__restrict__ perm, uint16_t *__restrict__ Xs,
              int K, int topk) {
     const int p = blockIdx.x;
-    const uint16_t *src = X + (size_t)(perm[p] / topk) * K;
+    const int g = perm[p];
     uint16_t *dst = Xs + (size_t)p * K;
+    if (g < 0) {
+        for (int i = threadIdx.x; i < K; i += blockDim.x) dst[i] = 0;
+        return;
+    }
+    const uint16_t *src = X + (size_t)(g / topk) * K;
     if ((K & 7) == 0) {
         for (int i = threadIdx.x; i < K / 8; i += blockDim.x) ((uint4 *)dst)[i] = ((const uint4 *)src)[i];
     } else {
@@ -338,7 +348,7 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
         return s;
     if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK)
         return s;
-    if ((s = quant_a_run(dtype, Hs, SA2, Hq, G, I, st)) != TERNOCL_OK) return s;
+    if ((s = quant_a_run(dtype, Hs, SA2, Hq, G, I, st, nullptr, 1, meta + E)) != TERNOCL_OK) return s;
     if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Hq, SA2, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK)
         return s;
     return moe_combine_run(dtype, Y, inv, RW, O, T, topk, H, st);

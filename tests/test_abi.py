@@ -98,3 +98,21 @@ def test_moe_layer_host_validation(entry):
     assert L.ternocl_last_error().decode()
     if entry == "ternocl_int2_moe_decode":
         assert call(Tk=4096, k=8) == 2
+
+
+def test_operand_size_guards():
+    """Operands the MFMA GEMMs address with 32-bit buffer offsets are rejected on
+    the host at 2^31 bytes (the pointers here are never dereferenced)."""
+    import ctypes
+    import ternocl_amd as T
+    L = T.lib()
+    # prefill GEMM: K * N / 4 bytes of packed weights at 2^31
+    assert _call_gemm(L, M=64, K=65536, N=131072) == 2
+    p = ctypes.c_void_p(4096)
+    # grouped GEMM: the gathered A rows (G / topk rows of K DT) at 2^31 bytes
+    assert L.ternocl_int2_moe_gemm(1, p, p, p, 1, p, p, p, None, 8, 262144, 128, 4096, 0, 0, None) == 2
+    assert L.ternocl_int2_moe_gemm(1, p, p, None, 1, p, p, p, None, 8, 1024, 1 << 21, 4096, 0, 0, None) == 2
+    # MoE layers: the expert-sorted rows T * topk * I * 2 at 2^31 bytes
+    for fn in (L.ternocl_int2_moe_prefill, L.ternocl_int2_moe_prefill_int8):
+        assert fn(1, p, p, p, 65536, 8, 8, 2048, 2048, p, p, p, p, p, p, p, p, 1 << 40, None) == 2
+    assert "2^31" in L.ternocl_last_error().decode()

@@ -66,9 +66,36 @@ def test_moe_route_drops_out_of_range_ids(dev, orc):
     assert np.array_equal(meta.cpu().numpy(), m)
     n = int(m[E])
     assert np.array_equal(perm.cpu().numpy()[:n], keep[pm])
+    assert (perm.cpu().numpy()[n:] == -1).all(), "perm past the kept rows must be -1"
     iv = inv.cpu().numpy()
     assert (iv[bad] == -1).all()
     assert np.array_equal(iv[keep[pm]], np.arange(n))
+
+
+@pytest.mark.parametrize("G", [3000, 40000])
+def test_moe_gather_after_dropped_ids(dev, orc, G):
+    """Route then gather with out-of-range ids: the kept rows are the token rows in
+    expert order and the rows past them (perm = -1) come out as zeros; the gather
+    reads nothing outside X (single- and multi-block route)."""
+    import torch
+    import ternocl_amd as T
+    E, topk, K, bf16 = 16, 4, 256, False
+    Tk = G // topk
+    g = synth.rng(G)
+    X = synth.activations(g, (Tk, K), bf16)
+    ids = g.integers(0, E, G, dtype=np.int32)
+    bad = g.random(G) < 0.2
+    ids[bad] = np.where(g.random(bad.sum()) < 0.5, -3, E)
+    meta, perm, _ = _route(T, ids, G, E)
+    dXs = torch.full((G, K), 7.0, dtype=torch.float16, device="cuda")
+    T.int2_moe_gather(dev_dt(X, bf16), perm, dXs, G, K, topk)
+    torch.cuda.synchronize()
+    n = int(meta.cpu().numpy()[E])
+    assert n == int((~bad).sum())
+    got = host_u16(dXs)
+    pm = perm.cpu().numpy()
+    assert np.array_equal(got[:n], X[pm[:n] // topk])
+    assert (got[n:] == 0).all()
 
 
 def test_moe_gather(dev, orc):

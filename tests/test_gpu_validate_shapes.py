@@ -1,0 +1,146 @@
+"""GPU parity at the reference's own validation shapes and the workload shapes,
+through the C ABI with the library's automatic kernel choice (the path a
+drop-in caller gets).
+
+Shape lists:
+* int2 upcvt: int2_fp16_upcvt/validate.sh:8-10 (M K N; fp16 and bf16);
+* int2 x int8 (quant_a + s8 x s2): int2_via_int2_x_int8_dpas/validate.sh:9-10;
+* the prefill workload M=1024 K=4096 N=14336 in both paths, and the decode
+  workload's sweep M in {1, 2, 4, 8} x (K, N) in {(4096, 14336), (14336, 4096)}
+  in bf16 with the bias + residual epilogue.
+
+At M >= 128 the gold is computed on a row sample: every column, and rows 0, 1,
+31, 32, 63, 64, 126, 127 of every 128-row tile plus the last row (both GEMM
+tiles are 128 rows high, so every tile and both halves of every wave's rows
+are checked).  Bar: |got - ref| <= 1e-3 + 1e-2 |ref| against the oracle's
+restatement of the reference's host gold.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from ternocl_amd import formats, synth
+from tests.gpu_util import allclose_report, dev_dt, dev_raw, host_f32, host_u16
+
+pytestmark = pytest.mark.gpu
+
+UPCVT_VALIDATE = [(1024, 17408, 5120), (1024, 5120, 14336), (1024, 5120, 34816), (1000, 5120, 4096),
+                  (77, 128, 48), (129, 256, 272), (200, 5120, 16384), (1, 5120, 34816), (1, 17408, 5120),
+                  (1, 5120, 248320), (1, 6144, 5120), (4, 6144, 5120), (3, 256, 48)]
+INT8_VALIDATE = [(1024, 17408, 5120), (1024, 5120, 14336), (1024, 5120, 34816), (1000, 5120, 4096),
+                 (77, 128, 48), (129, 256, 272), (200, 5120, 16384), (1, 5120, 34816), (1, 17408, 5120),
+                 (1, 5120, 248320), (4, 6144, 5120)]
+PREFILL_WORKLOAD = (1024, 4096, 14336)
+# 128 x 512 tiles with ragged M and a last column tile of 16 columns
+WIDE_RAGGED = (1000, 1024, 12304)
+
+
+def sample_rows(M: int) -> np.ndarray:
+    if M < 128:
+        return np.arange(M)
+    rows = {M - 1}
+    for t0 in range(0, M, 128):
+        rows.update(t0 + r for r in (0, 1, 31, 32, 63, 64, 126, 127) if t0 + r < M)
+    return np.array(sorted(rows))
+
+
+def _inputs(seed, M, K, N, bf16):
+    g = synth.rng(seed)
+    A = synth.activations(g, (M, K), bf16)
+    B = synth.int2_weights(g, K, N)
+    S = synth.scales(g, K, N, bf16)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = g.standard_normal(N).astype(np.float32) * np.float32(0.1)
+    return A, B, S, other, bias_f
+
+
+def _device_io(torch, S, other, bias_f, M, N, bf16, out_f32):
+    dO = dev_dt(other, bf16)
+    if out_f32:
+        dBias = torch.from_numpy(bias_f).cuda()
+        dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    else:
+        dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+        dC = torch.zeros((M, N), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    return dO, dBias, dC
+
+
+def _compare(orc, dC, acc_rows, other, bias_f, rows, bf16, postop, out_f32):
+    bias = bias_f if out_f32 else formats.f32_to_dt(bias_f, bf16)
+    want = orc.epilogue(acc_rows, other[rows], bias, postop, out_f32, bf16)
+    if out_f32:
+        got, ref = host_f32(dC)[rows], want
+    else:
+        got, ref = formats.dt_to_f32(host_u16(dC)[rows], bf16), formats.dt_to_f32(want, bf16)
+    return allclose_report(got, ref)
+
+
+def _upcvt_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
+    import torch
+    import ternocl_amd as T
+    print(f"upcvt M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32}", flush=True)
+    A, B, S, other, bias_f = _inputs(seed + 40000 + M + K + N, M, K, N, bf16)
+    dO, dBias, dC = _device_io(torch, S, other, bias_f, M, N, bf16, out_f32)
+    T.int2_fp16_upcvt_gemm(dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16), dC, dO, dBias, M, N, K,
+                           postop, out_f32)
+    torch.cuda.synchronize()
+    rows = sample_rows(M)
+    acc = orc.int2_gold(np.ascontiguousarray(A[rows]), B, S, rows.size, K, N, bf16)
+    return _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
+
+
+def _int8_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
+    import torch
+    import ternocl_amd as T
+    print(f"int8 M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32}", flush=True)
+    A, B, SB, other, bias_f = _inputs(seed + 50000 + M + K + N, M, K, N, bf16)
+    dA = dev_dt(A, bf16)
+    dSA = torch.zeros((K // 128, T.ldsa(M)), dtype=dA.dtype, device="cuda")
+    dAq = torch.zeros((M, K), dtype=torch.int8, device="cuda")
+    dO, dBias, dC = _device_io(torch, SB, other, bias_f, M, N, bf16, out_f32)
+    T.quant_a(dA, dSA, dAq, M, K)
+    T.int2_int8_gemm(None, dAq, dSA, dev_raw(B), dev_dt(SB, bf16), dC, dO, dBias, M, N, K, postop, out_f32)
+    torch.cuda.synchronize()
+    rows = sample_rows(M)
+    Ar = np.ascontiguousarray(A[rows])
+    SA = orc.scale_a(Ar, rows.size, K, bf16)
+    # quant_a's output on the sampled rows is bit-exact with the oracle's
+    got_q = dAq.cpu().numpy()[rows]
+    assert np.array_equal(got_q, orc.quant_a(Ar, SA, rows.size, K, bf16)), "Aq differs from the oracle"
+    acc = orc.int8_gold(Ar, B, SA, SB, rows.size, K, N, bf16)
+    return _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", UPCVT_VALIDATE + [PREFILL_WORKLOAD, WIDE_RAGGED])
+def test_upcvt_validate_shapes(dev, orc, M, K, N, bf16):
+    bad, dmax = _upcvt_case(dev, orc, M, K, N, bf16)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", INT8_VALIDATE + [PREFILL_WORKLOAD, WIDE_RAGGED])
+def test_int8_validate_shapes(dev, orc, M, K, N, bf16):
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_wide_tile_epilogues(dev, orc, bf16, postop, out_f32):
+    """Every epilogue on the 128 x 512 tile (ragged rows, a 16-column last tile)."""
+    M, K, N = WIDE_RAGGED[0], 256, WIDE_RAGGED[2]
+    bad, dmax = _upcvt_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
+    assert bad == 0, f"upcvt: {bad} bad (max |d| {dmax})"
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
+    assert bad == 0, f"int8: {bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
+def test_decode_workload_sweep(dev, orc, M, K, N):
+    """The decode workload: bf16, bias + residual (postop 5), automatic engine."""
+    bad, dmax = _upcvt_case(dev, orc, M, K, N, True, postop=5)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"

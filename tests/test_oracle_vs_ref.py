@@ -106,3 +106,23 @@ def test_bitcos_decode_ranks_gold_bitwise(orc, z):
         S = synth.scales(g, K, N, bf16, 0.75, 15.75)
         assert np.array_equal(orc.bitcos_gold(A, buf, S, M, K, N, bf16).view(np.uint32),
                               orc.ref_bitcos_gold(A, buf, S, M, K, N, bf16).view(np.uint32))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_epilogue_postop5_is_bias_then_residual(orc, out_f32, bf16):
+    """postop 5 (bias + residual, no single reference counterpart) equals the
+    reference's epilogue_ref applied twice (common/epilogue.hpp:98-115):
+    postop 3 into fp32, then postop 2 into the requested output type."""
+    g = synth.rng(55 + out_f32)
+    M, N = 6, 160
+    acc = (g.standard_normal((M, N)) * 6).astype(np.float32)
+    acc[0, :6] = [0.0, -0.0, 1e-8, -3.0, 65000.0, -1e30]
+    other = formats.f32_to_dt(g.uniform(-4, 4, (M, N)).astype(np.float32), bf16)
+    bias_f = g.uniform(-8, 8, N).astype(np.float32)
+    bias = bias_f if out_f32 else formats.f32_to_dt(bias_f, bf16)
+    mine = orc.epilogue(acc, other, bias, 5, out_f32, bf16)
+    bias32 = bias_f if out_f32 else formats.dt_to_f32(bias, bf16)  # DT -> fp32 is exact
+    step1 = orc.ref_epilogue(acc, None, bias32, 3, True, bf16)
+    theirs = orc.ref_epilogue(step1, other, None, 2, out_f32, bf16)
+    assert np.array_equal(mine.view(np.uint8), theirs.view(np.uint8))

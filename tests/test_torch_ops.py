@@ -38,6 +38,50 @@ def test_ops_registered_and_fake_shapes():
     assert ops.moe_prefill_int8(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd).shape == (M, H)
 
 
+def test_ops_reject_bad_inputs():
+    """Each operator checks dtype, shape and contiguity before any launch (meta
+    tensors: the checks run in the fake implementations, no library call)."""
+    import ternocl_amd.torch_ops  # noqa: F401
+    ops = torch.ops.ternocl
+    m = dict(device="meta")
+    M, K, N, E, topk, H, I = 5, 256, 48, 4, 2, 256, 128
+    A = torch.empty((M, K), dtype=torch.bfloat16, **m)
+    B = torch.empty((K // 16, N), dtype=torch.int32, **m)
+    S = torch.empty((K // 128, N), dtype=torch.bfloat16, **m)
+
+    def bad(fn, *args):
+        with pytest.raises(RuntimeError):
+            fn(*args)
+    bad(ops.int2_gemm, A.float(), B, S, None, None, 0, False)                 # fp32 activations
+    bad(ops.int2_gemm, A, B.long(), S, None, None, 0, False)                   # int64 weights
+    bad(ops.int2_gemm, A, B, S.half(), None, None, 0, False)                   # S dtype != A dtype
+    bad(ops.int2_gemm, A, B[:, :32], S, None, None, 0, False)                  # S columns != B columns
+    bad(ops.int2_gemm, A, B, S, torch.empty((M, N + 16), dtype=A.dtype, **m), None, 2, False)
+    bad(ops.int2_gemm, A, B, S, None, torch.empty(N, dtype=A.dtype, **m), 3, True)  # fp32 out: fp32 bias
+    bad(ops.int2_gemm, torch.empty((K, M), dtype=A.dtype, **m).t(), B, S, None, None, 0, False)  # not contiguous
+    Aq = torch.empty((M, K), dtype=torch.int8, **m)
+    SA = torch.empty((K // 128, 32), dtype=torch.bfloat16, **m)
+    bad(ops.int2_int8_gemm, Aq, SA[:, :16], B, S, None, None, 0, False)      # SA pitch != ldsa(M)
+    bad(ops.int2_int8_gemm, Aq.to(torch.uint8), SA, B, S, None, None, 0, False)
+    Bc = torch.empty(K // 32 * N + N + 64, dtype=torch.int32, **m)
+    bad(ops.bitcos_gemm, A, Bc, S, None, 2, N, None, None, 0, False)         # ls > 1 needs SR
+    bad(ops.fwht, A, torch.empty(K, dtype=torch.float16, **m), 256)           # signs must be int8
+    X = torch.empty((M, H), dtype=torch.bfloat16, **m)
+    ids = torch.empty((M, topk), dtype=torch.int32, **m)
+    RW = torch.empty((M, topk), dtype=torch.bfloat16, **m)
+    Bg = torch.empty((E, H // 16, I), dtype=torch.int32, **m)
+    Sg = torch.empty((E, H // 128, I), dtype=torch.bfloat16, **m)
+    Bd = torch.empty((E, I // 16, H), dtype=torch.int32, **m)
+    Sd = torch.empty((E, I // 128, H), dtype=torch.bfloat16, **m)
+    for op in (ops.moe_prefill, ops.moe_decode, ops.moe_prefill_int8):
+        op(X, ids, RW, E, Bg, Sg, Bg, Sg, Bd, Sd)                               # the good case
+        bad(op, X, ids.long(), RW, E, Bg, Sg, Bg, Sg, Bd, Sd)                  # torch.topk's int64 ids
+        bad(op, X, ids, RW, E + 1, Bg, Sg, Bg, Sg, Bd, Sd)                     # E != stacked experts
+        bad(op, X, ids, RW.half(), E, Bg, Sg, Bg, Sg, Bd, Sd)                  # RW dtype != X dtype
+        bad(op, X, ids, RW, E, Bg, Sg, Bg, Sg, Bg, Sd)                         # down weights transposed
+        bad(op, X, ids, RW, E, Bg, Sg[:, :, :64], Bg, Sg, Bd, Sd)              # scale shape
+
+
 @pytest.mark.gpu
 def test_ops_match_direct_calls(dev, orc):
     import ternocl_amd as T
