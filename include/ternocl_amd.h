@@ -296,6 +296,23 @@ ternocl_status ternocl_int2_moe_decode(int dtype, const void *X, const int *ids,
                                        const uint32_t *Bu, const void *Su, const uint32_t *Bd,
                                        const void *Sd, void *O, void *ws, size_t ws_bytes, void *stream);
 
+/* The same MoE decode layer without a workspace argument: it allocates nothing
+ * (no hipMalloc, no allocating library call), for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation.  No counterpart in the reference.  Its scratch is a
+ * fixed array of TERNOCL_NOALLOC_SCRATCH_BYTES per device, held until the
+ * process ends; the first call on a device looks up that array's device
+ * address (hipGetSymbolAddress, no allocation).  Shapes whose
+ * ternocl_int2_moe_decode_ws_bytes() exceed it return TERNOCL_ERR_WORKSPACE.
+ * Every call on one device shares that array: calls that overlap on one
+ * device (two streams, two threads) race and must be serialised by the
+ * caller.  Same results as ternocl_int2_moe_decode, bit for bit. */
+#define TERNOCL_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+ternocl_status ternocl_int2_moe_decode_noalloc(int dtype, const void *X, const int *ids, const void *RW,
+                                               int T, int E, int topk, int H, int I, const uint32_t *Bg,
+                                               const void *Sg, const uint32_t *Bu, const void *Su,
+                                               const uint32_t *Bd, const void *Sd, void *O, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

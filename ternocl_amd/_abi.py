@@ -53,6 +53,7 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_int2_moe_prefill_int8": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
     "ternocl_int2_moe_decode_ws_bytes": (Z, [I, I, I, I]),
     "ternocl_int2_moe_decode": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
+    "ternocl_int2_moe_decode_noalloc": (I, [I, P, P, P, I, I, I, I, I, P, P, P, P, P, P, P, P]),
 }
 
 

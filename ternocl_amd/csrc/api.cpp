@@ -101,6 +101,10 @@ ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const vo
                               int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                               const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
                               void *O, void *ws, hipStream_t st);
+ternocl_status moe_decode_noalloc_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                                      int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                      const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                                      void *O, hipStream_t st);
 // kernels (misc.hip)
 ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st);
 
@@ -457,10 +461,10 @@ size_t ternocl_int2_moe_decode_ws_bytes(int T, int topk, int H, int I) {
     return moe_decode_ws_bytes(T, topk, H, I);
 }
 
-ternocl_status ternocl_int2_moe_decode(int dtype, const void *X, const int *ids, const void *RW, int T,
-                                       int E, int topk, int H, int I, const uint32_t *Bg, const void *Sg,
-                                       const uint32_t *Bu, const void *Su, const uint32_t *Bd,
-                                       const void *Sd, void *O, void *ws, size_t ws_bytes, void *stream) {
+static ternocl_status check_moe_decode(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                                       int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                       const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                                       const void *O) {
     ternocl_status s = check_dtype(dtype);
     if (s != TERNOCL_OK) return s;
     if (!X || !ids || !RW || !Bg || !Sg || !Bu || !Su || !Bd || !Sd || !O)
@@ -469,10 +473,33 @@ ternocl_status ternocl_int2_moe_decode(int dtype, const void *X, const int *ids,
     if (H % 128 || I % 128) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "H and I must be multiples of 128");
     if ((size_t)T * topk > 32767) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "T * topk must be below 32768 (decode)");
     if (((uintptr_t)X & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "X must be 16-byte aligned");
+    return TERNOCL_OK;
+}
+
+ternocl_status ternocl_int2_moe_decode(int dtype, const void *X, const int *ids, const void *RW, int T,
+                                       int E, int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                       const uint32_t *Bu, const void *Su, const uint32_t *Bd,
+                                       const void *Sd, void *O, void *ws, size_t ws_bytes, void *stream) {
+    ternocl_status s = check_moe_decode(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O);
+    if (s != TERNOCL_OK) return s;
     if (!ws || ws_bytes < moe_decode_ws_bytes(T, topk, H, I))
         FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_int2_moe_decode_ws_bytes() bytes");
     if (((uintptr_t)ws & 255) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "ws must be 256-byte aligned");
     return moe_decode_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_moe_decode_noalloc(int dtype, const void *X, const int *ids, const void *RW, int T,
+                                               int E, int topk, int H, int I, const uint32_t *Bg,
+                                               const void *Sg, const uint32_t *Bu, const void *Su,
+                                               const uint32_t *Bd, const void *Sd, void *O, void *stream) {
+    ternocl_status s = check_moe_decode(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O);
+    if (s != TERNOCL_OK) return s;
+    if (moe_decode_ws_bytes(T, topk, H, I) > kNoAllocScratchBytes)
+        FAIL(TERNOCL_ERR_WORKSPACE, "this layer needs more scratch than the allocation-free entry holds "
+                                    "(ternocl_int2_moe_decode_ws_bytes() > TERNOCL_NOALLOC_SCRATCH_BYTES, 16 MiB): "
+                                    "call ternocl_int2_moe_decode with a workspace");
+    return moe_decode_noalloc_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O,
+                                  (hipStream_t)stream);
 }
 
 }  // extern "C"

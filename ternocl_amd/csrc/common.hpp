@@ -204,6 +204,9 @@ struct MoeI8Ws {
     size_t meta, perm, inv, sa1, u, h, sa2, y, xq, hq, total;
 };
 // Records the HIP error text for ternocl_last_error() and maps it to a status.
+// Scratch bytes of the allocation-free MoE decode entry (moe.hip).
+constexpr size_t kNoAllocScratchBytes = TERNOCL_NOALLOC_SCRATCH_BYTES;
+
 ternocl_status launch_status(hipError_t e);
 ternocl_status check_launch();
 void set_error(const char *msg);

@@ -25,6 +25,8 @@
 // in the layer: the grouped GEMM reads row perm[p] / topk of X directly.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace tcl {
 
 int moe_tile_rows();  // int2_gemm_mfma.hip
@@ -392,6 +394,53 @@ ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const vo
                                     nullptr, 1, st)) != TERNOCL_OK)
         return s;
     return moe_combine_run(dtype, Y, nullptr, RW, O, T, topk, H, st);
+}
+
+// ---- the MoE decode layer without a caller workspace ----
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops): the layer's scratch -- the fp32 gate/up rows and, for topk > 16, the
+// fp32 down rows, the same layout as the workspace of moe_decode_run -- lives in
+// one fixed array per device, held until the process ends.  Every call on a
+// device shares that device's array: calls that overlap on one device race.
+// Nothing in it has to start at zero (every row the layer reads back it has
+// written in the same call), so it is never cleared.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of scratch on each device (looked up once)
+}  // namespace
+
+ternocl_status moe_decode_noalloc_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
+                                      int topk, int H, int I, const uint32_t *Bg, const void *Sg,
+                                      const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
+                                      void *O, hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return launch_status(e);
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("device ordinal beyond the 64 devices the scratch table holds");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    void *ptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            // the host-side name of scratch is not a device address: kernels get
+            // the address the runtime reports for this device
+            void *p = nullptr;
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return launch_status(e);
+            if (!p) {
+                set_error("hipGetSymbolAddress returned no address for the scratch array");
+                return TERNOCL_ERR_LAUNCH;
+            }
+            g_scratch_ptr[dev] = p;
+        }
+        ptr = g_scratch_ptr[dev];
+    }
+    return moe_decode_run(dtype, X, ids, RW, T, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ptr, st);
 }
 
 }  // namespace tcl
