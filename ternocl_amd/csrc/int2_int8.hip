@@ -254,7 +254,9 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
     // threads t and t + BM (when THREADS = 2 BM) load and write the same row's
     // value, so the store below needs no branch
     const int srow = tid & (BM - 1);
-    const uint32_t vsa = (uint32_t)srow * 2;
+    // (rows past mrows load row mrows - 1: the last group's row m0 + srow may
+    // lie past SA's end, and the SGPR offset is not range-checked)
+    const uint32_t vsa = (uint32_t)min(srow, mrows - 1) * 2;
     uint32_t sa_raw = 0;
     auto sa_load = [&](int g) {
         const int gc = g < groups ? g : groups - 1;
@@ -426,6 +428,263 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
     });
 }
 
+// ---- wide-tile s8 x s2 GEMM (v_mfma_i32_32x32x32_i8) ------------------------
+//
+// The fold acc += float(dot) * (SB * (1 / SA)) is due once per output and
+// 128-row group whatever the tiling, and on gfx950 one VALU instruction of a
+// wave takes 4 cycles against 32 for a 32 x 32 x 32 int8 MFMA that covers 32
+// of the group's 128 rows: the fold's three VALU operations per output and
+// group cost 1.5x the group's MFMA time.  What the tiling changes is the rest
+// of the VALU work (the B decode, amortised over a wave's rows) and the LDS
+// traffic (the A fragments, amortised over a wave's columns).  This engine:
+//   * a workgroup of WVN waves side by side, each 32 RMB rows x 64 columns
+//     (RMB x 2 blocks of 32 x 32 outputs), 128 x 512 at the default shape:
+//     each 16-byte A chunk staged once serves 512 columns and each decoded
+//     B word 128 rows;
+//   * one LDS stage per 128-row group: the tile's A rows (4 x 4
+//     byte-transposed as in the 128 x 128 engine) and 1 / SA of its rows;
+//     three stage buffers, the next stage stored in the middle of the current
+//     one, one barrier per stage;
+//   * lane (c, h) = (l % 32, l / 32) holds k rows 16 h .. 16 h + 15 of each
+//     32-row k-chunk: the B fragment is one packed word per (column, k-chunk)
+//     through decode_s2, the A fragment the 16-byte chunk 2 kc + h of its row;
+//   * each block's dot products run from zero over the group's four k-chunks
+//     in int32 and are folded into the fp32 accumulators as in the 128 x 128
+//     engine.
+// GRP: the int8 MoE prefill's grouped GEMM, as k_int2_int8_gemm<..., GRP>
+// (workgroup (row tile, column block), its expert found by binary search).
+template <int RMB_, int WVN_> struct WTile {
+    static constexpr int RMB = RMB_, WVN = WVN_;
+    static constexpr int THREADS = 64 * WVN;
+    static constexpr int BM = 32 * RMB, BN = 64 * WVN;
+    static constexpr int AP = BM * 8 / THREADS;  // 16-byte A chunks per thread and stage
+    static_assert(BM * 8 % THREADS == 0, "A chunks must divide evenly");
+    static_assert(THREADS % BM == 0 && (BM & (BM - 1)) == 0, "threads cover the tile rows evenly");
+    static constexpr int ABYTES = BM * QA_PITCH;
+    static constexpr int SBYTES = ABYTES + BM * 4;  // one stage buffer: A rows, 1 / SA
+    static constexpr int EP_PITCH = 36;              // epilogue floats per row: 32 + 4
+    static constexpr int STAGE_BYTES = 3 * SBYTES;
+    static constexpr int EPI_BYTES = WVN * 16 * RMB * EP_PITCH * 4;
+    static constexpr int LDS_BYTES = STAGE_BYTES > EPI_BYTES ? STAGE_BYTES : EPI_BYTES;
+};
+typedef WTile<4, 8> WideTile;  // 128 x 512, eight waves of 128 x 64
+
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ i32x16_t mfma_i8_32(const i32x4_t &a, const i32x4_t &b, const i32x16_t &c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+template <class TC, bool BF16, bool GRP = false>
+__global__ void __launch_bounds__(TC::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
+                   const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB, void *__restrict__ C,
+                   const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N, int K,
+                   int postop, int out_f32, const int *__restrict__ meta = nullptr, int E = 0) {
+    constexpr int RMB = TC::RMB, BM = TC::BM, BN = TC::BN, AP = TC::AP, TH = TC::THREADS;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TC::LDS_BYTES];
+    int tm, tn, sa_off = 0;
+    const int lda = ldsa_of(M);  // (GRP: of all G rows)
+    if constexpr (GRP) {
+        const int ntn = (N + BN - 1) / BN;
+        const int tile = blockIdx.x / ntn;
+        tn = blockIdx.x - tile * ntn;
+        if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {  // the last expert whose first tile is <= tile
+            const int mid = (lo + hi + 1) >> 1;
+            if (meta[E + 1 + mid] <= tile) lo = mid;
+            else hi = mid - 1;
+        }
+        // (wave-uniform values: kept in scalar registers)
+        const int e = __builtin_amdgcn_readfirstlane(lo), row0 = __builtin_amdgcn_readfirstlane(meta[e]);
+        tm = __builtin_amdgcn_readfirstlane(tile - meta[E + 1 + e]);
+        M = __builtin_amdgcn_readfirstlane(meta[e + 1] - row0);
+        Aq += (size_t)row0 * K;
+        sa_off = row0;
+        SA += row0;
+        B += (size_t)e * (K / 16) * N;
+        SB += (size_t)e * (K / kGS) * N;
+        C = (uint8_t *)C + (size_t)row0 * N * (out_f32 ? 4 : 2);
+        if (Other) Other += (size_t)row0 * N;
+    } else {
+        const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+        if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int mrows = min(BM, M - m0), groups = K / kGS;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c32 = lane & 31, h = lane >> 5;
+    const int wn = 64 * wave;
+
+    // A staging: chunk id = tid + THREADS u -> row id >> 3, 16-byte chunk id & 7
+    // of the stage's 128 bytes; rows past mrows lie past the buffer's end and
+    // load as 0; the stage index is clamped, so every load is in range.
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(Aq + (size_t)m0 * K, (uint32_t)((size_t)mrows * K));
+    uint32_t va[AP];
+#pragma unroll
+    for (int u = 0; u < AP; ++u) {
+        const int id = tid + TH * u;
+        va[u] = (uint32_t)((id >> 3) * K + 16 * (id & 7));
+    }
+    uint4 av[AP];
+    auto a_load = [&](int g) __attribute__((always_inline)) {
+        const int gc = g < groups ? g : groups - 1;
+#pragma unroll
+        for (int u = 0; u < AP; ++u) {
+            const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u], gc * kGS, 0);
+            av[u] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
+        }
+    };
+    // 1 / SA of the tile's rows: threads t, t + BM, ... stage row t % BM (rows
+    // past mrows load row mrows - 1, as the last group's row m0 + srow may lie
+    // past SA's end and the SGPR offset is not range-checked, and store 0)
+    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - sa_off - m0) * 2));
+    const int srow = tid & (BM - 1);
+    const uint32_t vsa = (uint32_t)min(srow, mrows - 1) * 2;
+    uint32_t sa_raw = 0;
+    auto sa_load = [&](int g) __attribute__((always_inline)) {
+        const int gc = g < groups ? g : groups - 1;
+        sa_raw = __builtin_amdgcn_raw_buffer_load_b16(rSA, vsa, gc * lda * 2, 0);
+    };
+    auto a_store = [&](int buf) __attribute__((always_inline)) {
+        uint8_t *base = lds + buf * TC::SBYTES;
+#pragma unroll
+        for (int u = 0; u < AP; ++u) {
+            const int id = tid + TH * u;
+            const uint32_t d[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
+            uint32_t o[4];
+            transpose4x4(d, o);
+            *(uint4 *)(base + (id >> 3) * QA_PITCH + 16 * (id & 7)) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        const float sa = dt2f<BF16>(sa_raw);
+        *(float *)(base + TC::ABYTES + 4 * srow) = (srow < mrows && sa != 0.0f) ? 1.0f / sa : 0.0f;
+    };
+
+    // B words of this wave: 32-column block cb, k-chunk kc of group g -> word
+    // kp = 8 g + 2 kc + h of column n0 + wn + 32 cb + c32.  The offsets advance
+    // a group per load, so the loads past the last group (and a block past N
+    // in the last word row) return 0; a block past N elsewhere reads the next
+    // row's words, in range, feeding outputs that are not stored.
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rSB = buf_rsrc(SB + n0, (uint32_t)(((size_t)groups * N - n0) * 2));
+    uint32_t vb[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) vb[kc] = (uint32_t)(((2 * kc + h) * N + wn + c32) * 4);
+    uint32_t vsb = (uint32_t)((wn + c32) * 2);
+    uint32_t bw[2][4], sraw[2];
+    auto b_load = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc)
+                bw[cb][kc] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb[kc] + 128 * cb, 0, 0);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) sraw[cb] = __builtin_amdgcn_raw_buffer_load_b16(rSB, vsb + 64 * cb, 0, 0);
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) vb[kc] += (uint32_t)(32 * N);
+        vsb += (uint32_t)(2 * N);
+    };
+
+    f32x16_t acc[RMB][2];
+#pragma unroll
+    for (int mb = 0; mb < RMB; ++mb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = f32x16_t{};
+
+    // Stage g reads buffer g % 3.  B words and scales are loaded one stage
+    // ahead, A and SA one and a half: at the middle of stage g every wave
+    // stores stage g + 1's A into buffer (g + 1) % 3 and meets the stage's one
+    // barrier; that buffer was last read in stage g - 2, before the previous
+    // stage's barrier.
+    a_load(0);
+    sa_load(0);
+    b_load();
+    a_store(0);
+    a_load(1);
+    sa_load(1);
+    __syncthreads();
+    int cur = 0;
+    for (int g = 0; g < groups; ++g) {
+        const int nxt = cur == 2 ? 0 : cur + 1;
+        const uint8_t *abuf = lds + cur * TC::SBYTES;
+        i32x4_t bf[2][4];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) bf[cb][kc] = decode_s2(bw[cb][kc]);
+        const float sbf[2] = {dt2f<BF16>(sraw[0]), dt2f<BF16>(sraw[1])};
+        b_load();
+#pragma unroll
+        for (int mb = 0; mb < RMB; ++mb) {
+            if (mb == RMB / 2) {
+                a_store(nxt);  // past the last stage: never read
+                __syncthreads();
+                a_load(g + 2);
+                sa_load(g + 2);
+            }
+            const int row = 32 * mb + c32;
+            i32x4_t af[4];
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                const uint4 v = *(const uint4 *)(abuf + row * QA_PITCH + 16 * (2 * kc + h));
+                af[kc] = i32x4_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+            // 1 / SA of this lane's rows 32 mb + 8 j + 4 h + i (i = 0..3)
+            f32x4_t inv4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) inv4[j] = *(const f32x4_t *)(abuf + TC::ABYTES + 4 * (32 * mb + 8 * j + 4 * h));
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                i32x16_t dot = mfma_i8_32(af[0], bf[cb][0], i32x16_t{});
+#pragma unroll
+                for (int kc = 1; kc < 4; ++kc) dot = mfma_i8_32(af[kc], bf[cb][kc], dot);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[mb][cb][v] += (float)dot[v] * (sbf[cb] * inv4[v >> 2][v & 3]);
+            }
+        }
+        cur = nxt;
+    }
+
+    // Epilogue through LDS, one 32-column block and 16-row half of each 32-row
+    // block at a time: element e of lane (c32, h) is row 8 (e / 4) + 4 h + e % 4
+    // of its 32-row block, column c32; the wave writes its [16 RMB][EP_PITCH]
+    // fp32 block and reads back 4 adjacent columns of one row per lane
+    // (8 lanes per row of 32 columns) for epi_store4_c.
+    constexpr int EP = TC::EP_PITCH;
+    float *ct = (float *)lds + (size_t)wave * 16 * RMB * EP;
+    __syncthreads();  // the stage buffers are free
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+        constexpr int P = decltype(P_)::value;
+        constexpr bool F32 = decltype(F_)::value;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const int n = n0 + wn + 32 * cb + 4 * (lane & 7);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+                for (int mb = 0; mb < RMB; ++mb)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        ct[(16 * mb + 8 * (j >> 2) + 4 * h + (j & 3)) * EP + c32] = acc[mb][cb][8 * hf + j];
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int pass = 0; pass < 2 * RMB; ++pass) {
+                    const int br = 8 * pass + (lane >> 3);
+                    const int r = 32 * (br >> 4) + 16 * hf + (br & 15);
+                    const float4 t = *(const float4 *)(ct + br * EP + 4 * (lane & 7));
+                    const float v4[4] = {t.x, t.y, t.z, t.w};
+                    if (r < mrows && n < N) epi_store4_c<BF16, P, F32>(C, Other, Bias, N, m0 + r, n, v4);
+                }
+                __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes
+            }
+        }
+    });
+}
+
 // Test hook: the MFMA B fragment each word decodes to (4 dwords per word).
 __global__ void k_int2_s8_decode(const uint32_t *__restrict__ B, uint32_t *__restrict__ D, int words) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -468,56 +727,91 @@ static hipError_t int8_gemm_launch(int dtype, const void *Asrc, const void *SA, 
     return hipGetLastError();
 }
 
-// The int8 MoE prefill's grouped GEMM on the expert-sorted rows: Aq [G][K]
-// int8 from quant_a (upfront), or, Aq NULL, the DT rows A quantized while
-// staged; SA [K/128][ldsa(G)].  Grid: an upper bound of the row tiles (each
-// expert's ragged tail adds at most one) times the column blocks.
-template <bool QA>
-static hipError_t int8_moe_launch(int dtype, const int *meta, const void *Asrc, const void *SA, const uint32_t *B,
-                                  const void *SB, void *C, const void *Other, int E, int G, int N, int K,
-                                  int postop, int out_f32, hipStream_t st) {
-    typedef QTile<4, 4, 2, 2> TC;
-    const int ntn = (N + TC::BN - 1) / TC::BN;
-    const int max_tiles = (G + TC::BM - 1) / TC::BM + E;
-    const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
+// The wide-tile engine (QMODE 0: int8 Aq from quant_a).
+static hipError_t int8_gemm_w_launch(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
+                                     const void *SB, void *C, const void *Other, const void *Bias, int M, int N,
+                                     int K, int postop, int out_f32, hipStream_t st) {
+    typedef WideTile TC;
+    const int mt = (M + TC::BM - 1) / TC::BM, nt = (N + TC::BN - 1) / TC::BN;
+    const dim3 grid(xcd_ashare_grid(mt, nt)), block(TC::THREADS);
     if (dtype == TERNOCL_BF16)
-        hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, QA, true>), grid, block, 0, st, Asrc, (const uint16_t *)SA,
-                           B, (const uint16_t *)SB, C, (const uint16_t *)Other, nullptr, G, N, K, postop, out_f32,
-                           meta, E);
+        hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
+                           (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32,
+                           nullptr, 0);
     else
-        hipLaunchKernelGGL((k_int2_int8_gemm<TC, false, QA, true>), grid, block, 0, st, Asrc, (const uint16_t *)SA,
-                           B, (const uint16_t *)SB, C, (const uint16_t *)Other, nullptr, G, N, K, postop, out_f32,
-                           meta, E);
+        hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
+                           (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32,
+                           nullptr, 0);
+    return hipGetLastError();
+}
+
+// The int8 MoE prefill's grouped GEMM on the expert-sorted rows: Aq [G][K]
+// int8 from quant_a (upfront: the wide-tile engine), or, Aq NULL, the DT rows
+// A quantized while staged (the 128 x 128 engine); SA [K/128][ldsa(G)].
+// Grid: an upper bound of the row tiles (each expert's ragged tail adds at
+// most one) times the column blocks.  Both engines' tiles have the route's
+// 128 rows.
+static hipError_t int8_moe_launch(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
+                                  const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G,
+                                  int N, int K, int postop, int out_f32, hipStream_t st) {
+    const bool bf = dtype == TERNOCL_BF16;
+    const uint16_t *sa = (const uint16_t *)SA, *sb = (const uint16_t *)SB, *oth = (const uint16_t *)Other;
+    if (Aq) {
+        typedef WideTile TC;
+        const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
+        const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
+        if (bf)
+            hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
+                               nullptr, G, N, K, postop, out_f32, meta, E);
+        else
+            hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
+                               nullptr, G, N, K, postop, out_f32, meta, E);
+    } else {
+        typedef QTile<4, 4, 2, 2> TC;
+        const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
+        const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
+        if (bf)
+            hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, true, true>), grid, block, 0, st, A, sa, B, sb, C, oth,
+                               nullptr, G, N, K, postop, out_f32, meta, E);
+        else
+            hipLaunchKernelGGL((k_int2_int8_gemm<TC, false, true, true>), grid, block, 0, st, A, sa, B, sb, C, oth,
+                               nullptr, G, N, K, postop, out_f32, meta, E);
+    }
     return hipGetLastError();
 }
 
 ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
                                  const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G, int N,
                                  int K, int postop, int out_f32, hipStream_t st) {
-    const hipError_t e = Aq ? int8_moe_launch<false>(dtype, meta, Aq, SA, B, SB, C, Other, E, G, N, K, postop,
-                                                     out_f32, st)
-                            : int8_moe_launch<true>(dtype, meta, A, SA, B, SB, C, Other, E, G, N, K, postop,
-                                                    out_f32, st);
-    return launch_status(e);
+    return launch_status(int8_moe_launch(dtype, meta, A, Aq, SA, B, SB, C, Other, E, G, N, K, postop, out_f32, st));
 }
 
-int int8_moe_tile_rows() { return QTile<4, 4, 2, 2>::BM; }
+int int8_moe_tile_rows() {
+    static_assert(QTile<4, 4, 2, 2>::BM == WideTile::BM, "both grouped engines tile the route's rows");
+    return WideTile::BM;
+}
 
+// Tile planner: the 128 x 512 wide tile whenever it yields at least 192 tiles
+// (three quarters of the 256 CUs, one workgroup each); else 128 x 128 tiles
+// (2 x 2 waves of 64 x 64, two workgroups per CU), which fill the chip at a
+// quarter of the wide tile's width (at M = 1024, K = 14336, N = 4096: 64 wide
+// tiles, 252 us, against 147 us on 256 narrow ones).  QMODE 1 (DT A quantized
+// while staged) always runs the 128 x 128 engine.
 ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
                                   hipStream_t st) {
-    // 128 x 128 tiles, 2 x 2 waves of 64 x 64: two waves per SIMD (a 128-row
-    // wave tile's 128 fp32 accumulators do not fit beside the rest)
     typedef QTile<4, 4, 2, 2> Tile;
     const size_t es = Aq ? 1 : 2;
     if ((size_t)M * K * es >= (1u << 31) || (size_t)(K / 16) * N * 4 >= (1u << 31)) {
         set_error("int2_int8_gemm: the A operand and B must each be below 2^31 bytes");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
-    const hipError_t e = Aq
-        ? int8_gemm_launch<Tile, false>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
-        : int8_gemm_launch<Tile, true>(dtype, A, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
+    const bool wide = Aq && (size_t)((M + WideTile::BM - 1) / WideTile::BM) * ((N + WideTile::BN - 1) / WideTile::BN) >= 192;
+    const hipError_t e =
+        wide  ? int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+        : Aq  ? int8_gemm_launch<Tile, false>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+              : int8_gemm_launch<Tile, true>(dtype, A, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
     return launch_status(e);
 }
 

@@ -127,6 +127,49 @@ def test_int8_gemm_parity(dev, orc, M, K, N, bf16):
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
 
 
+def _wide_tile(M, N):
+    """The library's planner rule: the 128 x 512 tile when it yields >= 192 tiles."""
+    return -(-M // 128) * -(-N // 512) >= 192
+
+
+# shapes the planner sends to the 128 x 512 engine: a ragged last row tile
+# (1500 = 11 * 128 + 92), a ragged last column tile (8208 = 16 * 512 + 16:
+# one 16-column block of one wave), and an exact tiling
+WIDE_SHAPES = [(1500, 256, 8208), (1024, 512, 14336), (1536, 384, 12304)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", WIDE_SHAPES)
+def test_int8_gemm_wide_tile_parity(dev, orc, M, K, N, bf16):
+    """Every output of the 128 x 512 engine, all 2-bit codes, against the oracle."""
+    import torch
+    import ternocl_amd as T
+    assert _wide_tile(M, N)
+    print(f"int8 wide-tile gemm M={M} K={K} N={N} bf16={bf16}", flush=True)
+    A, B, SB, other, bias_f = _int8_case(4100 + M + N, M, K, N, bf16, all_codes=True)
+    dC = _int8_run(T, torch, A, B, SB, other, bias_f, M, K, N, bf16, 0, False)
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, 0, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_int8_gemm_wide_tile_epilogues(dev, orc, bf16, postop, out_f32):
+    import torch
+    import ternocl_amd as T
+    M, K, N = 1500, 128, 8208
+    assert _wide_tile(M, N)
+    print(f"int8 wide-tile epilogue postop={postop} out_f32={out_f32} bf16={bf16}", flush=True)
+    A, B, SB, other, bias_f = _int8_case(191 + postop, M, K, N, bf16)
+    dC = _int8_run(T, torch, A, B, SB, other, bias_f, M, K, N, bf16, postop, out_f32)
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, postop, out_f32)
+    got = dC.cpu().numpy() if out_f32 else host_u16(dC)
+    bad, dmax = allclose_report(_as_f32(got, out_f32, bf16), _as_f32(want, out_f32, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_int8_gemm_all_codes_and_reference_distribution(dev, orc, bf16):
     """Every 2-bit code (code 2 = -2) and the reference driver's A ~ U[-5, 5]."""
