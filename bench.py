@@ -21,12 +21,17 @@ each timed the same way (> 2 GiB rotation, HIP-graph replays between events):
 
 Timing: the W warm-up steps and then exactly K timed steps are captured in HIP
 graphs (host launch overhead stays off the GPU timeline) and replayed on one
-stream between HIP events, after a device synchronize; per-kernel durations
-come from graphs of that kernel's launches alone.  Bytes follow the reference
+stream between HIP events, after a device synchronize; every figure is the
+median of 3 timed replays (the reference's median-of-3 re-measure,
+int2_fp16_upcvt/bench.sh:52-63).  `value` and `roofline` come from the timed
+step; per-kernel durations come from graphs of that kernel's launches alone,
+and each headline shape is also timed with its decode removed (the same kernel
+streaming the same bytes: the engine's memory ceiling, the reference's own
+method, int2_fp16_upcvt/README.md:135-137).  Bytes follow the reference
 byte models (int2_fp16_upcvt/main.cpp:331-333, bitcos_fp16_upcvt/main.cpp:289-293),
 ops 2*M*N*K (int2_moe/prefill.cpp:350 for the MoE layer).  The CPU baseline is
-the reference's own host gold (compiled from its sources into oracle/_ref)
-timed on this machine's CPU cores.
+the reference's own host golds (compiled from its sources into oracle/_ref)
+timed on this machine's CPU cores, all of them and one, per config.
 """
 from __future__ import annotations
 
@@ -124,11 +129,20 @@ def time_graph(torch, g, s):
     return e0.elapsed_time(e1) * 1e-3  # seconds
 
 
+REPEATS = 3  # every figure: the median of this many timed replays
+
+
+def median_replays(torch, g, s, reps=REPEATS):
+    """Median and all of reps timed replays of graph g (after one warm replay)."""
+    time_graph(torch, g, s)
+    ts = [time_graph(torch, g, s) for _ in range(reps)]
+    return float(np.median(ts)), ts
+
+
 def per_launch_us(torch, sb, n):
-    """Average duration of one launch of this shape (graph of n launches)."""
+    """Duration of one launch of this shape: a graph of n launches, median of 3 replays."""
     g, s = graph_of(torch, sb.launch, n)
-    time_graph(torch, g, s)  # warm replay
-    t = time_graph(torch, g, s)
+    t, _ = median_replays(torch, g, s)
     return t / n * 1e6
 
 
@@ -142,38 +156,115 @@ def check_parity(sb, orc, formats):
     return bad, float(d.max())
 
 
-def cpu_baseline(sample_s: float):
-    """The reference's host gold (compute_gold + epilogue_ref, compiled from the
-    reference sources into oracle/_ref) or, where that was not built, the
-    oracle's restatement of it, timed on this machine's CPU cores on the
-    (K=4096, N=14336) M = 1 shape, repeated for about sample_s seconds."""
-    from oracle import binding as orc
-    from ternocl_amd import formats, synth
-    M, K, N = 1, 4096, 14336
-    g = synth.rng(7)
-    A = synth.activations(g, (M, K), True)
-    B = synth.int2_weights(g, K, N)
-    S = synth.scales(g, K, N, True)
-    bias = formats.f32_to_dt(g.standard_normal(N).astype(np.float32) * np.float32(0.1), True)
-    kind = "reference" if orc.ref_available() else "port"
-    if kind == "reference":
-        gold = lambda: orc.ref_epilogue(orc.ref_int2_gold(A, B, S, M, K, N, True), None, bias, 3, False, True)
-    else:
-        gold = lambda: orc.epilogue(orc.int2_gold(A, B, S, M, K, N, True), None, bias, 3, False, True)
-    gold()
+def ceiling_us(torch, T, sb):
+    """The shape's GEMV kernel with the decode removed (ternocl_int2_gemv_stream_probe):
+    the same plan, weight and scale stream, reduction and stores, on the same
+    rotated weight sets; graph of 200 launches, median of 3."""
+    out = torch.empty((sb.M, sb.N), dtype=torch.float32, device="cuda")
+    it = [0]
+
+    def call():
+        s = it[0] % sb.sets
+        it[0] += 1
+        T.int2_gemv_stream_probe(sb.dB[s], sb.dS[s], out, sb.M, sb.N, sb.K)
+    return graph_time_us(torch, call, 200)
+
+
+def _rate(fn, sample_s):
+    """Calls of fn in about sample_s seconds (at least one, after one untimed call)."""
+    fn()
     n, t0 = 0, time.perf_counter()
     while True:
-        gold()
+        fn()
         n += 1
         el = time.perf_counter() - t0
         if el >= sample_s or n >= 10000:
-            break
-    per = el / n
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    return {"value": round(gemv_bytes(M, K, N) / per / 1e9, 3), "unit": "GB/s", "cores": cores,
-            "kind": kind,
-            "sample": f"{n} calls of the host gold (compute_gold + epilogue_ref postop 3) for "
-                      f"M=1 K={K} N={N} bf16 in {el:.1f} s ({per * 1e3:.2f} ms/call), OpenMP over outputs"}
+            return n, el
+
+
+def cpu_baseline(sample_s: float):
+    """The reference's host golds (compiled from the reference sources into
+    oracle/_ref; where that was not built, the oracle's restatement) timed on
+    this machine's CPU cores, on all cores (OpenMP over outputs, as the golds
+    are written) and on one core.  The headline is the decode GEMV gold
+    (compute_gold + epilogue_ref postop 3) at M=1 K=4096 N=14336 bf16, about
+    sample_s seconds per core count; the other configs about sample_s / 4 each:
+      c1  M=1 K=N=4096 fp16 int2 gold, no epilogue (full);
+      c3  int8 gold (compute_scale_a + the s8 x s2 gold) on 8 of the 1024 rows:
+          the work is linear in the rows, so the rate is the full problem's;
+      c4  BITCOS gold M=1 K=5376 N=21504 fp16 z=.5 (full);
+      c5  the MoE prefill check's double-precision layer for 4 of the 2048
+          tokens (the oracle's restatement of int2_moe/prefill.cpp:289-318;
+          that driver is not compiled), rate per token."""
+    from oracle import binding as orc
+    from ternocl_amd import formats, synth
+    ref = orc.ref_available()
+    kind = "reference" if ref else "port"
+    cores = orc.max_threads()
+    g = synth.rng(7)
+    # c2: the headline shape
+    M, K, N = 1, 4096, 14336
+    A, B, S = synth.activations(g, (M, K), True), synth.int2_weights(g, K, N), synth.scales(g, K, N, True)
+    bias = formats.f32_to_dt(g.standard_normal(N).astype(np.float32) * np.float32(0.1), True)
+    if ref:
+        c2 = lambda: orc.ref_epilogue(orc.ref_int2_gold(A, B, S, M, K, N, True), None, bias, 3, False, True)
+    else:
+        c2 = lambda: orc.epilogue(orc.int2_gold(A, B, S, M, K, N, True), None, bias, 3, False, True)
+    # c1
+    A1, B1, S1 = synth.activations(g, (1, 4096), False), synth.int2_weights(g, 4096, 4096), synth.scales(g, 4096, 4096, False)
+    c1 = (lambda: orc.ref_int2_gold(A1, B1, S1, 1, 4096, 4096, False)) if ref else \
+         (lambda: orc.int2_gold(A1, B1, S1, 1, 4096, 4096, False))
+    # c3: 8 rows of the M=1024 prefill
+    r3, K3, N3 = 8, 4096, 14336
+    A3, B3, S3 = synth.activations(g, (r3, K3), False), synth.int2_weights(g, K3, N3), synth.scales(g, K3, N3, False)
+    if ref:
+        c3 = lambda: orc.ref_int8_gold(A3, B3, orc.ref_scale_a(A3, r3, K3, False), S3, r3, K3, N3, False)
+    else:
+        c3 = lambda: orc.int8_gold(A3, B3, orc.scale_a(A3, r3, K3, False), S3, r3, K3, N3, False)
+    # c4
+    K4, N4 = 5376, 21504
+    A4 = synth.activations(g, (1, K4), False)
+    buf4, _ = synth.bitcos_weights(g, K4, N4, 0.5)
+    S4 = synth.scales(g, K4, N4, False)
+    c4 = (lambda: orc.ref_bitcos_gold(A4, buf4, S4, 1, K4, N4, False)) if ref else \
+         (lambda: orc.bitcos_gold(A4, buf4, S4, 1, K4, N4, False))
+    bytes4 = formats.bitcos_bytes(buf4) + K4 * 2 + N4 * 2 + (K4 // 128) * N4 * 2
+    # c5: 4 tokens of the MoE layer
+    Tk, E, topk, H, I, t5 = 2048, 64, 8, 2048, 1408, 4
+    X5 = synth.activations(g, (t5, H), True)
+    ids5, RW5 = synth.moe_routing(g, t5, E, topk, True)
+    w5 = []
+    for K_, N_ in ((H, I), (H, I), (I, H)):
+        w5.append(np.stack([synth.int2_weights(g, K_, N_) for _ in range(E)]))
+        w5.append(np.stack([synth.scales(g, K_, N_, True) for _ in range(E)]))
+    c5 = lambda: orc.moe_ref_tokens(X5, ids5, RW5, 0, t5, topk, H, I, *w5, True)
+    flops5 = 2.0 * t5 * topk * (2 * H * I + I * H)
+
+    configs = [
+        ("c2", c2, sample_s, gemv_bytes(M, K, N), 1e9, "GB/s", f"M=1 K={K} N={N} bf16 compute_gold + epilogue_ref postop 3"),
+        ("c1", c1, sample_s / 4, 1 * 4096 * 2 + 4096 * 4096 / 4 + 4096 * 2 + 32 * 4096 * 2, 1e9, "GB/s",
+         "M=1 K=N=4096 fp16 compute_gold"),
+        ("c3", c3, sample_s / 4, 2.0 * r3 * N3 * K3, 1e12, "TOPS",
+         f"compute_scale_a + int8 compute_gold on {r3} of the 1024 rows, K={K3} N={N3} fp16 (rate = full problem's)"),
+        ("c4", c4, sample_s / 4, bytes4, 1e9, "GB/s", f"BITCOS compute_gold M=1 K={K4} N={N4} fp16 z=.5"),
+        ("c5", c5, sample_s / 4, flops5, 1e12, "TFLOPS",
+         f"MoE prefill check layer (double) for {t5} of {Tk} tokens, E={E} top-{topk} H={H} I={I} (oracle restatement)"),
+    ]
+    per = {}
+    for name, fn, secs, work, scale, unit, what in configs:
+        e = {"unit": unit, "sample": what}
+        for tag, nth in (("all_cores", cores), ("one_core", 1)):
+            orc.set_threads(nth)
+            n, el = _rate(fn, secs if tag == "all_cores" else secs / 2)
+            e[tag] = {"value": round(work * n / el / scale, 4), "cores": nth, "calls": n,
+                      "ms_per_call": round(el / n * 1e3, 3)}
+        per[name] = e
+    orc.set_threads(cores)
+    head = per["c2"]["all_cores"]
+    return {"value": head["value"], "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"{head['calls']} calls of the host gold (compute_gold + epilogue_ref postop 3) for "
+                      f"M=1 K={K} N={N} bf16 ({head['ms_per_call']} ms/call), OpenMP over outputs",
+            "one_core": per["c2"]["one_core"], "per_config": per}
 
 
 def rotation(torch, tensors, set_bytes):
@@ -183,10 +274,10 @@ def rotation(torch, tensors, set_bytes):
 
 
 def graph_time_us(torch, fn, n):
-    """Average duration of one fn() call from a HIP graph of n calls (warm replay first)."""
+    """Duration of one fn() call from a HIP graph of n calls (warm replay, then the median of 3)."""
     g, s = graph_of(torch, fn, n)
-    time_graph(torch, g, s)
-    return time_graph(torch, g, s) / n * 1e6
+    t, _ = median_replays(torch, g, s)
+    return t / n * 1e6
 
 
 def dev16(torch, a, bf16):
@@ -519,7 +610,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-sample-s", type=float, default=12.0)
+    ap.add_argument("--cpu-sample-s", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the M = 2, 4, 8 sweep and the VALU and bf16-MFMA engines")
     ap.add_argument("--only-headline", action="store_true", help="skip the prefill, C1, C4 and C5 workloads")
@@ -611,17 +702,20 @@ def main():
     for sb in sbs:
         parity.append(check_parity(sb, orc, formats))
 
-    # warm-up steps, then exactly K timed steps, each a graph replay
+    # warm-up steps, then exactly K timed steps, each a graph replay; the K-step
+    # graph is replayed REPEATS times and the median is the value
     gw, sw = graph_of(torch, step, max(args.warmup, 1))
     gt, st = graph_of(torch, step, args.steps)
     torch.cuda.synchronize()
     time_graph(torch, gw, sw)
-    t = time_graph(torch, gt, st)
+    ts = [time_graph(torch, gt, st) for _ in range(REPEATS)]
+    t = float(np.median(ts))
     replay_same = all(np.array_equal(sb.output(), e) for sb, e in zip(sbs, eager))
     step_bytes = sum(sb.bytes() for sb in sbs)
     value = step_bytes * args.steps / t / 1e9
 
-    # per-shape launch durations (graph of that shape alone)
+    # per-shape launch durations (graph of that shape alone), and the same
+    # kernel with the decode removed (the memory ceiling of its structure)
     shapes = {}
     tot_b, tot_t = 0.0, 0.0
     for sb, (bad, dmax) in zip(sbs, parity):
@@ -629,10 +723,13 @@ def main():
         gbs = sb.bytes() / (us * 1e-6) / 1e9
         tot_b += sb.bytes()
         tot_t += us
+        c_us = ceiling_us(torch, T, sb)
         shapes[f"K{sb.K}_N{sb.N}"] = {"us_per_launch": round(us, 3), "GB/s": round(gbs, 1),
                                       "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(sb.bytes()),
+                                      "decode_removed_us": round(c_us, 3),
+                                      "of_decode_removed": round(c_us / us, 4),
                                       "weight_sets": sb.sets, "parity_bad": bad, "max_abs_diff": dmax}
-    achieved = tot_b / (tot_t * 1e-6) / 1e9
+    isolated = tot_b / (tot_t * 1e-6) / 1e9
 
     extra = {}
     if not args.no_sweep:
@@ -700,8 +797,14 @@ def main():
                                "step = (K=4096,N=14336) + (K=14336,N=4096)",
                    "M": 1, "shapes": [list(s) for s in SHAPES], "epilogue": "acc + bias[n] + residual",
                    "engine": "fp8 x fp4 block-scaled MFMA (engine 4)"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "measured": "the timed step (value): algorithmic bytes of its two GEMV launches / "
+                                 "their time, median of 3 replays of the K-step graph",
+                     "isolated_per_shape": {"achieved": round(isolated, 1),
+                                            "frac": round(isolated / HBM_PEAK_GBS, 4),
+                                            "measured": "each shape's launches alone in a graph of 200"}},
+        "repeats": {"n": REPEATS, "step_ms": [round(x / args.steps * 1e3, 5) for x in ts]},
         "shapes": shapes,
         "parity": {"ok": all(b == 0 for b, _ in parity) and replay_same,
                    "graph_replay_bit_identical": replay_same,

@@ -112,6 +112,15 @@ ternocl_status ternocl_int2_dequant(int dtype, const uint32_t *B, const void *S,
                                     int N, void *stream);
 ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B, uint32_t *D,
                                         int K, int N, void *stream);
+/* Measurement hook, no GEMV: the decode GEMV's kernel (engine 4, the plan it
+ * takes for this M, N, K) with the decode removed -- no activations, no MFMA;
+ * it streams the same B and S bytes with the same grid, cross-wave reduction
+ * and stores, writing C[m, n] = a checksum of column n's words.  Its duration
+ * is the engine's memory ceiling, measured as the reference measures its own
+ * (int2_fp16_upcvt/README.md:135-137: the GEMV with the decode removed).
+ * C: fp32 [M, N]; M <= 4, N % 16 == 0, K % 128 == 0. */
+ternocl_status ternocl_int2_gemv_stream_probe(int dtype, const uint32_t *B, const void *S, void *C, int M,
+                                             int N, int K, void *stream);
 
 /* ---- int2 x int8 prefill ---------------------------------------------------
  * Replaces quant_a (int2_via_int2_x_int8_dpas/int2_int8_dpas.cl:105-106):

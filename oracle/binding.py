@@ -240,6 +240,17 @@ def moe_ref_tokens(X, ids, RW, T0, T1, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16:
     return O
 
 
+def set_threads(n: int) -> None:
+    """OpenMP threads of the oracle's and (where built) the compiled reference's loops."""
+    orc().orc_set_threads(int(n))
+    if ref_available():
+        ref().ref_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(orc().orc_max_threads())
+
+
 # ---- the compiled reference (oracle/_ref) ------------------------------------
 
 def ref_int2_gold(A, B, S, M, K, N, bf16: bool) -> np.ndarray:

@@ -57,6 +57,9 @@ namespace ref_bitcos {
 extern "C" {
 
 void ref_set_bf16(int bf16) { dt_is_bf16() = bf16 != 0; }
+// OpenMP threads of the reference's gold loops (the CPU baseline times 1 core and all)
+void ref_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int ref_max_threads() { return omp_get_max_threads(); }
 float ref_tof(uint16_t h) { return tof(h); }
 uint16_t ref_fromf(float f) { return fromf(f); }
 

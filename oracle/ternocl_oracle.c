@@ -47,6 +47,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -493,3 +494,7 @@ void orc_moe_ref_tokens(int bf16, const uint16_t *X, const int *ids, const uint1
         free(h);
     }
 }
+
+/* OpenMP threads of the oracle's loops (the CPU baseline times 1 core and all). */
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int orc_max_threads(void) { return omp_get_max_threads(); }

@@ -85,6 +85,9 @@ void orc_moe_ref_tokens(int bf16, const uint16_t *X, const int *ids, const uint1
                         const uint32_t *Bu, const uint16_t *Su, const uint32_t *Bd,
                         const uint16_t *Sd, double *O, int round_up);
 
+void orc_set_threads(int n);
+int orc_max_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

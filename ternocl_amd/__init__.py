@@ -22,7 +22,7 @@ from . import _abi
 __all__ = [
     "TernoclError", "lib", "library_path", "FP16", "BF16",
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
-    "int2_gemv_decode", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
+    "int2_gemv_decode", "int2_gemv_stream_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
     "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
     "bitcos_fp16_upcvt_gemm", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
@@ -146,6 +146,14 @@ def int2_gemv_decode(B, D, K: int, N: int, bf16: bool, engine: int = MFMA, strea
 
 
 # ---- int2 x int8 (int2_via_int2_x_int8_dpas/int2_int8_dpas.cl) ------------
+
+def int2_gemv_stream_probe(B, S, C, M: int, N: int, K: int, stream=None) -> None:
+    """The decode GEMV (engine 4) with the decode removed: streams B and S as the GEMV
+    does and writes a checksum per column into C (fp32 [M, N]) -- a memory-ceiling
+    measurement, not a GEMV.  The dtype comes from S."""
+    _check(lib().ternocl_int2_gemv_stream_probe(_dtype_of(S), _ptr(B), _ptr(S), _ptr(C), M, N, K,
+                                                 _stream(stream)))
+
 
 def ldsa(M: int) -> int:
     """Row pitch of SA, (M + 31) & ~31 (LDSA of int2_int8_dpas.cl:58)."""

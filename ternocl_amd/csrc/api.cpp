@@ -49,6 +49,8 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
                                 const void *Other, const void *Bias, int M, int N, int K, int postop,
                                 int out_f32, int waves, int cpl, int gpw, hipStream_t st);
 ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
+ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const void *S, void *C, int M, int N,
+                                          int K, hipStream_t st);
 // kernels (int2_gemm_mfma.hip)
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
@@ -230,6 +232,17 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
     if (engine == 3) return int2_gemm_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     if (engine == 2) return int2_mfma_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
     return int2_gemv_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
+}
+
+ternocl_status ternocl_int2_gemv_stream_probe(int dtype, const uint32_t *B, const void *S, void *C, int M,
+                                             int N, int K, void *stream) {
+    ternocl_status s = check_dtype(dtype);
+    if (s != TERNOCL_OK) return s;
+    if (!B || !S || !C) FAIL(TERNOCL_ERR_INVALID_ARG, "B, S and C must be non-null");
+    if (M < 1 || N < 16 || N % 16 || K < kGS || K % kGS)
+        FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "need M >= 1, N % 16 == 0 and K % 128 == 0");
+    if ((size_t)(K / 16) * N * 4 >= 0x80000000u) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "B must be below 2^31 bytes");
+    return int2_gemv_stream_probe_run(dtype, B, S, C, M, N, K, (hipStream_t)stream);
 }
 
 int ternocl_ldsa(int M) { return (M + 31) & ~31; }

@@ -143,6 +143,10 @@ __host__ __device__ constexpr int f4_window_bytes(int rr, int gpw) { return (gpw
 // QM 3 (the MoE decode's down GEMV): A is fp32, gate rows, with the up rows
 // ldsa floats further; the activation is h = DT(gate * sigmoid(gate) * up),
 // the reference's rounding point (int2_moe/int2_moe.cl:95).
+// QM 4 (a measurement, not a GEMV): the kernel with the decode removed -- no
+// activations, no pieces, no MFMA; it streams the same weight and scale bytes
+// with the same grid, reduction and stores (acc += float(w0 ^ w1) * s), the
+// memory ceiling of the engine's structure.
 template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
     static constexpr bool I8 = QM == 1 || QM == 2;
     static constexpr int P = I8 ? 2 : f4_pieces(BF16), RS = kF4RowStride, RR = RS * MR;
@@ -391,7 +395,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
                int K, int postop, int out_f32, int swz, F4Group grp = F4Group{},
                const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
-    constexpr bool I8 = QM == 1 || QM == 2;
+    constexpr bool I8 = QM == 1 || QM == 2, NODEC = QM == 4;
     constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
     static_assert(RR <= 16, "too many MFMA rows");
     extern __shared__ uint8_t lds8[];
@@ -441,13 +445,13 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int rho = c & (RR - 1);  // A row (piece row) this lane feeds; rows >= RR are don't-care
 
     F4Stage<MR, GPW, BF16, QM> st;
-    st.load(A, M, K, groups, g0w, lane, SA, ldsa);
+    if constexpr (!NODEC) st.load(A, M, K, groups, g0w, lane, SA, ldsa);
     int after = f4_loads_after_barrier();
     F4Slab<CPL, GPW> cur;
     cur.load(B + after, S + after, N, groups, g0w, q, n0);
     F4EpiIn<MR, CPL, BF16> ein;  // behind the weights: waited for only at the epilogue
     ein.load(Other, Bias, postop, out_f32, M, N, q, n0, wave == 0);
-    st.store(wlds, lane);
+    if constexpr (!NODEC) st.store(wlds, lane);
 
     constexpr int ROWS = I8 ? 1 : P;  // accumulators per column: the pieces of row m = q, or their sum
     float acc[CPL][ROWS];
@@ -462,7 +466,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         const bool more = win + 1 < windows;
         F4Slab<CPL, GPW> nxt;
         if (more) {
-            st.load(A, M, K, groups, (win + 1) * gw + g0w, lane, SA, ldsa);
+            if constexpr (!NODEC) st.load(A, M, K, groups, (win + 1) * gw + g0w, lane, SA, ldsa);
             after = f4_loads_after_barrier();
             nxt.load(B + after, S + after, N, groups, (win + 1) * gw + g0w, q, n0);
         }
@@ -470,6 +474,12 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         for (int gi = 0; gi < GPW; ++gi) {
             const int g = win * gw + g0w + gi;
             if (g >= groups) break;  // uniform across the wave
+            if constexpr (NODEC) {
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+                    acc[j][0] += (float)(cur.w[gi][0].v[j] ^ cur.w[gi][1].v[j]) * dt2f<BF16>(cur.scale(gi, j));
+                continue;
+            }
             const uint8_t *row = buf + (gi * RR + rho) * 128 + 32 * q;
             const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
             const int sa = buf[GPW * RR * 128 + (gi * RR + rho) * 4 + q];
@@ -504,7 +514,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         if (more) {
             asm volatile("" ::: "memory");
             uint8_t *nb = wlds + (size_t)((win + 1) & 1) * WB;
-            st.store(nb, lane);
+            if constexpr (!NODEC) st.store(nb, lane);
             cur = nxt;
         }
     }
@@ -632,7 +642,7 @@ F4Plan f4_plan(bool bf16, int M, int N, int K, int waves, int cpl, int gpw) {
     return p;
 }
 
-template <int MR, int CPL, int GPW, bool BF16>
+template <int MR, int CPL, int GPW, bool BF16, int QMODE = 0>
 hipError_t f4_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
                        const void *Other, const void *Bias, int M, int N, int K, int postop,
                        int out_f32, hipStream_t st) {
@@ -641,48 +651,48 @@ hipError_t f4_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const 
     } else {
         const int strips = N / (16 * CPL);
         const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
-        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16>), dim3(strips), dim3(64 * p.waves), p.lds,
+        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QMODE>), dim3(strips), dim3(64 * p.waves), p.lds,
                            st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other,
                            Bias, M, N, K, postop, out_f32, swz);
         return hipGetLastError();
     }
 }
 
-template <int MR, int CPL, bool BF16>
+template <int MR, int CPL, bool BF16, int QMODE = 0>
 hipError_t f4_launch_g(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
                        const void *Other, const void *Bias, int M, int N, int K, int postop,
                        int out_f32, hipStream_t st) {
     switch (p.gpw) {
-    case 1: return f4_launch_t<MR, CPL, 1, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    case 2: return f4_launch_t<MR, CPL, 2, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    case 4: return f4_launch_t<MR, CPL, 4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 1: return f4_launch_t<MR, CPL, 1, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 2: return f4_launch_t<MR, CPL, 2, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 4: return f4_launch_t<MR, CPL, 4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     case 8:
-        if constexpr (MR <= 2 && CPL <= 2) return f4_launch_t<MR, CPL, 8, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        if constexpr (MR <= 2 && CPL <= 2) return f4_launch_t<MR, CPL, 8, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         return hipErrorInvalidValue;
     default:
-        if constexpr (MR == 1 && CPL == 1) return f4_launch_t<MR, CPL, 16, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        if constexpr (MR == 1 && CPL == 1) return f4_launch_t<MR, CPL, 16, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         return hipErrorInvalidValue;
     }
 }
 
-template <int MR, bool BF16>
+template <int MR, bool BF16, int QMODE = 0>
 hipError_t f4_launch_c(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
                        const void *Other, const void *Bias, int M, int N, int K, int postop,
                        int out_f32, hipStream_t st) {
-    if (p.cpl == 4) return f4_launch_g<MR, 4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    if (p.cpl == 2) return f4_launch_g<MR, 2, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    return f4_launch_g<MR, 1, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (p.cpl == 4) return f4_launch_g<MR, 4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (p.cpl == 2) return f4_launch_g<MR, 2, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return f4_launch_g<MR, 1, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
-template <bool BF16>
+template <bool BF16, int QMODE = 0>
 hipError_t f4_launch(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
                      const void *Other, const void *Bias, int M, int N, int K, int postop,
                      int out_f32, hipStream_t st) {
     switch (p.mr) {
-    case 1: return f4_launch_c<1, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    case 2: return f4_launch_c<2, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    case 4: return f4_launch_c<4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    default: return f4_launch_c<4, BF16>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 1: return f4_launch_c<1, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 2: return f4_launch_c<2, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 4: return f4_launch_c<4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    default: return f4_launch_c<4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     }
 }
 
@@ -836,6 +846,26 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
     }
     const hipError_t e = bf16 ? f4_launch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st)
                               : f4_launch<false>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    return launch_status(e);
+}
+
+// The decode-removed variant (QM 4) with the plan int2_gemv_f4_run would use
+// for the same shape: the memory ceiling of the engine (a measurement).
+ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const void *S, void *C, int M, int N,
+                                          int K, hipStream_t st) {
+    const bool bf16 = dtype == TERNOCL_BF16;
+    if (M < 1 || M > kF4MaxM || (size_t)M * N * 4 >= 0x7ff00000u) {
+        set_error("the decode-removed GEMV takes M <= 4 and M * N * 4 < 2^31 bytes of output");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    const F4Plan p = f4_plan(bf16, M, N, K, 0, 0, 0);
+    if (N % (16 * p.cpl) || p.lds > kF4MaxLds) {
+        set_error("N must be a multiple of 16 * cols_per_lane");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    // (C fp32: postop 0, out_f32 1)
+    const hipError_t e = bf16 ? f4_launch<true, 4>(p, nullptr, B, S, C, nullptr, nullptr, M, N, K, 0, 1, st)
+                              : f4_launch<false, 4>(p, nullptr, B, S, C, nullptr, nullptr, M, N, K, 0, 1, st);
     return launch_status(e);
 }
 

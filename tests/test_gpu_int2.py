@@ -217,6 +217,28 @@ def test_gemv_f4_decode_bit_exact(dev, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (1, 14336, 4096), (3, 1024, 512)])
+def test_gemv_stream_probe_checksum(dev, M, K, N, bf16):
+    """The decode-removed measurement kernel streams every word and scale it
+    should: row m < M of its output is half the sum over groups g of
+    float(B[8g + 2m, n] ^ B[8g + 2m + 1, n]) * S[g, n] (the words lane q = m of
+    the GEMV takes), to fp32 rounding."""
+    import torch
+    import ternocl_amd as T
+    g = synth.rng(71 + M)
+    B = g.integers(0, 2**32, size=(K // 16, N), dtype=np.uint32)
+    S = synth.scales(g, K, N, bf16)
+    C = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    T.int2_gemv_stream_probe(dev_raw(B), dev_dt(S, bf16), C, M, N, K)
+    torch.cuda.synchronize()
+    s = formats.dt_to_f32(S, bf16).astype(np.float64)
+    for m in range(M):
+        x = (B[2 * m::8] ^ B[2 * m + 1::8]).astype(np.float32).astype(np.float64)
+        want = 0.5 * (x * s).sum(axis=0)
+        np.testing.assert_allclose(C[m].cpu().numpy(), want, rtol=1e-5)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 1024), (2, 1024, 272), (4, 2048, 512)])
 def test_gemv_f4_pieces_exact(dev, orc, M, K, N, bf16):
     """The fp8 pieces sum to each activation exactly, so the fp32 result agrees
