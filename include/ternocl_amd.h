@@ -210,6 +210,29 @@ int ternocl_bitcos_pick_ls(int M, int N, int K);
 ternocl_status ternocl_bitcos_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,
                                       int N, void *stream);
 
+/* ---- host packers (CPU; no GPU call) -----------------------------------------
+ * Produce the kernels' weight formats from dense ternary weights W: int8
+ * [K, N] row-major, values -1, 0, +1 (any other value: TERNOCL_ERR_INVALID_ARG).
+ * ternocl_int2_pack: B uint32 [K/16][N], word (kp, n) bits 2j..2j+1 = code of
+ *   row 16 kp + j, codes 0 / 1 / 3 for 0 / +1 / -1 (int2_fp16_upcvt.cl:6-19;
+ *   the reference generates packed codes directly, int2_fp16_upcvt/main.cpp:238-242).
+ *   K % 16 == 0.  ternocl_int2_unpack is the reverse (code 2 reads as -2).
+ * ternocl_bitcos_pack: the BITCOS buffer of common/bitcos.hpp:1-8 (bitmap
+ *   [K/32][N] | offsets [N] | sign streams | 4 pad words), the layout
+ *   bitcos_random (common/bitcos.hpp:31-78) builds; ternocl_bitcos_pack_words
+ *   gives its length in uint32 words (0 for invalid W or shape).  K % 32 == 0.
+ *   ternocl_bitcos_unpack decodes a buffer back to W (bitcos_decode_col,
+ *   common/bitcos.hpp:97-106, for every column).
+ * ternocl_bitcos_slice_ranks_host: the slice ranks SR [ls-1][N] of
+ *   common/bitcos.hpp:81-94 on the host (ternocl_bitcos_slice_ranks computes
+ *   the same on the GPU). */
+ternocl_status ternocl_int2_pack(const int8_t *W, uint32_t *B, int K, int N);
+ternocl_status ternocl_int2_unpack(const uint32_t *B, int8_t *W, int K, int N);
+size_t ternocl_bitcos_pack_words(const int8_t *W, int K, int N);
+ternocl_status ternocl_bitcos_pack(const int8_t *W, int K, int N, uint32_t *buf, size_t words);
+ternocl_status ternocl_bitcos_unpack(const uint32_t *buf, size_t words, int K, int N, int8_t *W);
+ternocl_status ternocl_bitcos_slice_ranks_host(const uint32_t *buf, int K, int N, int ls, uint32_t *SR);
+
 /* ---- Hadamard input transform -------------------------------------------
  * Replaces hadamard_fwht(x, signs, y, K, use_signs) (hadamard/hadamard_fwht.cl:62-64)
  * with -DHB as an argument and the row count explicit:

@@ -23,6 +23,7 @@ __all__ = [
     "TernoclError", "lib", "library_path", "FP16", "BF16",
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
     "int2_gemv_decode", "int2_gemv_stream_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
+    "int2_pack", "int2_unpack", "bitcos_pack", "bitcos_unpack", "bitcos_slice_ranks_host",
     "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
     "bitcos_fp16_upcvt_gemm", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
@@ -153,6 +154,71 @@ def int2_gemv_stream_probe(B, S, C, M: int, N: int, K: int, stream=None) -> None
     measurement, not a GEMV.  The dtype comes from S."""
     _check(lib().ternocl_int2_gemv_stream_probe(_dtype_of(S), _ptr(B), _ptr(S), _ptr(C), M, N, K,
                                                  _stream(stream)))
+
+
+# ---- host packers (CPU, through the C ABI) -----------------------------------
+
+def _host_i8(W, K=None, N=None):
+    import numpy as np
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    if W.ndim != 2:
+        raise ValueError("W must be [K, N]")
+    return W
+
+
+def _cptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def int2_pack(W):
+    """int8 [K, N] ternary -> B uint32 [K/16, N] (ternocl_int2_pack)."""
+    import numpy as np
+    W = _host_i8(W)
+    K, N = W.shape
+    B = np.empty((K // 16, N), np.uint32)
+    _check(lib().ternocl_int2_pack(_cptr(W), _cptr(B), K, N))
+    return B
+
+
+def int2_unpack(B, K: int):
+    """B uint32 [K/16, N] -> int8 [K, N] (ternocl_int2_unpack)."""
+    import numpy as np
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    N = B.shape[1]
+    W = np.empty((K, N), np.int8)
+    _check(lib().ternocl_int2_unpack(_cptr(B), _cptr(W), K, N))
+    return W
+
+
+def bitcos_pack(W):
+    """int8 [K, N] ternary -> the BITCOS buffer, uint32 (ternocl_bitcos_pack)."""
+    import numpy as np
+    W = _host_i8(W)
+    K, N = W.shape
+    n = lib().ternocl_bitcos_pack_words(_cptr(W), K, N)
+    if n == 0:
+        raise TernoclError(1, "bitcos_pack: W must be ternary with K % 32 == 0")
+    buf = np.empty(n, np.uint32)
+    _check(lib().ternocl_bitcos_pack(_cptr(W), K, N, _cptr(buf), n))
+    return buf
+
+
+def bitcos_unpack(buf, K: int, N: int):
+    """The BITCOS buffer -> int8 [K, N] ternary (ternocl_bitcos_unpack)."""
+    import numpy as np
+    buf = np.ascontiguousarray(buf, dtype=np.uint32)
+    W = np.empty((K, N), np.int8)
+    _check(lib().ternocl_bitcos_unpack(_cptr(buf), buf.size, K, N, _cptr(W)))
+    return W
+
+
+def bitcos_slice_ranks_host(buf, K: int, N: int, ls: int):
+    """Slice ranks [ls-1, N] of a BITCOS buffer, on the host (ternocl_bitcos_slice_ranks_host)."""
+    import numpy as np
+    buf = np.ascontiguousarray(buf, dtype=np.uint32)
+    SR = np.zeros(max(ls - 1, 0) * N, np.uint32)
+    _check(lib().ternocl_bitcos_slice_ranks_host(_cptr(buf), K, N, ls, _cptr(SR) if SR.size else None))
+    return SR
 
 
 def ldsa(M: int) -> int:

@@ -42,6 +42,12 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_bitcos_slice_ranks": (I, [P, P, I, I, I, P]),
     "ternocl_bitcos_pick_ls": (I, [I, I, I]),
     "ternocl_bitcos_dequant": (I, [I, P, P, P, I, I, P]),
+    "ternocl_int2_pack": (I, [P, P, I, I]),
+    "ternocl_int2_unpack": (I, [P, P, I, I]),
+    "ternocl_bitcos_pack_words": (Z, [P, I, I]),
+    "ternocl_bitcos_pack": (I, [P, I, I, P, Z]),
+    "ternocl_bitcos_unpack": (I, [P, Z, I, I, P]),
+    "ternocl_bitcos_slice_ranks_host": (I, [P, I, I, I, P]),
     "ternocl_hadamard_fwht": (I, [I, P, P, P, I, I, I, I, P]),
     "ternocl_moe_tile_rows": (I, []),
     "ternocl_int2_moe_route": (I, [P, P, P, P, I, I, P]),
