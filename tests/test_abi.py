@@ -116,3 +116,12 @@ def test_operand_size_guards():
     for fn in (L.ternocl_int2_moe_prefill, L.ternocl_int2_moe_prefill_int8):
         assert fn(1, p, p, p, 65536, 8, 8, 2048, 2048, p, p, p, p, p, p, p, p, 1 << 40, None) == 2
     assert "2^31" in L.ternocl_last_error().decode()
+    # s8 x s2 GEMM: int8 A (M * K bytes) at 2^31
+    assert L.ternocl_int2_int8_gemm(0, None, p, p, p, p, p, None, None, 65536, 4096, 32768, 0, 0, None) == 2
+    assert "2^31" in L.ternocl_last_error().decode()
+    # M-tiled BITCOS: the re-packed int2 weights (K * N / 4 bytes of workspace) at 2^31
+    assert L.ternocl_bitcos_fp16_upcvt_gemm_mt(0, p, p, p, None, 1, p, None, None, 64, 131072, 65536, 0, 0,
+                                               p, 1 << 40, None) == 2
+    assert "2^31" in L.ternocl_last_error().decode()
+    # the decode-removed measurement kernel: B at 2^31 bytes
+    assert L.ternocl_int2_gemv_stream_probe(0, p, p, p, 1, 131072, 65536, None) == 2
