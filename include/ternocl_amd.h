@@ -60,11 +60,15 @@ const char *ternocl_version(void);
  * and int2_fp16_upcvt_gemm_mt (prefill, :341-343):
  *   C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(B[k,n])))
  * The library picks the kernel: a decode GEMV for M <= 16, an MFMA GEMM above.
- * ws / ws_bytes: optional device scratch, kept from the XeTLA plugin's entry
- * (the acc/cnt buffers of int2_upcvt_gemm_impl,
+ * ws / ws_bytes: optional device scratch (16-byte aligned), kept from the XeTLA
+ * plugin's entry (the acc/cnt buffers of its global k-slicing,
  * tools/xetla_epilogue_parity/parity.cpp:26-41); ternocl_int2_gemm_ws_bytes()
- * says how much a shape uses (0: pass NULL).  The GEMVs need none: each
- * workgroup owns whole columns, so no call keeps state between launches. */
+ * says how much a shape uses (0: pass NULL).  The prefill GEMM uses it for
+ * deterministic split-K on shapes whose 128 x 512 tiles would leave CUs idle
+ * (M = 1024, K = 14336, N = 4096: 4 K-slices): fp32 partial tiles per slice,
+ * then a reduction that adds the slices in order and applies the epilogue,
+ * the same bits on every run.  Without the scratch (NULL or short) those
+ * shapes run on 128 x 128 tiles instead.  The GEMVs need none. */
 size_t ternocl_int2_gemm_ws_bytes(int M, int N, int K);
 ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
                                             const void *S, void *C, const void *Other,

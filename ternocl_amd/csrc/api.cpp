@@ -54,7 +54,9 @@ ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const vo
 // kernels (int2_gemm_mfma.hip)
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
-                                  int postop, int out_f32, hipStream_t st);
+                                  int postop, int out_f32, hipStream_t st, void *ws = nullptr,
+                                  size_t ws_bytes = 0);
+size_t int2_gemm_ws_need(int M, int N, int K);
 ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (int2_int8.hip)
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
@@ -162,8 +164,10 @@ const char *ternocl_last_error(void) { return g_err; }
 const char *ternocl_version(void) { return "0.1.0"; }
 
 size_t ternocl_int2_gemm_ws_bytes(int M, int N, int K) {
-    (void)M; (void)N; (void)K;
-    return 0;  // no kernel of this build keeps scratch between launches
+    // the prefill GEMM's split-K partials (M > 16, shapes whose 128 x 512 tiles
+    // leave CUs idle); the GEMVs need none
+    if (M <= 16 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    return int2_gemm_ws_need(M, N, K);
 }
 
 ternocl_status ternocl_workspace_zero(void *ws, size_t ws_bytes, void *stream) {
@@ -178,7 +182,6 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
                                                const ternocl_gemv_tile *tile, void *stream) {
     ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
-    (void)ws; (void)ws_bytes;
     const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0};
     if (t.engine < 0 || t.engine > 4) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..4");
     if (t.engine == 3 || (M > 16 && t.engine == 0)) {
@@ -186,7 +189,7 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
         if ((size_t)(K / 16) * (size_t)N * 4 >= kMaxBufBytes)
             FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the prefill GEMM takes packed weights (K * N / 4 bytes) below 2^31 bytes");
         return int2_gemm_mfma_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32,
-                                  (hipStream_t)stream);
+                                  (hipStream_t)stream, ws, ws_bytes);
     }
     if (M <= 16) {
         // automatic: the fp8 x fp4 engine where it applies, else the bf16/fp16 MFMA GEMV

@@ -146,7 +146,9 @@ template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
 };
 
 // One BM x BN output tile of rows [0, mrows) of ar (mrows <= BM) and columns
-// [n0, n0 + BN) (columns >= N masked); C row r is crow0 + r.
+// [n0, n0 + BN) (columns >= N masked); C row r is crow0 + r.  The tile runs
+// over kseg rows of K (a multiple of 128): A's rows have stride K, and ar, B
+// and S start at the segment's first row (split-K: one K-slice).
 // DUAL: the MoE gate/up pair in one pass over A -- acc from (B, S) is the up
 // projection, acc2 from (B2, S2) the gate; C = DT(silu(gate) * DT(up)), the
 // two-launch sequence's result (up rounded to DT, then POSTOP 1) bit for bit.
@@ -154,15 +156,15 @@ template <class Cfg, bool BF16, bool DUAL = false, bool SHORT = false>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
                                           const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                           void *__restrict__ C, const uint16_t *__restrict__ Other,
-                                          const void *__restrict__ Bias, int crow0, int N, int K, int n0,
-                                          int postop, int out_f32, uint16_t *lds,
+                                          const void *__restrict__ Bias, int crow0, int N, int K, int kseg,
+                                          int n0, int postop, int out_f32, uint16_t *lds,
                                           const uint32_t *__restrict__ B2 = nullptr,
                                           const uint16_t *__restrict__ S2 = nullptr) {
     constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = SHORT ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int wm = (wave / Cfg::WVN) * 16 * NMB, wn = (wave % Cfg::WVN) * 16 * NCB;
-    const int stages = K / BK;
+    const int stages = kseg / BK;
 
     // All operand loads are buffer loads with per-lane offsets set up once and
     // issued unconditionally (a load under a branch is waited for at the
@@ -213,11 +215,11 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     static_assert(NMB % 2 == 0 && NCB % 2 == 0, "32 x 32 MFMA blocks");
     constexpr int MB2 = NMB / 2, CB2 = NCB / 2;
     const int c32 = lane & 31, q32 = lane >> 5;
-    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
-    const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(kseg / 16) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S + n0, (uint32_t)(((size_t)(kseg / kGS) * N - n0) * 2));
     // (DUAL: the gate weights, same shape, same offsets)
-    const __amdgpu_buffer_rsrc_t rB2 = buf_rsrc(DUAL ? B2 + n0 : B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
-    const __amdgpu_buffer_rsrc_t rS2 = buf_rsrc(DUAL ? S2 + n0 : S + n0, (uint32_t)(((size_t)(K / kGS) * N - n0) * 2));
+    const __amdgpu_buffer_rsrc_t rB2 = buf_rsrc(DUAL ? B2 + n0 : B + n0, (uint32_t)(((size_t)(kseg / 16) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rS2 = buf_rsrc(DUAL ? S2 + n0 : S + n0, (uint32_t)(((size_t)(kseg / kGS) * N - n0) * 2));
     uint32_t vb = (uint32_t)((wn + c32) * 4);
     const uint32_t vs0 = (uint32_t)((wn + c32) * 2);
     constexpr int NB = DUAL ? 2 : 1;  // weight matrices
@@ -429,19 +431,57 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     else epi_dispatch(postop, out_f32, epilogue);
 }
 
+// splits > 1 (deterministic split-K): workgroup (tile, slice s) runs K rows
+// [s K / splits, (s + 1) K / splits) and writes its fp32 partial tile into
+// part + s M N (no epilogue); k_splitk_reduce adds the slices in order.  The
+// slices of a tile are adjacent in the XCD order, so they share its A rows.
 template <class Cfg, bool BF16>
 __global__ void __launch_bounds__(Cfg::THREADS)
 k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
-            const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
+            const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32, int splits = 1,
+            float *__restrict__ part = nullptr) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
-    int tm, tn;
-    if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
-    const ARows ar{A + (size_t)tm * Cfg::BM * K, nullptr, 1};
+    int tm, tns;
+    if (!xcd_tile_ashare(blockIdx.x, mt, nt * splits, tm, tns)) return;  // whole workgroup: padding
+    const int tn = tns / splits, sl = tns - tn * splits;
+    const int kseg = K / splits, k0 = sl * kseg;
+    const ARows ar{A + (size_t)tm * Cfg::BM * K + k0, nullptr, 1};
     const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
-    gemm_tile<Cfg, BF16>(ar, (uint32_t)((size_t)mrows * K * 2), mrows, B, S, C, Other, Bias, tm * Cfg::BM,
-                              N, K, tn * Cfg::BN, postop, out_f32, lds);
+    if (splits > 1) {
+        C = part + (size_t)sl * M * N;
+        Other = nullptr;
+        Bias = nullptr;
+        postop = 0;
+        out_f32 = 1;
+    }
+    gemm_tile<Cfg, BF16>(ar, (uint32_t)(((size_t)mrows * K - k0) * 2), mrows, B + (size_t)(k0 / 16) * N,
+                         S + (size_t)(k0 / kGS) * N, C, Other, Bias, tm * Cfg::BM, N, K, kseg, tn * Cfg::BN,
+                         postop, out_f32, lds);
+}
+
+// The split-K reduction and epilogue: C[m, n..n+3] = ct(epi(sum over slices
+// s = 0, 1, ... in order of part[s][m][n..n+3])), one thread per 4 outputs.
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+k_splitk_reduce(const float *__restrict__ part, int splits, void *__restrict__ C, const uint16_t *__restrict__ Other,
+                const void *__restrict__ Bias, int M, int N, int postop, int out_f32) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)M * N;
+    if (i >= mn / 4) return;
+    float4 t = ((const float4 *)part)[i];
+    for (int s = 1; s < splits; ++s) {
+        const float4 u = ((const float4 *)(part + s * mn))[i];
+        t.x += u.x;
+        t.y += u.y;
+        t.z += u.z;
+        t.w += u.w;
+    }
+    const float v[4] = {t.x, t.y, t.z, t.w};
+    const int m = (int)(4 * i / N), n = (int)(4 * i - (size_t)m * N);
+    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+        epi_store4_c<BF16, decltype(P_)::value, decltype(F_)::value>(C, Other, Bias, N, m, n, v);
+    });
 }
 
 // Grouped GEMM of the MoE prefill (int2_moe/int2_moe_prefill.cl:72-141): the
@@ -479,7 +519,7 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
     const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : mrows) * K * 2);
     const size_t bo = (size_t)e * (K / 16) * N, so = (size_t)e * (K / kGS) * N;
     gemm_tile<Cfg, BF16, DUAL, true>(ar, a_bytes, mrows, B_all + bo, S_all + so, C_all, Other_all, nullptr, row0 + m0,
-                               N, K, tn * Cfg::BN, postop, out_f32, lds, DUAL ? B2_all + bo : nullptr,
+                               N, K, K, tn * Cfg::BN, postop, out_f32, lds, DUAL ? B2_all + bo : nullptr,
                                DUAL ? S2_all + so : nullptr);
 }
 
@@ -617,11 +657,54 @@ ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, i
     return check_launch();
 }
 
+// Split-K slices for a shape whose 128 x 512 tiles would leave CUs idle: the
+// fewest slices (2, 4 or 8) that make >= 192 work units, each slice a
+// multiple of 128 rows and at least 1024 rows of K; 1 = no split.
+int gemm_splits(int M, int N, int K) {
+    const long tiles = (long)((M + 127) / 128) * ((N + 511) / 512);
+    if (tiles >= 192) return 1;
+    for (int s = 2; s <= 8; s *= 2)
+        if (K % (128 * s) == 0 && K / s >= 1024 && tiles * s >= 192) return s;
+    return 1;
+}
+
+// Workspace of the split-K path: the fp32 partial tiles of every slice.
+size_t int2_gemm_ws_need(int M, int N, int K) {
+    const int s = gemm_splits(M, N, K);
+    return s > 1 ? (size_t)s * M * N * 4 : 0;
+}
+
+// With a workspace of int2_gemm_ws_need bytes (16-byte aligned), shapes that
+// split run the 128 x 512 tile over K-slices into it and a reduction kernel
+// adds the slices in order and applies the epilogue (deterministic: the same
+// bits on every run); without one they take the plan of gemm_plan.
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
-                                  int postop, int out_f32, hipStream_t st) {
+                                  int postop, int out_f32, hipStream_t st, void *ws, size_t ws_bytes) {
+    const int splits = gemm_splits(M, N, K);
+    const bool bf = dtype == TERNOCL_BF16;
+    if (splits > 1 && ws && ws_bytes >= int2_gemm_ws_need(M, N, K) && ((uintptr_t)ws & 15) == 0) {
+        typedef TileCfg<8, 4, 1, 8> Cfg;
+        const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
+        float *part = (float *)ws;
+        const dim3 grid(xcd_ashare_grid(mt, nt * splits));
+        if (bf)
+            hipLaunchKernelGGL((k_int2_gemm<Cfg, true>), grid, dim3(Cfg::THREADS), 0, st, (const uint16_t *)A, B,
+                               (const uint16_t *)S, C, nullptr, nullptr, M, N, K, 0, 1, splits, part);
+        else
+            hipLaunchKernelGGL((k_int2_gemm<Cfg, false>), grid, dim3(Cfg::THREADS), 0, st, (const uint16_t *)A, B,
+                               (const uint16_t *)S, C, nullptr, nullptr, M, N, K, 0, 1, splits, part);
+        const unsigned blocks = (unsigned)(((size_t)M * N / 4 + 255) / 256);
+        if (bf)
+            hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(blocks), dim3(256), 0, st, part, splits, C,
+                               (const uint16_t *)Other, Bias, M, N, postop, out_f32);
+        else
+            hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(blocks), dim3(256), 0, st, part, splits, C,
+                               (const uint16_t *)Other, Bias, M, N, postop, out_f32);
+        return check_launch();
+    }
     const GemmPlan p = gemm_plan(M, N);
-    if (dtype == TERNOCL_BF16) gemm_dispatch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (bf) gemm_dispatch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else gemm_dispatch<false>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     return check_launch();
 }

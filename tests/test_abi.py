@@ -71,6 +71,13 @@ def test_status_strings():
 def test_ws_bytes_query():
     import ternocl_amd as T
     assert T.int2_gemm_ws_bytes(1, 14336, 4096) == 0  # the GEMV keeps no scratch
+    # the prefill GEMM's split-K partials: 4 K-slices of fp32 [M, N] where the
+    # 128 x 512 tiles would leave CUs idle (8 x 8 = 64 tiles here) ...
+    assert T.int2_gemm_ws_bytes(1024, 4096, 14336) == 4 * 1024 * 4096 * 4
+    assert T.int2_gemm_ws_bytes(200, 16384, 5120) == 4 * 200 * 16384 * 4
+    # ... and none where they fill the chip, or K is too short to slice
+    assert T.int2_gemm_ws_bytes(1024, 14336, 4096) == 0
+    assert T.int2_gemm_ws_bytes(256, 1024, 1024) == 0
 
 
 @pytest.mark.parametrize("entry", ["ternocl_int2_moe_prefill", "ternocl_int2_moe_prefill_int8",

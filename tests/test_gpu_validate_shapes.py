@@ -144,3 +144,58 @@ def test_decode_workload_sweep(dev, orc, M, K, N):
     """The decode workload: bf16, bias + residual (postop 5), automatic engine."""
     bad, dmax = _upcvt_case(dev, orc, M, K, N, True, postop=5)
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+# Split-K (a workspace of ternocl_int2_gemm_ws_bytes): shapes whose 128 x 512
+# tiles would leave CUs idle, including a ragged one (last row tile 104 rows,
+# last column tile 16 columns).
+SPLITK_SHAPES = [(1024, 14336, 4096), (1024, 17408, 5120), (200, 5120, 16384), (1000, 4096, 4112)]
+
+
+def _splitk_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
+    import torch
+    import ternocl_amd as T
+    need = T.int2_gemm_ws_bytes(M, N, K)
+    assert need > 0, "this shape should split"
+    print(f"split-K M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32} ws={need}", flush=True)
+    A, B, S, other, bias_f = _inputs(seed + 60000 + M + K + N, M, K, N, bf16)
+    dA, dB, dS = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16)
+    dO, dBias, dC = _device_io(torch, S, other, bias_f, M, N, bf16, out_f32)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
+    torch.cuda.synchronize()
+    first = dC.clone()
+    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(first, dC), "split-K results differ between runs"
+    # the same call without the workspace (no split) agrees within the rule
+    _, _, dC2 = _device_io(torch, S, other, bias_f, M, N, bf16, out_f32)
+    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC2, dO, dBias, M, N, K, postop, out_f32)
+    torch.cuda.synchronize()
+    if out_f32:
+        a, b = host_f32(dC), host_f32(dC2)
+    else:
+        a, b = formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(host_u16(dC2), bf16)
+    bad_nows, _ = allclose_report(a, b)
+    rows = sample_rows(M)
+    acc = orc.int2_gold(np.ascontiguousarray(A[rows]), B, S, rows.size, K, N, bf16)
+    bad, dmax = _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
+    return bad, dmax, bad_nows
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", SPLITK_SHAPES)
+def test_splitk_parity(dev, orc, M, K, N, bf16):
+    bad, dmax, bad_nows = _splitk_case(dev, orc, M, K, N, bf16)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+    assert bad_nows == 0, f"{bad_nows} elements differ from the unsplit GEMM beyond the rule"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_splitk_epilogues(dev, orc, bf16, postop, out_f32):
+    M, K, N = SPLITK_SHAPES[-1]
+    bad, dmax, bad_nows = _splitk_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+    assert bad_nows == 0
