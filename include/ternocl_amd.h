@@ -80,7 +80,7 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint
 typedef struct {
     int engine;          /* 1: VALU GEMV (v_dot2 MACs, M <= 8); 2: bf16/fp16 MFMA GEMV (M <= 16);
                             3: MFMA prefill GEMM (any M, 128 x 128 tiles; the M > 16 engine);
-                            4: block-scaled fp8 x fp4 MFMA GEMV (M <= 4, A 16-byte aligned;
+                            4: block-scaled fp8 x fp4 MFMA GEMV (M <= 8, A 16-byte aligned;
                                the automatic choice where it applies) */
     int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
     int cols_per_lane;   /* MFMA: adjacent columns per lane, 1, 2 or 4 (16-, 32- or 64-column strips) */
@@ -90,7 +90,7 @@ typedef struct {
 } ternocl_gemv_tile;
 
 /* Same as ternocl_int2_fp16_upcvt_gemm with an explicit tile (NULL = automatic:
- * the fp8 x fp4 GEMV for M <= 4 (A 16-byte aligned), the bf16/fp16 MFMA GEMV
+ * the fp8 x fp4 GEMV for M <= 8 (A 16-byte aligned), the bf16/fp16 MFMA GEMV
  * for other M <= 16, the prefill GEMM above).  When M > 16 the engine
  * must be 0 or 3. */
 ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const uint32_t *B,
@@ -122,7 +122,7 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
  * and stores, writing C[m, n] = a checksum of column n's words.  Its duration
  * is the engine's memory ceiling, measured as the reference measures its own
  * (int2_fp16_upcvt/README.md:135-137: the GEMV with the decode removed).
- * C: fp32 [M, N]; M <= 4, N % 16 == 0, K % 128 == 0. */
+ * C: fp32 [M, N]; M <= 8, N % 16 == 0, K % 128 == 0. */
 ternocl_status ternocl_int2_gemv_stream_probe(int dtype, const uint32_t *B, const void *S, void *C, int M,
                                              int N, int K, void *stream);
 

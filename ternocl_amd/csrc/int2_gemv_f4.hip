@@ -1,6 +1,6 @@
 // int2_gemv_f4.hip -- decode GEMV for packed 2-bit ternary weights on the
 // gfx950 block-scaled fp8 x fp4 matrix cores (engine 4, the default for
-// M <= 4).  Replaces int2_fp16_upcvt_gemm
+// M <= 8).  Replaces int2_fp16_upcvt_gemm
 // (int2_fp16_upcvt/int2_fp16_upcvt.cl:193-290):
 //
 //   C[m,n] = ct(epi(sum_g S[g,n] * sum_{k in g} A[m,k] * code(B[k,n])))
@@ -66,7 +66,11 @@ typedef short s16x2_t __attribute__((ext_vector_type(2)));
 // activation row's pieces sit in one lane of the MFMA result (rows 4q..4q+3).
 __host__ __device__ constexpr int f4_pieces(bool bf16) { return bf16 ? 3 : 4; }
 constexpr int kF4RowStride = 4;
-constexpr int kF4MaxM = 16 / kF4RowStride;
+// Rows per launch: 4 per MFMA row set of 16; M 5..8 take two row sets, two
+// MFMAs per group and column on the same decoded weights (the int8 modes: 4).
+constexpr int kF4MaxM = 32 / kF4RowStride;
+constexpr int kF4MaxMI8 = 16 / kF4RowStride;
+__host__ __device__ constexpr int f4_rsets(int mr) { return mr > 4 ? 2 : 1; }
 
 // One weight word (rows 0..15 of a column) -> fp4 dwords: d0 nibble n = row 2n,
 // d1 nibble n = row 2n + 1; nibble = (b1 << 3) | (b0 << 2) of the row's code.
@@ -318,7 +322,7 @@ template <int CPL, int GPW> struct F4Slab {
 // which returns 0 without a memory access, so the loads can be issued early
 // and waited for only at the epilogue.
 template <int MR, int CPL, bool BF16> struct F4EpiIn {
-    static constexpr int OPL = 1;  // outputs per lane: row m = q
+    static constexpr int OPL = f4_rsets(MR);  // outputs per lane: rows m = q + 4h, h < OPL
     // raw bits, converted only in the epilogue (a conversion here would make
     // the compiler wait for these loads, which follow every weight load)
     uint32_t o[OPL][CPL], b[CPL];
@@ -329,13 +333,16 @@ template <int MR, int CPL, bool BF16> struct F4EpiIn {
         const uint32_t bb = ub ? (uint32_t)((size_t)N * (out_f32 ? 4 : 2)) : 0u;
         const __amdgpu_buffer_rsrc_t ro = buf_rsrc(uo ? Other : nullptr, ob);
         const __amdgpu_buffer_rsrc_t rb = buf_rsrc(ub ? Bias : nullptr, bb);
-        const int m = q < M ? q : M - 1;
         const uint32_t off = 0x7ffffff0u;
         const int bsz = out_f32 ? 4 : 2;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const uint32_t oo = mine ? (uint32_t)(((size_t)m * N + n0 + j) * 2) : off;
-            o[0][j] = __builtin_amdgcn_raw_buffer_load_b16(ro, oo, 0, 0);
+#pragma unroll
+            for (int h = 0; h < OPL; ++h) {
+                const int m = q + 4 * h < M ? q + 4 * h : M - 1;
+                const uint32_t oo = mine ? (uint32_t)(((size_t)m * N + n0 + j) * 2) : off;
+                o[h][j] = __builtin_amdgcn_raw_buffer_load_b16(ro, oo, 0, 0);
+            }
             const uint32_t bo = mine ? (uint32_t)((n0 + j) * bsz) : off;
             b[j] = out_f32 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb, bo, 0, 0)
                            : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, bo, 0, 0);
@@ -397,7 +404,8 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
     constexpr bool I8 = QM == 1 || QM == 2, NODEC = QM == 4;
     constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
-    static_assert(RR <= 16, "too many MFMA rows");
+    constexpr int RSETS = f4_rsets(MR), RR1 = RR < 16 ? RR : 16;  // MFMA row sets, rows per set
+    static_assert(RR <= 32 && (RSETS == 1 || QM == 0 || NODEC), "two row sets: the DT mode only");
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -442,7 +450,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     constexpr int WB = f4_window_bytes(RR, GPW);
     const int nbuf = windows > 1 ? 2 : 1;
     uint8_t *wlds = lds8 + (size_t)wave * nbuf * WB;
-    const int rho = c & (RR - 1);  // A row (piece row) this lane feeds; rows >= RR are don't-care
+    const int rho = c & (RR1 - 1);  // A row (piece row) this lane feeds in each row set; rows >= RR are don't-care
 
     F4Stage<MR, GPW, BF16, QM> st;
     if constexpr (!NODEC) st.load(A, M, K, groups, g0w, lane, SA, ldsa);
@@ -454,11 +462,13 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     if constexpr (!NODEC) st.store(wlds, lane);
 
     constexpr int ROWS = I8 ? 1 : P;  // accumulators per column: the pieces of row m = q, or their sum
-    float acc[CPL][ROWS];
+    float acc[RSETS][CPL][ROWS];  // row set t: rows m = q + 4t
 #pragma unroll
-    for (int j = 0; j < CPL; ++j)
+    for (int t = 0; t < RSETS; ++t)
 #pragma unroll
-        for (int i = 0; i < ROWS; ++i) acc[j][i] = 0.0f;
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < ROWS; ++i) acc[t][j][i] = 0.0f;
 
     for (int win = 0; win < windows; ++win) {
         asm volatile("" ::: "memory");  // staging writes precede the reads (in-order LDS per wave)
@@ -477,14 +487,19 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             if constexpr (NODEC) {
 #pragma unroll
                 for (int j = 0; j < CPL; ++j)
-                    acc[j][0] += (float)(cur.w[gi][0].v[j] ^ cur.w[gi][1].v[j]) * dt2f<BF16>(cur.scale(gi, j));
+                    acc[0][j][0] += (float)(cur.w[gi][0].v[j] ^ cur.w[gi][1].v[j]) * dt2f<BF16>(cur.scale(gi, j));
                 continue;
             }
-            const uint8_t *row = buf + (gi * RR + rho) * 128 + 32 * q;
-            const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
-            const int sa = buf[GPW * RR * 128 + (gi * RR + rho) * 4 + q];
-            const v8i_t av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
-                              (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            v8i_t av[RSETS];
+            int sa[RSETS];
+#pragma unroll
+            for (int t = 0; t < RSETS; ++t) {
+                const int pr = gi * RR + 16 * t + rho;
+                const uint8_t *row = buf + pr * 128 + 32 * q;
+                const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
+                sa[t] = buf[GPW * RR * 128 + pr * 4 + q];
+                av[t] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            }
             float inv = 0.0f;  // int8 modes: 1 / SA[g, m] of row m = q (clamped into the rows staged)
             if constexpr (I8)
                 inv = *(const float *)(buf + GPW * RR * 128 + (gi * RR + RS * (q < MR ? q : MR - 1) + 2) * 4);
@@ -499,15 +514,18 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                     f4_decode(cur.w[gi][1].v[j], e0, e1);
                 }
                 const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
-                const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa, 0, 127);
                 const float s = dt2f<BF16>(cur.scale(gi, j));
-                if constexpr (I8) {
-                    const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
-                    acc[j][0] += dot * (s * inv);
-                } else {
 #pragma unroll
-                    for (int i = 0; i < ROWS; ++i) acc[j][i] = d[i] * s + acc[j][i];
+                for (int t = 0; t < RSETS; ++t) {
+                    const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        av[t], bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa[t], 0, 127);
+                    if constexpr (I8) {
+                        const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
+                        acc[t][j][0] += dot * (s * inv);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < ROWS; ++i) acc[t][j][i] = d[i] * s + acc[t][j][i];
+                    }
                 }
             }
         }
@@ -520,20 +538,23 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     }
 
     // ---- pieces -> outputs (x 1/2: the fp4 operand held 2v), then waves ----
-    // lane q holds rows 4q .. 4q + P - 1: the pieces of output row m = q
-    constexpr int OPL = F4EpiIn<MR, CPL, BF16>::OPL, QV = MR;
+    // lane q holds, in row set h, rows 4q .. 4q + P - 1 of the set: the pieces
+    // of output row m = q + 4h
+    constexpr int OPL = F4EpiIn<MR, CPL, BF16>::OPL, QV = MR < 4 ? MR : 4;
     float out[CPL][OPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        if constexpr (I8) {
-            out[j][0] = acc[j][0];
-        } else {
-            float t = acc[j][0];
+    for (int j = 0; j < CPL; ++j)
 #pragma unroll
-            for (int i = 1; i < P; ++i) t += acc[j][i];
-            out[j][0] = t * 0.5f;
+        for (int h = 0; h < OPL; ++h) {
+            if constexpr (I8) {
+                out[j][h] = acc[h][j][0];
+            } else {
+                float t = acc[h][j][0];
+#pragma unroll
+                for (int i = 1; i < P; ++i) t += acc[h][j][i];
+                out[j][h] = t * 0.5f;
+            }
         }
-    }
     const bool live = q < QV;
     if constexpr (DS) {  // y_j of every slot, then wave 0's weighted sum in slot order
         float *red = (float *)(lds8 + (size_t)nbuf * W * WB);  // [W][CPL][16]
@@ -578,7 +599,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
         for (int h = 0; h < OPL; ++h) {
-            const int m = q + h;
+            const int m = q + 4 * h;
             if (m >= M) break;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
@@ -598,7 +619,7 @@ struct F4Plan {
 
 constexpr size_t kF4MaxLds = 96 * 1024;
 
-int f4_mr(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
+int f4_mr(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
 size_t f4_lds(int MR, int waves, int gpw, int cpl, int groups) {
     const int rr = kF4RowStride * MR;
@@ -646,7 +667,7 @@ template <int MR, int CPL, int GPW, bool BF16, int QMODE = 0>
 hipError_t f4_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const void *S, void *C,
                        const void *Other, const void *Bias, int M, int N, int K, int postop,
                        int out_f32, hipStream_t st) {
-    if constexpr (kF4RowStride * MR > 16) {
+    if constexpr (kF4RowStride * MR > 32) {
         return hipErrorInvalidValue;
     } else {
         const int strips = N / (16 * CPL);
@@ -692,7 +713,7 @@ hipError_t f4_launch(const F4Plan &p, const void *A, const uint32_t *B, const vo
     case 1: return f4_launch_c<1, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     case 2: return f4_launch_c<2, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     case 4: return f4_launch_c<4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    default: return f4_launch_c<4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    default: return f4_launch_c<8, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     }
 }
 
@@ -791,7 +812,7 @@ __global__ void k_int2_f4_decode(const uint32_t *__restrict__ B, uint32_t *__res
 
 }  // namespace
 
-// Whether the fp8 x fp4 engine takes a call: M <= 4, A 16-byte aligned (it
+// Whether the fp8 x fp4 engine takes a call: M <= 8, A 16-byte aligned (it
 // reads A with 16-byte loads), and byte offsets into C, Other and Bias below
 // 2^31 (its buffer loads use 32-bit offsets).
 bool int2_gemv_f4_supports(int M, int N, const void *A) {
@@ -803,7 +824,7 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
                                 int out_f32, int waves, int cpl, int gpw, hipStream_t st) {
     const bool bf16 = dtype == TERNOCL_BF16;
     if (M > kF4MaxM) {
-        set_error("the fp8 x fp4 GEMV takes M <= 4");
+        set_error("the fp8 x fp4 GEMV takes M <= 8");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
     if ((size_t)M * N * 4 >= 0x7ff00000u) {
@@ -855,7 +876,7 @@ ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const vo
                                           int K, hipStream_t st) {
     const bool bf16 = dtype == TERNOCL_BF16;
     if (M < 1 || M > kF4MaxM || (size_t)M * N * 4 >= 0x7ff00000u) {
-        set_error("the decode-removed GEMV takes M <= 4 and M * N * 4 < 2^31 bytes of output");
+        set_error("the decode-removed GEMV takes M <= 8 and M * N * 4 < 2^31 bytes of output");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
     const F4Plan p = f4_plan(bf16, M, N, K, 0, 0, 0);
@@ -873,7 +894,7 @@ ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const vo
 // the tile takes 2 columns per lane); Aq 8-byte or A 16-byte aligned; C,
 // Other and Bias byte offsets below 2^31.
 bool int2_int8_gemv_supports(int M, int N, int K, const void *A, const int8_t *Aq) {
-    if (M < 1 || M > kF4MaxM || N % 16 || (size_t)M * N * 4 >= 0x7ff00000u) return false;
+    if (M < 1 || M > kF4MaxMI8 || N % 16 || (size_t)M * N * 4 >= 0x7ff00000u) return false;
     if (Aq ? ((uintptr_t)Aq & 7) != 0 : ((uintptr_t)A & 15) != 0) return false;
     const F4Plan p = f4q_plan(M, N, K);
     return N % (16 * p.cpl) == 0 && p.lds <= kF4MaxLds;

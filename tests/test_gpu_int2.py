@@ -24,7 +24,7 @@ SHAPES = [(1, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (2, 4096, 14336),
           (16, 4096, 4096), (13, 1024, 272), (11, 640, 48)]
 
 
-F4_MAX_M = {False: 4, True: 4}  # the fp8 x fp4 engine: 4 fp8 pieces per fp16, 3 per bf16
+F4_MAX_M = {False: 8, True: 8}  # the fp8 x fp4 engine: two 16-row MFMA row sets of 4 rows each
 
 
 @pytest.mark.parametrize("engine", [1, 2, 4])
@@ -36,7 +36,7 @@ def test_gemv_parity(dev, orc, M, K, N, bf16, engine):
     if engine == 1 and M > 8:
         pytest.skip("the VALU GEMV takes M <= 8")
     if engine == 4 and M > F4_MAX_M[bf16]:
-        pytest.skip("the fp8 x fp4 GEMV takes M <= 4")
+        pytest.skip("the fp8 x fp4 GEMV takes M <= 8")
     print(f"gemv parity M={M} K={K} N={N} bf16={bf16} engine={engine}", flush=True)
     A, B, S, other, bias_f = _inputs(1000 + M + K + N, M, K, N, bf16)
     dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 0, False, tile=T.gemv_tile(engine))
@@ -239,7 +239,7 @@ def test_gemv_stream_probe_checksum(dev, M, K, N, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 1024), (2, 1024, 272), (4, 2048, 512)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 1024), (2, 1024, 272), (4, 2048, 512), (6, 1024, 272), (8, 2048, 512)])
 def test_gemv_f4_pieces_exact(dev, orc, M, K, N, bf16):
     """The fp8 pieces sum to each activation exactly, so the fp32 result agrees
     with the fp32 host gold to accumulation-order rounding (far inside the
