@@ -445,8 +445,10 @@ k_int2_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
     int tm, tns;
     if (!xcd_tile_ashare(blockIdx.x, mt, nt * splits, tm, tns)) return;  // whole workgroup: padding
-    const int tn = tns / splits, sl = tns - tn * splits;
-    const int kseg = K / splits, k0 = sl * kseg;
+    // (uniform: kept in scalar registers, so the buffer descriptors built
+    // from them stay scalar -- a divided value otherwise reads as per-lane)
+    const int tn = __builtin_amdgcn_readfirstlane(tns / splits), sl = __builtin_amdgcn_readfirstlane(tns - tn * splits);
+    const int kseg = __builtin_amdgcn_readfirstlane(K / splits), k0 = sl * kseg;
     const ARows ar{A + (size_t)tm * Cfg::BM * K + k0, nullptr, 1};
     const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
     if (splits > 1) {
