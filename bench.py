@@ -88,13 +88,16 @@ class ShapeBench:
         self.dB = [B0.clone() for _ in range(self.sets)]
         self.dS = [S0.clone() for _ in range(self.sets)]
         self.dC = torch.empty((M, N), dtype=dt, device=dev)
+        wsb = T.int2_gemm_ws_bytes(M, N, K)  # the K split's slice sums and strip counters
+        self.ws = torch.zeros(wsb, dtype=torch.uint8, device=dev) if wsb else None
         self.next = 0
 
     def launch(self):
         s = self.next % self.sets
         self.next += 1
         self.T.int2_fp16_upcvt_gemm(self.dA, self.dB[s], self.dS[s], self.dC, self.dO, self.dBias,
-                                    self.M, self.N, self.K, POSTOP_BIAS_RESIDUAL, False, tile=self.tile)
+                                    self.M, self.N, self.K, POSTOP_BIAS_RESIDUAL, False, ws=self.ws,
+                                    tile=self.tile)
 
     def bytes(self):
         return gemv_bytes(self.M, self.K, self.N)

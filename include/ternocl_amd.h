@@ -68,7 +68,14 @@ const char *ternocl_version(void);
  * (M = 1024, K = 14336, N = 4096: 4 K-slices): fp32 partial tiles per slice,
  * then a reduction that adds the slices in order and applies the epilogue,
  * the same bits on every run.  Without the scratch (NULL or short) those
- * shapes run on 128 x 128 tiles instead.  The GEMVs need none. */
+ * shapes run on 128 x 128 tiles instead.  The fp8 x fp4 GEMV splits K over
+ * several workgroups per column strip where one workgroup per strip would
+ * leave CUs idle or stage too much of A (K = 14336, N = 4096; M >= 3):
+ * fp32 slice sums [slices][M][N] and a counter per 16-column strip, the
+ * last workgroup of a strip adding the slices in order.  Its counters must
+ * read zero before the first call on a scratch (ternocl_workspace_zero once);
+ * every call leaves them zero.  Without the scratch the GEMV runs unsplit.
+ * Calls that share one scratch must not overlap. */
 size_t ternocl_int2_gemm_ws_bytes(int M, int N, int K);
 ternocl_status ternocl_int2_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
                                             const void *S, void *C, const void *Other,
@@ -87,6 +94,8 @@ typedef struct {
     int groups_per_wave; /* MFMA: 128-row groups per wave per LDS window, 1..16 (power of
                             two, times M rounded up to a power of two <= 16) */
     int col_lanes;       /* VALU: lanes across a strip of 4*col_lanes columns, 4, 8 or 16 */
+    int k_slices;        /* fp8 x fp4 GEMV: workgroups per column strip, each over a slice of K,
+                            1..16 (at most one per 128-row group; > 1 needs the ws above) */
 } ternocl_gemv_tile;
 
 /* Same as ternocl_int2_fp16_upcvt_gemm with an explicit tile (NULL = automatic:

@@ -115,9 +115,9 @@ VALU, MFMA, GEMM, F4 = 1, 2, 3, 4  # engines: VALU GEMV, MFMA GEMV, MFMA prefill
 
 
 def gemv_tile(engine: int = 0, waves: int = 0, cols_per_lane: int = 0, groups_per_wave: int = 0,
-              col_lanes: int = 0) -> "GemvTile":
+              col_lanes: int = 0, k_slices: int = 0) -> "GemvTile":
     """A decode-GEMV tile (0 = automatic for every field)."""
-    return GemvTile(engine, waves, cols_per_lane, groups_per_wave, col_lanes)
+    return GemvTile(engine, waves, cols_per_lane, groups_per_wave, col_lanes, k_slices)
 
 
 def int2_fp16_upcvt_gemm(A, B, S, C, Other, Bias, M: int, N: int, K: int, postop: int = 0,

@@ -13,7 +13,7 @@ P = C.c_void_p
 class GemvTile(C.Structure):
     """ternocl_gemv_tile (include/ternocl_amd.h)."""
     _fields_ = [("engine", C.c_int), ("waves", C.c_int), ("cols_per_lane", C.c_int),
-                ("groups_per_wave", C.c_int), ("col_lanes", C.c_int)]
+                ("groups_per_wave", C.c_int), ("col_lanes", C.c_int), ("k_slices", C.c_int)]
 
 I = C.c_int
 Z = C.c_size_t

@@ -47,7 +47,9 @@ ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, co
                                   hipStream_t st);
 ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                 const void *Other, const void *Bias, int M, int N, int K, int postop,
-                                int out_f32, int waves, int cpl, int gpw, hipStream_t st);
+                                int out_f32, int waves, int cpl, int gpw, int ks, void *ws, size_t ws_bytes,
+                                hipStream_t st);
+size_t int2_gemv_f4_ws_need(int M, int N, int K);
 ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const void *S, void *C, int M, int N,
                                           int K, hipStream_t st);
@@ -164,9 +166,10 @@ const char *ternocl_last_error(void) { return g_err; }
 const char *ternocl_version(void) { return "0.1.0"; }
 
 size_t ternocl_int2_gemm_ws_bytes(int M, int N, int K) {
-    // the prefill GEMM's split-K partials (M > 16, shapes whose 128 x 512 tiles
-    // leave CUs idle); the GEMVs need none
-    if (M <= 16 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    if (M < 1 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    // the fp8 x fp4 GEMV's K split: slice sums and a counter per strip
+    if (M <= 16) return int2_gemv_f4_ws_need(M, N, K);
+    // the prefill GEMM's split-K partials (shapes whose 128 x 512 tiles leave CUs idle)
     return int2_gemm_ws_need(M, N, K);
 }
 
@@ -182,9 +185,11 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
                                                const ternocl_gemv_tile *tile, void *stream) {
     ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
-    const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0};
+    const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0, 0};
     if (t.engine < 0 || t.engine > 4) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..4");
+    if (t.k_slices < 0 || t.k_slices > 16) FAIL(TERNOCL_ERR_INVALID_ARG, "k_slices must be 0..16");
     if (t.engine == 3 || (M > 16 && t.engine == 0)) {
+        if (t.k_slices > 1) FAIL(TERNOCL_ERR_INVALID_ARG, "k_slices > 1: the fp8 x fp4 GEMV (engine 4) only");
         // the GEMM addresses the packed weights with 32-bit buffer offsets
         if ((size_t)(K / 16) * (size_t)N * 4 >= kMaxBufBytes)
             FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the prefill GEMM takes packed weights (K * N / 4 bytes) below 2^31 bytes");
@@ -195,7 +200,9 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
         // automatic: the fp8 x fp4 engine where it applies, else the bf16/fp16 MFMA GEMV
         if (t.engine == 4 || (t.engine == 0 && int2_gemv_f4_supports(M, N, A)))
             return int2_gemv_f4_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,
-                                    t.cols_per_lane, t.groups_per_wave, (hipStream_t)stream);
+                                    t.cols_per_lane, t.groups_per_wave, t.k_slices, ws, ws_bytes,
+                                    (hipStream_t)stream);
+        if (t.k_slices > 1) FAIL(TERNOCL_ERR_INVALID_ARG, "k_slices > 1: the fp8 x fp4 GEMV (engine 4) only");
         if (t.engine == 1) {
             if (M > 8) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the VALU GEMV takes M <= 8");
             return int2_gemv_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,

@@ -50,6 +50,13 @@
 // window; each wave stages its own groups' pieces (no workgroup barrier
 // before its MACs); wave partials are reduced through LDS in wave order
 // (deterministic bit for bit).
+//
+// K slices (with the caller's workspace): KS workgroups share a strip, each
+// over a contiguous 1/KS of the groups, so each stages only its slice of the
+// activations -- the per-workgroup cost that grows with M * K.  Each writes
+// its fp32 sums to the workspace; the workgroup that finishes last (a counter
+// per strip) adds the KS slices in slice order and applies the epilogue, so
+// the result does not depend on the order the workgroups run in.
 #include "common.hpp"
 
 #include <climits>
@@ -395,13 +402,17 @@ struct F4Group {
 // [ldsa] the activation scales, A int8 (QM 1) or DT quantized while staged (QM
 // 2); per group and column acc += float(dot) * (SB * (1 / SA)), the int32 dot
 // exact (piece rows 4m, 4m + 1 sum to 2 dot).
+// ksn > 1 (the plain DT GEMV, grid.y = ksn): K slice blockIdx.y; part fp32
+// [ksn][M][N] slice sums, cnt one zero-initialised counter per strip (left at
+// zero again).
 template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0, bool DS = false>
 __global__ void __launch_bounds__(64 * f4_max_waves(MR, CPL))
 k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ S, void *__restrict__ C,
                const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N,
                int K, int postop, int out_f32, int swz, F4Group grp = F4Group{},
-               const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
+               const uint16_t *__restrict__ SA = nullptr, int ldsa = 0, int ksn = 1, float *part = nullptr,
+               uint32_t *cnt = nullptr) {
     constexpr bool I8 = QM == 1 || QM == 2, NODEC = QM == 4;
     constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
     constexpr int RSETS = f4_rsets(MR), RR1 = RR < 16 ? RR : 16;  // MFMA row sets, rows per set
@@ -410,7 +421,18 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int W = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
-    const int groups = K / kGS;
+    int groups = K / kGS;
+    int ks = 0;
+    if constexpr (QM == 0 && !GRP && !DS) {
+        if (ksn > 1) {  // slice ks: groups [ks gps, ks gps + gps) (the host keeps every slice non-empty)
+            ks = blockIdx.y;
+            const int gps = (groups + ksn - 1) / ksn, g_lo = ks * gps;
+            groups = min(gps, groups - g_lo);
+            A += (size_t)g_lo * kGS;
+            B += (size_t)g_lo * 8 * N;
+            S += (size_t)g_lo * N;
+        }
+    }
     const int gw = DS ? GPW : W * GPW;   // groups per window (DS: each wave covers all of K)
     const int g0w = DS ? 0 : wave * GPW;  // this wave's first group of a window
     const int windows = (groups + gw - 1) / gw;
@@ -594,6 +616,58 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 for (int h = 0; h < OPL; ++h) out[j][h] += red[((w2 - 1) * CPL + j) * JS + (q * 16 + c) * OPL + h];
     }
     if (!live) return;
+    if constexpr (QM == 0 && !GRP && !DS) {
+        if (ksn > 1) {
+            // This slice's sums, then the strip's counter; the last of the ksn
+            // workgroups adds the slices in order.  The sums are stored and
+            // loaded with device-scope accesses (coherent across the XCDs' L2
+            // caches by themselves, no cache write-back or invalidate, which
+            // a device-scope fence would do in every workgroup); the wait for
+            // the stores to complete orders them before the counter, and the
+            // last workgroup's loads follow the counter's result.
+#pragma unroll
+            for (int h = 0; h < OPL; ++h) {
+                const int m = q + 4 * h;
+                if (m < M)
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j)
+                        __hip_atomic_store(part + ((size_t)ks * M + m) * N + n0 + j, out[j][h], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_waitcnt(0);
+            uint32_t prev = 0;
+            if (lane == 0)  // wraps to 0 at the last arrival
+                prev = __builtin_amdgcn_atomic_inc32(cnt + strip, (uint32_t)(ksn - 1), __ATOMIC_RELAXED, "agent");
+            prev = __builtin_amdgcn_readfirstlane(prev);
+            if (prev != (uint32_t)(ksn - 1)) return;
+            // four slices' loads in flight at a time (rows and slices past the
+            // end clamped, loaded and not added), then added in slice order
+            for (int s0 = 0; s0 < ksn; s0 += 4) {
+                float v[4][OPL][CPL];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int s2 = s0 + u < ksn ? s0 + u : ksn - 1;
+#pragma unroll
+                    for (int h = 0; h < OPL; ++h) {
+                        const int m = q + 4 * h < M ? q + 4 * h : M - 1;
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j)
+                            v[u][h][j] = __hip_atomic_load(part + ((size_t)s2 * M + m) * N + n0 + j,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (s0 + u >= ksn) break;
+#pragma unroll
+                    for (int h = 0; h < OPL; ++h)
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j) out[j][h] = s0 + u == 0 ? v[u][h][j] : out[j][h] + v[u][h][j];
+                }
+            }
+        }
+    }
     epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
         constexpr int PO = decltype(P_)::value;
         constexpr bool F32 = decltype(F_)::value;
@@ -615,6 +689,9 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 struct F4Plan {
     int cpl, waves, gpw, mr;
     size_t lds;
+    int ks = 1;                // K slices (workgroups per strip)
+    float *part = nullptr;     // ks > 1: slice sums fp32 [ks][M][N] ...
+    uint32_t *cnt = nullptr;   // ... and a counter per strip (workspace)
 };
 
 constexpr size_t kF4MaxLds = 96 * 1024;
@@ -629,12 +706,13 @@ size_t f4_lds(int MR, int waves, int gpw, int cpl, int groups) {
 }
 
 // Automatic tile: 2 columns per lane (32-column strips) when that still gives
-// >= 384 workgroups, else 1; then waves x groups-per-wave (<= 4) covering K
-// with the fewest idle group slots, then the fewest windows.
-F4Plan f4_plan(bool bf16, int M, int N, int K, int waves, int cpl, int gpw) {
-    const int MR = f4_mr(M), groups = K / kGS;
+// >= 384 workgroups, else 1; then waves x groups-per-wave (<= 4) covering a
+// K slice (ks slices) with the fewest idle group slots, then the fewest windows.
+F4Plan f4_plan(bool bf16, int M, int N, int K, int waves, int cpl, int gpw, int ks = 1) {
+    const int MR = f4_mr(M), groups = (K / kGS + ks - 1) / ks;
     F4Plan p;
     p.mr = MR;
+    p.ks = ks;
     p.cpl = cpl > 0 ? cpl : ((N % 32 == 0 && N / 32 >= 384) ? 2 : 1);
     int bw = 8, bg = 1;
     long best = LONG_MIN;
@@ -672,9 +750,9 @@ hipError_t f4_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const 
     } else {
         const int strips = N / (16 * CPL);
         const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
-        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QMODE>), dim3(strips), dim3(64 * p.waves), p.lds,
-                           st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other,
-                           Bias, M, N, K, postop, out_f32, swz);
+        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QMODE>), dim3(strips, p.ks), dim3(64 * p.waves),
+                           p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other,
+                           Bias, M, N, K, postop, out_f32, swz, F4Group{}, nullptr, 0, p.ks, p.part, p.cnt);
         return hipGetLastError();
     }
 }
@@ -686,7 +764,9 @@ hipError_t f4_launch_g(const F4Plan &p, const void *A, const uint32_t *B, const 
     switch (p.gpw) {
     case 1: return f4_launch_t<MR, CPL, 1, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     case 2: return f4_launch_t<MR, CPL, 2, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    case 4: return f4_launch_t<MR, CPL, 4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    case 4:  // (groups per wave x rows <= 16: the host checks)
+        if constexpr (MR <= 4) return f4_launch_t<MR, CPL, 4, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        return hipErrorInvalidValue;
     case 8:
         if constexpr (MR <= 2 && CPL <= 2) return f4_launch_t<MR, CPL, 8, BF16, QMODE>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         return hipErrorInvalidValue;
@@ -819,9 +899,49 @@ bool int2_gemv_f4_supports(int M, int N, const void *A) {
     return M >= 1 && M <= kF4MaxM && ((uintptr_t)A & 15) == 0 && (size_t)M * N * 4 < 0x7ff00000u;
 }
 
+// Workspace of a K split: one counter per 16-column strip (a 256-byte
+// block), then the slice sums fp32 [ks][M][N].
+size_t f4_cnt_bytes(int N) { return ((size_t)(N / 16) * 4 + 255) & ~(size_t)255; }
+size_t f4_split_ws(int M, int N, int ks) { return ks > 1 ? f4_cnt_bytes(N) + (size_t)ks * M * N * 4 : 0; }
+
+// Slices that leave none empty: ceil(G / ceil(G / ks)).
+int f4_slices(int groups, int ks) {
+    const int gps = (groups + ks - 1) / ks;
+    return (groups + gps - 1) / gps;
+}
+
+// Automatic K split (when the caller gives the workspace), from graph-timed
+// sweeps of M = 1..8 on K x N = 4096 x 14336, 14336 x 4096 and 4096 x 4096:
+// a split pays only where the unsplit plan has fewer than 384 strips (one
+// workgroup each) and K is long (>= 64 groups), or M is 5..8 (its staging
+// grows with M); about 28 groups per slice, 16-column-wide MFMA operands
+// shared by 4 columns per lane at M >= 5 (2 below).  K = 14336, N = 4096:
+// M = 1 7.9 -> 7.3 us, M = 8 23.2 -> 12.2 us; K = N = 4096, M = 8: 8.6 -> 7.1.
+void f4_auto_split(int M, int N, int K, int cpl_req, int &cpl, int &ks) {
+    const int groups = K / kGS, MR = f4_mr(M);
+    const int cpl_u = cpl_req > 0 ? cpl_req : ((N % 32 == 0 && N / 32 >= 384) ? 2 : 1);
+    cpl = cpl_u;
+    ks = 1;
+    if (N / (16 * cpl_u) >= 384 || groups < 16 || (MR < 8 && groups < 64)) return;
+    const int c = cpl_req > 0 ? cpl_req : (MR >= 8 && groups >= 64 && N % 64 == 0 ? 4 : (N % 32 == 0 ? 2 : 1));
+    int k = 2;  // the power of two nearest groups / 28 (log scale), 2 .. 16
+    while (k < 16 && (double)groups / 28.0 > k * 1.4142) k *= 2;
+    cpl = c;
+    ks = f4_slices(groups, k);
+}
+
+// Workspace bytes of the automatic plan (0: no K split).
+size_t int2_gemv_f4_ws_need(int M, int N, int K) {
+    if (M < 1 || M > kF4MaxM || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    int cpl, ks;
+    f4_auto_split(M, N, K, 0, cpl, ks);
+    return f4_split_ws(M, N, ks);
+}
+
 ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                 const void *Other, const void *Bias, int M, int N, int K, int postop,
-                                int out_f32, int waves, int cpl, int gpw, hipStream_t st) {
+                                int out_f32, int waves, int cpl, int gpw, int ks, void *ws, size_t ws_bytes,
+                                hipStream_t st) {
     const bool bf16 = dtype == TERNOCL_BF16;
     if (M > kF4MaxM) {
         set_error("the fp8 x fp4 GEMV takes M <= 8");
@@ -852,7 +972,28 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
         set_error("the fp8 x fp4 GEMV reads A with 16-byte loads: A must be 16-byte aligned");
         return TERNOCL_ERR_INVALID_ARG;
     }
-    const F4Plan p = f4_plan(bf16, M, N, K, waves, cpl, gpw);
+    if (ks < 0 || ks > 16) {
+        set_error("k_slices must be 0 (automatic) .. 16");
+        return TERNOCL_ERR_INVALID_ARG;
+    }
+    const bool ws_ok = ws && ((uintptr_t)ws & 15) == 0;
+    int pc = cpl, pk = ks > 0 ? f4_slices(K / kGS, ks) : 1;
+    if (ks == 0) {  // automatic: split where the workspace holds it, else one slice
+        f4_auto_split(M, N, K, cpl, pc, pk);
+        if (pk > 1 && !(ws_ok && ws_bytes >= f4_split_ws(M, N, pk))) {
+            pk = 1;
+            pc = cpl;
+        }
+    } else if (pk > 1 && !(ws_ok && ws_bytes >= f4_split_ws(M, N, pk))) {
+        set_error("k_slices > 1 needs a 16-byte aligned workspace of ternocl_int2_gemm_ws_bytes() bytes "
+                  "for that split");
+        return TERNOCL_ERR_WORKSPACE;
+    }
+    F4Plan p = f4_plan(bf16, M, N, K, waves, pc, gpw, pk);
+    if (pk > 1) {
+        p.cnt = (uint32_t *)ws;
+        p.part = (float *)((uint8_t *)ws + f4_cnt_bytes(N));
+    }
     if (p.waves > f4_max_waves(p.mr, p.cpl)) {
         set_error("more than 8 waves per workgroup only for M = 1 with 16-column strips (cols_per_lane 1)");
         return TERNOCL_ERR_INVALID_ARG;

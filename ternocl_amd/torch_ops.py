@@ -95,7 +95,9 @@ def int2_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, other: Optional
     M, K = A.shape
     N = B.shape[1]
     C = torch.empty((M, N), dtype=_out_dtype(A, out_f32), device=A.device)
-    T.int2_fp16_upcvt_gemm(A, B, S, C, other, bias, M, N, K, postop, out_f32)
+    wsb = T.int2_gemm_ws_bytes(M, N, K)  # K-split sums / counters (zeroed: the counters start at 0)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=A.device) if wsb else None
+    T.int2_fp16_upcvt_gemm(A, B, S, C, other, bias, M, N, K, postop, out_f32, ws=ws)
     return C
 
 

@@ -70,7 +70,15 @@ def test_status_strings():
 
 def test_ws_bytes_query():
     import ternocl_amd as T
-    assert T.int2_gemm_ws_bytes(1, 14336, 4096) == 0  # the GEMV keeps no scratch
+    # the fp8 x fp4 GEMV's K split: 256-byte block of strip counters + slices of fp32 [M, N]
+    assert T.int2_gemm_ws_bytes(1, 14336, 4096) == 0  # 448 32-column strips fill the chip unsplit
+    assert T.int2_gemm_ws_bytes(1, 4096, 14336) == 1024 + 4 * 1 * 4096 * 4  # 128 strips x 4 slices
+    assert T.int2_gemm_ws_bytes(8, 4096, 14336) == 1024 + 4 * 8 * 4096 * 4  # 64 strips x 4 slices
+    assert T.int2_gemm_ws_bytes(8, 4096, 4096) == 1024 + 2 * 8 * 4096 * 4  # 128 strips x 2 slices
+    assert T.int2_gemm_ws_bytes(4, 4096, 4096) == 0  # 32 groups: unsplit below M = 5
+    assert T.int2_gemm_ws_bytes(5, 14336, 4096) == 0  # 448 strips
+    assert T.int2_gemm_ws_bytes(8, 4096, 512) == 0  # 4 groups: too short to slice
+    assert T.int2_gemm_ws_bytes(9, 4096, 14336) == 0  # the bf16/fp16 MFMA GEMV keeps no scratch
     # the prefill GEMM's split-K partials: 4 K-slices of fp32 [M, N] where the
     # 128 x 512 tiles would leave CUs idle (8 x 8 = 64 tiles here) ...
     assert T.int2_gemm_ws_bytes(1024, 4096, 14336) == 4 * 1024 * 4096 * 4

@@ -238,6 +238,63 @@ def test_gemv_stream_probe_checksum(dev, M, K, N, bf16):
         np.testing.assert_allclose(C[m].cpu().numpy(), want, rtol=1e-5)
 
 
+KSPLIT = [(8, 14336, 4096, 8, 4), (5, 4096, 14336, 2, 4), (1, 14336, 4096, 4, 2), (3, 5120, 272, 3, 1),
+          (7, 384, 2064, 4, 1), (2, 256, 48, 4, 1), (4, 40960, 64, 16, 4), (8, 1024, 1024, 5, 2)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ks,cpl", KSPLIT)
+def test_gemv_f4_k_slices(dev, orc, M, K, N, ks, cpl, bf16):
+    """K split over ks workgroups per strip (slices of at most one per group;
+    K = 256 with ks = 4 runs 2): the gold within 1e-3 + 1e-2 |ref| with and
+    without the epilogue operands, bit-identical over repeated calls (the last
+    workgroup adds the slices in order), the strip counters back at zero."""
+    import torch
+    import ternocl_amd as T
+    print(f"gemv f4 k-slices M={M} K={K} N={N} ks={ks} cpl={cpl} bf16={bf16}", flush=True)
+    A, B, S, other, bias_f = _inputs(55 + M + ks, M, K, N, bf16)
+    tile = T.gemv_tile(T.F4, 0, cpl, 0, 0, ks)
+    dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16), dev_dt(other, bf16)
+    dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+    cnt_bytes = ((N // 16) * 4 + 255) // 256 * 256
+    ws = torch.zeros(cnt_bytes + ks * M * N * 4, dtype=torch.uint8, device="cuda")
+    for postop in (0, 5):
+        outs = []
+        for _ in range(3):
+            dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+            T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, False, ws=ws, tile=tile)
+            torch.cuda.synchronize()
+            outs.append(host_u16(dC))
+        assert all(np.array_equal(outs[0], o) for o in outs[1:]), "non-deterministic"
+        assert not ws[:cnt_bytes].any().item(), "strip counters not left at zero"
+        want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, False)
+        bad, dmax = allclose_report(formats.dt_to_f32(outs[0], bf16), formats.dt_to_f32(want, bf16))
+        assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
+
+
+def test_gemv_f4_k_slices_need_the_workspace(dev):
+    """An explicit split without a large enough workspace is an error; the
+    automatic plan without one runs unsplit."""
+    import torch
+    import ternocl_amd as T
+    M, K, N = 8, 14336, 4096
+    need = T.int2_gemm_ws_bytes(M, N, K)
+    assert need == 1024 + 4 * M * N * 4  # 4 slices of fp32 [M, N] after the 64 strip counters
+    dA = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
+    dB = torch.zeros((K // 16, N), dtype=torch.int32, device="cuda")
+    dS = torch.zeros((K // 128, N), dtype=torch.bfloat16, device="cuda")
+    dC = torch.ones((M, N), dtype=torch.bfloat16, device="cuda")
+    short = torch.zeros(need - 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, None, None, M, N, K, ws=short, tile=T.gemv_tile(T.F4, 0, 4, 0, 0, 8))
+    assert e.value.status == 3
+    with pytest.raises(T.TernoclError):  # k_slices on another engine
+        T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, None, None, M, N, K, tile=T.gemv_tile(T.MFMA, 0, 0, 0, 0, 2))
+    T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, None, None, M, N, K, ws=short)
+    torch.cuda.synchronize()
+    assert not dC.any().item()
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 1024), (2, 1024, 272), (4, 2048, 512), (6, 1024, 272), (8, 2048, 512)])
 def test_gemv_f4_pieces_exact(dev, orc, M, K, N, bf16):
