@@ -266,15 +266,27 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // A fragments of k-step ks of the stage in LDS buffer buf: row wm + 32 mb + c32,
     // elements 8 q32 .. 8 q32 + 7 of the stage's 16-element chunk ks (stored as
     // pairs (j, j + 8))
-    auto a_frags = [&](const uint16_t *buf, int ks, uint32_t af[MB2][4]) __attribute__((always_inline)) {
+    // (the first lmb 32-row blocks: SHORT tiles read only the blocks that hold rows)
+    auto a_frags = [&](const uint16_t *buf, int ks, uint32_t af[MB2][4], auto LMB_) __attribute__((always_inline)) {
 #pragma unroll
-        for (int mb = 0; mb < MB2; ++mb) {
+        for (int mb = 0; mb < decltype(LMB_)::value; ++mb) {
             const uint4 v = *(const uint4 *)(buf + (size_t)(wm + 32 * mb + c32) * A_PITCH + 16 * ks + 8 * q32);
             af[mb][0] = v.x; af[mb][1] = v.y; af[mb][2] = v.z; af[mb][3] = v.w;
         }
     };
     uint32_t af0[MB2][4];  // k-step 0 fragments of the coming stage, read a stage early
-    a_frags(lds, 0, af0);
+    // SHORT (tiles that may end early, as an expert's last tile): the 32-row
+    // blocks of this wave that hold tile rows.  Its MFMAs and A fragment reads
+    // stop there (none: the wave still stages A and meets the barriers); the
+    // loop is compiled per count, so no branch sits inside it.  (uniform)
+    const int lmb = SHORT ? max(0, min(MB2, (mrows - wm + 31) / 32)) : MB2;
+    constexpr bool kDeadWaves = SHORT && Cfg::WVM > 1;  // a wave's rows can all lie past the tile's end
+    if (kDeadWaves && lmb == 0) {
+    } else if (lmb == 1 && MB2 > 1) {
+        a_frags(lds, 0, af0, std::integral_constant<int, 1>{});
+    } else {
+        a_frags(lds, 0, af0, std::integral_constant<int, MB2>{});
+    }
     // Stage st reads LDS buffer st % 3.  B words and scales are loaded one
     // stage ahead, A two stages ahead (register set st & 1).  Between k-steps 1
     // and 2 a wave stores stage st + 1's A into buffer (st + 1) % 3, reads its
@@ -286,12 +298,9 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // K is a multiple of 128: the stage count is even and the loop runs in
     // pairs with the register set fixed at compile time.
     constexpr uint32_t kBuf = (uint32_t)Cfg::BM * A_PITCH;  // DT elements per buffer
-    // SHORT (tiles that may end early, as an expert's last tile): a wave whose
-    // rows all lie past the tile's last row skips its MFMAs; it still stages A
-    // and meets the barriers.
-    const bool rows_live = !SHORT || wm < mrows;
     uint32_t cur = 0;  // st % 3
-    auto stage = [&](int st, int par) __attribute__((always_inline)) {
+    auto stage = [&](int st, int par, auto LMB_) __attribute__((always_inline)) {
+        constexpr int LMB = decltype(LMB_)::value;  // live 32-row blocks (MB2: all)
         const uint16_t *abuf = lds + cur * kBuf;
         const uint32_t nxt = cur == 2 ? 0 : cur + 1;
         uint32_t bwc[NB][CB2][4];
@@ -321,41 +330,49 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         for (int ks = 0; ks < 4; ++ks) {
             if (ks == 0) {
 #pragma unroll
-                for (int mb = 0; mb < MB2; ++mb)
+                for (int mb = 0; mb < LMB; ++mb)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) af[mb][i] = af0[mb][i];
             } else if (ks == 2) {
                 __builtin_amdgcn_sched_barrier(0);
                 a_store(lds + nxt * kBuf, par ^ 1);  // past the last stage: never read
-                a_frags(abuf, 2, af);
+                a_frags(abuf, 2, af, LMB_);
                 __syncthreads();
                 // the next stage's k-step 0 fragments (its buffer is complete
                 // now): its first MFMAs wait for no LDS read
-                a_frags(lds + nxt * kBuf, 0, af0);
+                a_frags(lds + nxt * kBuf, 0, af0, LMB_);
                 __builtin_amdgcn_sched_barrier(0);
             } else {
-                a_frags(abuf, ks, af);
+                a_frags(abuf, ks, af, LMB_);
             }
-            if (!rows_live) continue;  // uniform: this wave's rows are all past the tile's last row
 #pragma unroll
             for (int cb = 0; cb < CB2; ++cb) {
                 uint32_t bf[4];
                 frag(bwc[0][cb][ks], q32, sop[0][cb], bf);
 #pragma unroll
-                for (int mb = 0; mb < MB2; ++mb) acc[mb][cb] = mfma32<BF16>(af[mb], bf, acc[mb][cb]);
+                for (int mb = 0; mb < LMB; ++mb) acc[mb][cb] = mfma32<BF16>(af[mb], bf, acc[mb][cb]);
                 if constexpr (DUAL) {
                     uint32_t bg[4];
                     frag(bwc[NB - 1][cb][ks], q32, sop[NB - 1][cb], bg);
 #pragma unroll
-                    for (int mb = 0; mb < MB2; ++mb) acc2[mb][cb] = mfma32<BF16>(af[mb], bg, acc2[mb][cb]);
+                    for (int mb = 0; mb < LMB; ++mb) acc2[mb][cb] = mfma32<BF16>(af[mb], bg, acc2[mb][cb]);
                 }
             }
         }
         cur = nxt;
     };
-    for (int st = 0; st < stages; st += 2) {
-        stage(st, 0);
-        stage(st + 1, 1);
+    auto run = [&](auto LMB_) __attribute__((always_inline)) {
+        for (int st = 0; st < stages; st += 2) {
+            stage(st, 0, LMB_);
+            stage(st + 1, 1, LMB_);
+        }
+    };
+    if constexpr (SHORT) {
+        if (kDeadWaves && lmb == 0) run(std::integral_constant<int, 0>{});
+        else if (MB2 > 1 && lmb == 1) run(std::integral_constant<int, 1>{});
+        else run(std::integral_constant<int, MB2>{});
+    } else {
+        run(std::integral_constant<int, MB2>{});
     }
 
     // Epilogue through LDS, one 32-column block and 16-row half of each 32-row
