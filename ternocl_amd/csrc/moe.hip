@@ -15,11 +15,10 @@
 //
 // The route is a stable counting sort (rows of an expert in assignment order),
 // so every run produces the same permutation: the reference's atomic-order
-// permutation is not reproducible.  One workgroup: a histogram (LDS atomics,
-// order-free), the offsets, then blocks of 16384 assignments in order, each
-// wave holding a contiguous segment of the block in registers and ranking its
-// lanes among equal expert ids with log2(E) ballots; the waves' per-expert
-// counts are prefix-summed in wave order, and every assignment gets its slot.
+// permutation is not reproducible.  A workgroup per 1024 assignments, each
+// counting all ids (the histogram) and those before its chunk, ranking lanes
+// among equal expert ids with log2(E) ballots, and placing its chunk: no
+// communication between workgroups.
 // Assignments whose expert id is outside [0, E) are dropped: no row,
 // inv = -1, no contribution to the combine.  The gather is not a separate pass
 // in the layer: the grouped GEMM reads row perm[p] / topk of X directly.
@@ -40,105 +39,68 @@ ternocl_status moe_gate_up_run(int dtype, const int *meta, const void *A_all, co
 namespace {
 
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
-constexpr int kRouteChunks = 16;                                 // 64-id chunks per wave and block
-constexpr int kRouteBlock = kRouteWaves * kRouteChunks * 64;     // ids per block (16384)
+constexpr int kRoutePieces = 1;                                // 64-id pieces per wave of a chunk
+constexpr int kRouteChunk = kRouteWaves * kRoutePieces * 64;   // ids placed per workgroup (1024)
 
-// Stable counting sort in one workgroup, in blocks of kRouteBlock ids: wave w
-// owns the contiguous segment [w, w + 1) * kRouteChunks * 64 of a block and
-// holds its ids in registers.  Pass 1 ranks every block into per-wave counts
-// (wave-private LDS rows, no atomics), whose sums give the histogram and the
-// offsets.  Pass 2 prefix-sums the per-wave counts in wave order on top of each
-// expert's running base (blocks in order, waves in order, chunks in order,
-// lanes in order: the stable order) and places every id.  Global loads happen
-// at the start of a block and stores at its end: no memory latency inside the
-// loops.
+// Lanes of a wave holding the same valid expert id as this lane (log2(E)
+// ballots); invalid lanes get an empty set.
+__device__ __forceinline__ unsigned long long route_group(bool valid, int e, int E) {
+    unsigned long long same = __ballot(valid);
+    for (int bit = 0; (1 << bit) < E; ++bit) {
+        const bool on = (e >> bit) & 1;
+        const unsigned long long bal = __ballot(valid && on);
+        same &= on ? bal : ~bal;
+    }
+    return valid ? same : 0ull;
+}
+
+// Stable counting sort over ceil(G / kRouteChunk) workgroups, no
+// communication between them: workgroup b places the ids of its chunk
+// [b C, (b + 1) C).  It counts all ids (the histogram, hence each expert's
+// first row) and those before its chunk (the expert's rows that precede the
+// chunk) with LDS atomics (integer counts: order-free); then it ranks its
+// chunk in order (waves in order, pieces in order, lanes in order, lanes of
+// one expert found with log2(E) ballots) and writes perm and inv.  Workgroup
+// 0 writes meta.  Ids outside [0, E) are dropped (inv = -1), and perm past
+// the kept rows is -1.
 __global__ void __launch_bounds__(kRouteThreads)
 k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict__ perm,
             int *__restrict__ inv, int G, int E, int rpt) {
     extern __shared__ int sh[];
-    __shared__ int s_rows;  // kept assignments (meta[E])
-    int *cnt = sh, *run = sh + E, *wcnt = sh + 2 * E;  // wcnt [kRouteWaves][E]
+    // counts of all ids tot [E] (first those from the chunk on) and of the
+    // ids before the chunk bef [E], the
+    // chunk's per-wave counts / wave bases wc [W][E], each expert's first row
+    // for this chunk base [E]
+    int *tot = sh, *bef = sh + E, *wc = sh + 2 * E, *base = sh + (2 + kRouteWaves) * E;
+    __shared__ int s_rows;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const unsigned long long below = (1ull << lane) - 1ull;
-    int *mine = wcnt + wave * E;  // this wave's running counts
-    int eid[kRouteChunks], loc[kRouteChunks];
-
-    // Load a block's ids (wave w: the contiguous segment w of the block), then
-    // rank them: per 64-id chunk, lanes with equal expert ids find each other
-    // with log2(E) ballots, read the wave's running count of that expert and
-    // the chunk's leader advances it (LDS operations of one wave run in order).
-    auto load_block = [&](int b0) {
-        const int seg0 = b0 + wave * kRouteChunks * 64;
-#pragma unroll
-        for (int c = 0; c < kRouteChunks; ++c) {
-            const int g = seg0 + c * 64 + lane;
-            eid[c] = g < G ? ids[g] : -1;
-        }
-    };
-    auto rank_block = [&]() {
-#pragma unroll
-        for (int c = 0; c < kRouteChunks; ++c) {
-            const bool valid = eid[c] >= 0 && eid[c] < E;  // out-of-range ids are dropped
-            const int e = valid ? eid[c] : 0;
-            unsigned long long same = __ballot(valid);
-            for (int bit = 0; (1 << bit) < E; ++bit) {
-                const bool on = (e >> bit) & 1;
-                const unsigned long long bal = __ballot(valid && on);
-                same &= on ? bal : ~bal;
-            }
-            const int before = valid ? mine[e] : 0;  // every lane reads before the leader writes
-            loc[c] = before + __popcll(same & below);
-            if (valid && (same & below) == 0ull) mine[e] = before + __popcll(same);
-        }
-    };
-    // per-wave counts -> bases: wcnt[w][e] = run[e] + counts of waves < w
-    auto wave_bases = [&]() {
-        for (int x = tid; x < E; x += kRouteThreads) {
-            int r = run[x];
-            for (int w = 0; w < kRouteWaves; ++w) {
-                const int c = wcnt[w * E + x];
-                wcnt[w * E + x] = r;
-                r += c;
-            }
-            run[x] = r;
-        }
-    };
-    // dst: perm in global memory, or (one block) its copy in LDS, written out
-    // in order afterwards: the scattered 4-byte stores stay on chip
-    auto place_block = [&](int b0, int *dst) {
-        const int seg0 = b0 + wave * kRouteChunks * 64;
-#pragma unroll
-        for (int c = 0; c < kRouteChunks; ++c) {
-            const int g = seg0 + c * 64 + lane;
-            if (eid[c] >= 0 && eid[c] < E) {
-                const int p = mine[eid[c]] + loc[c];
-                dst[p] = g;
-                inv[g] = p;
-            } else if (g < G) {
-                inv[g] = -1;
-            }
-        }
-    };
-
-    // Pass 1: every block's ids ranked into per-wave counts (no atomics).
-    for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wcnt[i] = 0;
+    const int c0 = blockIdx.x * kRouteChunk;
+    for (int i = tid; i < (2 + kRouteWaves) * E; i += kRouteThreads) sh[i] = 0;
     __syncthreads();
-    for (int b0 = 0; b0 < G; b0 += kRouteBlock) {
-        load_block(b0);
-        rank_block();
+
+    // counts, sixteen ids' loads in flight per thread (G = 16384: one round)
+    for (int i0 = tid; i0 < G; i0 += 16 * kRouteThreads) {
+        int ev[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int g = i0 + u * kRouteThreads;
+            ev[u] = g < G ? ids[g] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int g = i0 + u * kRouteThreads;
+            if (ev[u] >= 0 && ev[u] < E) atomicAdd((g < c0 ? bef : tot) + ev[u], 1);  // before / from the chunk
+        }
     }
     __syncthreads();
-    for (int x = tid; x < E; x += kRouteThreads) {
-        int c = 0;
-        for (int w = 0; w < kRouteWaves; ++w) c += wcnt[w * E + x];
-        cnt[x] = c;
-    }
+    for (int e = tid; e < E; e += kRouteThreads) tot[e] += bef[e];
     __syncthreads();
     if (wave == 0) {  // row and row-tile offsets: a 64-lane inclusive scan per 64 experts
         int r0 = 0, t0 = 0;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + lane;
-            const int c = e < E ? cnt[e] : 0, tl = (c + rpt - 1) / rpt;
+            const int c = e < E ? tot[e] : 0, tl = (c + rpt - 1) / rpt;
             int r = c, t = tl;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -146,47 +108,67 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
                 if (lane >= o) { r += ru; t += tu; }
             }
             if (e < E) {
-                meta[e] = r0 + r - c;
-                meta[E + 1 + e] = t0 + t - tl;
-                run[e] = r0 + r - c;
+                base[e] = r0 + r - c + bef[e];
+                if (blockIdx.x == 0) {
+                    meta[e] = r0 + r - c;
+                    meta[E + 1 + e] = t0 + t - tl;
+                }
             }
             r0 += __shfl(r, 63);
             t0 += __shfl(t, 63);
         }
         if (lane == 0) {
-            meta[E] = r0;
-            meta[2 * E + 1] = t0;
             s_rows = r0;
+            if (blockIdx.x == 0) {
+                meta[E] = r0;
+                meta[2 * E + 1] = t0;
+            }
+        }
+    }
+
+    // rank this chunk: wave w's ids c0 + (w P + c) 64 + lane, pieces c in order
+    int eid[kRoutePieces], loc[kRoutePieces];
+    const int seg = c0 + wave * kRoutePieces * 64;
+    int *mine = wc + wave * E;
+#pragma unroll
+    for (int c = 0; c < kRoutePieces; ++c) {
+        const int g = seg + c * 64 + lane;
+        eid[c] = g < G ? ids[g] : -1;
+    }
+#pragma unroll
+    for (int c = 0; c < kRoutePieces; ++c) {
+        const bool valid = eid[c] >= 0 && eid[c] < E;
+        const int e = valid ? eid[c] : 0;
+        const unsigned long long same = route_group(valid, e, E);
+        const int before = valid ? mine[e] : 0;  // every lane reads before the leader writes
+        loc[c] = before + __popcll(same & below);
+        if (valid && (same & below) == 0ull) mine[e] = before + __popcll(same);
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kRouteThreads) {  // wave counts -> wave bases, in wave order
+        int r = base[e];
+        for (int w = 0; w < kRouteWaves; ++w) {
+            const int n = wc[w * E + e];
+            wc[w * E + e] = r;
+            r += n;
         }
     }
     __syncthreads();
-
-    // Pass 2: place.  One block (G <= kRouteBlock): its ranks are still in
-    // registers and wcnt holds its per-wave counts.  Otherwise each block is
-    // loaded and ranked again, on top of the running bases.
-    if (G <= kRouteBlock) {
-        int *sperm = wcnt + kRouteWaves * E;  // [meta[E]] rows
-        wave_bases();
-        __syncthreads();
-        place_block(0, sperm);
-        __syncthreads();
-        const int rows = s_rows;
-        for (int i = tid; i < rows; i += kRouteThreads) perm[i] = sperm[i];
-        for (int i = rows + tid; i < G; i += kRouteThreads) perm[i] = -1;  // dropped assignments
-        return;
+#pragma unroll
+    for (int c = 0; c < kRoutePieces; ++c) {
+        const int g = seg + c * 64 + lane;
+        if (eid[c] >= 0 && eid[c] < E) {
+            const int p = mine[eid[c]] + loc[c];
+            perm[p] = g;
+            inv[g] = p;
+        } else if (g < G) {
+            inv[g] = -1;
+        }
     }
-    for (int b0 = 0; b0 < G; b0 += kRouteBlock) {
-        load_block(b0);
-        for (int e = lane; e < E; e += 64) mine[e] = 0;
-        __syncthreads();
-        rank_block();
-        __syncthreads();
-        wave_bases();
-        __syncthreads();
-        place_block(b0, perm);
-        __syncthreads();  // wcnt is reset for the next block
-    }
-    for (int i = s_rows + tid; i < G; i += kRouteThreads) perm[i] = -1;  // dropped assignments
+    // perm past the kept rows: this workgroup's share of [rows, G)
+    const int rows = s_rows;
+    for (int i = c0 + tid; i < min(c0 + kRouteChunk, G); i += kRouteThreads)
+        if (i >= rows) perm[i] = -1;
 }
 
 // Xs[p] = X[perm[p] / topk] (rows of K DT), one workgroup per row; a row whose
@@ -239,13 +221,12 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
 
 }  // namespace
 
-// counts, running bases and per-wave counts; with one block also perm's LDS copy
-size_t moe_route_lds(int E, int G) {
-    return ((size_t)(2 + kRouteWaves) * E + (G <= kRouteBlock ? (size_t)G : 0)) * sizeof(int);
-}
+// per-wave total, preceding and chunk counts, and each expert's base row
+size_t moe_route_lds(int E) { return (size_t)(3 + kRouteWaves) * E * sizeof(int); }
 
 ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st) {
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), moe_route_lds(E, G), st, ids, meta, perm, inv,
+    const unsigned blocks = (unsigned)((G + kRouteChunk - 1) / kRouteChunk);
+    hipLaunchKernelGGL(k_moe_route, dim3(blocks), dim3(kRouteThreads), moe_route_lds(E), st, ids, meta, perm, inv,
                        G, E, moe_tile_rows());
     return check_launch();
 }
