@@ -399,15 +399,17 @@ def bench_c4(torch, T, synth, formats, orc):
         T.bitcos_slice_ranks(dB, dSR, K, N, ls)
         sets, W = rotation(torch, [dB, dev16(torch, S, bf16), dSR], buf.nbytes + S.nbytes)
         dC = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        wsb = T.bitcos_gemv_ws_bytes(N, ls)  # the split launch's sums and strip counters
+        dws = torch.zeros(max(wsb, 16), dtype=torch.uint8, device="cuda")
         it = [0]
 
         def fwht():
             T.hadamard_fwht(dx, ds, dy, M, K, HB, True)
 
-        def gemv():
+        def gemv(ws=dws):
             b, sc, sr = W[it[0] % sets]
             it[0] += 1
-            T.bitcos_fp16_upcvt_gemm(dy, b, sc, sr, dC, None, None, M, N, K, ls)
+            T.bitcos_fp16_upcvt_gemm(dy, b, sc, sr, dC, None, None, M, N, K, ls, ws=ws)
 
         def call():
             fwht()
@@ -422,9 +424,11 @@ def bench_c4(torch, T, synth, formats, orc):
         bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
         us = graph_time_us(torch, call, 200)
         g_us = graph_time_us(torch, gemv, 200)
+        g1_us = graph_time_us(torch, lambda: gemv(None), 200)  # one workgroup per strip
         f_us = graph_time_us(torch, fwht, 200)
         nbytes = M * K * 2 + buf.nbytes + S.nbytes + M * N * 2  # bitcos_fp16_upcvt/main.cpp:289-291
-        out[f"z{z}"] = {"us": round(us, 2), "gemv_us": round(g_us, 2), "fwht_us": round(f_us, 2),
+        out[f"z{z}"] = {"us": round(us, 2), "gemv_us": round(g_us, 2), "gemv_unsplit_us": round(g1_us, 2),
+                        "fwht_us": round(f_us, 2),
                         "gemv_GB/s": round(nbytes / g_us / 1e3, 1),
                         "gemv_hbm_frac": round(nbytes / g_us / 1e3 / HBM_PEAK_GBS, 4),
                         "pipeline_GB/s": round((nbytes + 2 * M * K * 2 + K) / us / 1e3, 1),

@@ -191,6 +191,22 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const ui
                                               const void *S, const uint32_t *SR, int ls, void *C,
                                               const void *Other, const void *Bias, int M, int N,
                                               int K, int postop, int out_f32, void *stream);
+/* The same call with device scratch (no reference counterpart: the
+ * reference's GEMV runs one workgroup per 64-column strip, as the entry
+ * above does).  Where the strips would load the CUs unevenly (N = 21504:
+ * 336 strips on 256 CUs) a strip's ls slices are spread over several
+ * workgroups, which store fp32 sums [slices][4][N] and a counter per strip
+ * there; the last workgroup of a strip adds the sums in order (the same bits
+ * on every run).  ws: ternocl_bitcos_gemv_ws_bytes(N, ls) bytes, 16-byte
+ * aligned, zeroed once before its first use (ternocl_workspace_zero); every
+ * call leaves the counters at zero.  NULL or short: the unsplit launch.
+ * Calls that share a workspace must not overlap. */
+size_t ternocl_bitcos_gemv_ws_bytes(int N, int ls);
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm_ws(int dtype, const void *A, const uint32_t *B,
+                                                 const void *S, const uint32_t *SR, int ls, void *C,
+                                                 const void *Other, const void *Bias, int M, int N,
+                                                 int K, int postop, int out_f32, void *ws, size_t ws_bytes,
+                                                 void *stream);
 /* ---- BITCOS M-tiled prefill ---------------------------------------------
  * Replaces bitcos_fp16_upcvt_gemm_mt (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:303-305):
  * the same C as ternocl_bitcos_fp16_upcvt_gemm (within the float tolerance) for

@@ -25,7 +25,7 @@ __all__ = [
     "int2_gemv_decode", "int2_gemv_stream_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
     "int2_pack", "int2_unpack", "bitcos_pack", "bitcos_unpack", "bitcos_slice_ranks_host",
     "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
-    "bitcos_fp16_upcvt_gemm", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
+    "bitcos_fp16_upcvt_gemm", "bitcos_gemv_ws_bytes", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
     "moe_tile_rows", "int2_moe_route", "int2_moe_gather", "int2_moe_gemm", "int2_moe_combine",
     "int2_moe_prefill_ws_bytes", "int2_moe_prefill", "int2_moe_prefill_int8_ws_bytes", "int2_moe_prefill_int8",
@@ -251,13 +251,26 @@ def int2_s8_decode(B, D, K: int, N: int, stream=None) -> None:
 
 # ---- BITCOS (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl) ------------------------
 
+def bitcos_gemv_ws_bytes(N: int, ls: int) -> int:
+    """Scratch bytes of bitcos_fp16_upcvt_gemm's split launch (0: none)."""
+    return lib().ternocl_bitcos_gemv_ws_bytes(N, ls)
+
+
 def bitcos_fp16_upcvt_gemm(A, B, S, SR, C, Other, Bias, M: int, N: int, K: int, ls: int = 1,
-                           postop: int = 0, out_f32: bool = False, stream=None) -> None:
+                           postop: int = 0, out_f32: bool = False, ws=None, stream=None) -> None:
     """bitcos_fp16_upcvt_gemv(A, B, S, SR, C, Other, Bias, M, N, K) of
-    bitcos_fp16_upcvt.cl:179 with LS = ls K slices (SR computed for that ls)."""
-    _check(lib().ternocl_bitcos_fp16_upcvt_gemm(_dtype_of(A), _ptr(A), _ptr(B), _ptr(S), _ptr(SR), ls,
-                                                _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
-                                                int(bool(out_f32)), _stream(stream)))
+    bitcos_fp16_upcvt.cl:179 with LS = ls K slices (SR computed for that ls).
+    ``ws`` (bitcos_gemv_ws_bytes, zeroed once): the launch that spreads a
+    strip's slices over several workgroups where that evens out the CUs."""
+    if ws is None:
+        _check(lib().ternocl_bitcos_fp16_upcvt_gemm(_dtype_of(A), _ptr(A), _ptr(B), _ptr(S), _ptr(SR), ls,
+                                                    _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                                    int(bool(out_f32)), _stream(stream)))
+    else:
+        _check(lib().ternocl_bitcos_fp16_upcvt_gemm_ws(_dtype_of(A), _ptr(A), _ptr(B), _ptr(S), _ptr(SR), ls,
+                                                       _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                                       int(bool(out_f32)), _ptr(ws), _nbytes(ws),
+                                                       _stream(stream)))
 
 
 def bitcos_gemm_mt_ws_bytes(K: int, N: int) -> int:

@@ -36,6 +36,8 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_int2_int8_gemm": (I, [I, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "ternocl_int2_s8_decode": (I, [P, P, I, I, P]),
     "ternocl_bitcos_fp16_upcvt_gemm": (I, [I, P, P, P, P, I, P, P, P, I, I, I, I, I, P]),
+    "ternocl_bitcos_fp16_upcvt_gemm_ws": (I, [I, P, P, P, P, I, P, P, P, I, I, I, I, I, P, Z, P]),
+    "ternocl_bitcos_gemv_ws_bytes": (Z, [I, I]),
     "ternocl_bitcos_gemm_mt_ws_bytes": (Z, [I, I]),
     "ternocl_bitcos_fp16_upcvt_gemm_mt": (I, [I, P, P, P, P, I, P, P, P, I, I, I, I, I, P, Z, P]),
     "ternocl_bitcos_to_int2": (I, [P, P, I, P, I, I, P]),

@@ -72,7 +72,9 @@ ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, 
 int bitcos_max_ls();
 ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, const void *S,
                                const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias,
-                               int M, int N, int K, int postop, int out_f32, hipStream_t st);
+                               int M, int N, int K, int postop, int out_f32, hipStream_t st, void *ws = nullptr,
+                               size_t ws_bytes = 0);
+size_t bitcos_gemv_ws_need(int N, int ls);
 ternocl_status bitcos_slice_ranks_run(const uint32_t *Bc, uint32_t *SR, int N, int K, int ls,
                                       hipStream_t st);
 ternocl_status bitcos_dequant_run(int dtype, const uint32_t *Bc, const void *S, void *W, int N, int K,
@@ -286,17 +288,31 @@ ternocl_status ternocl_int2_s8_decode(const uint32_t *B, uint32_t *D, int K, int
     return int2_s8_decode_run(B, D, K, N, (hipStream_t)stream);
 }
 
-ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
-                                              const void *S, const uint32_t *SR, int ls, void *C,
-                                              const void *Other, const void *Bias, int M, int N,
-                                              int K, int postop, int out_f32, void *stream) {
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm_ws(int dtype, const void *A, const uint32_t *B,
+                                                 const void *S, const uint32_t *SR, int ls, void *C,
+                                                 const void *Other, const void *Bias, int M, int N,
+                                                 int K, int postop, int out_f32, void *ws, size_t ws_bytes,
+                                                 void *stream) {
     ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
     if (ls < 1 || ls > bitcos_max_ls()) FAIL(TERNOCL_ERR_INVALID_ARG, "ls must be 1..16");
     if (K % (64 * ls)) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "BITCOS needs K % (64 * ls) == 0");
     if (ls > 1 && !SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR (slice ranks for ls slices) must be non-null when ls > 1");
     return bitcos_gemv_run(dtype, A, B, S, SR, ls, C, Other, Bias, M, N, K, postop, out_f32,
-                           (hipStream_t)stream);
+                           (hipStream_t)stream, ws, ws_bytes);
+}
+
+ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,
+                                              const void *S, const uint32_t *SR, int ls, void *C,
+                                              const void *Other, const void *Bias, int M, int N,
+                                              int K, int postop, int out_f32, void *stream) {
+    return ternocl_bitcos_fp16_upcvt_gemm_ws(dtype, A, B, S, SR, ls, C, Other, Bias, M, N, K, postop, out_f32,
+                                             nullptr, 0, stream);
+}
+
+size_t ternocl_bitcos_gemv_ws_bytes(int N, int ls) {
+    if (N < 16 || N % 16 || ls < 1 || ls > bitcos_max_ls()) return 0;
+    return bitcos_gemv_ws_need(N, ls);
 }
 
 static ternocl_status check_bitcos_slices(int N, int K, int ls, const uint32_t *SR) {

@@ -13,7 +13,11 @@
 // Work split: lane = output column (64 columns per wave, every bitmap load is
 // 256 contiguous bytes), wave s of a workgroup = K slice s (it enters the
 // column's sign stream at SR[s-1]); the slices reduce through LDS in slice
-// order (deterministic).  Per 64-row chunk a lane loads the column's two
+// order (deterministic).  With a workspace the ls slices of a strip may be
+// spread over ksw workgroups (grid.y), so that the launch fills the CUs evenly
+// (N = 21504: 336 strips of 14 waves leave 80 CUs with twice the work); each
+// writes its sums to the workspace and the last of a strip's workgroups (a
+// device-scope counter) adds them in order and applies the epilogue.  Per 64-row chunk a lane loads the column's two
 // bitmap words and three sign words (the chunk consumes at most 64 sign bits
 // from the column's rank onwards); loads run four chunks (bitmap) and three
 // chunks (signs, whose address needs the rank, i.e. the previous bitmap words)
@@ -27,6 +31,7 @@
 // partial per 128-row group, then acc += partial * S as the reference's host
 // gold (bitcos_fp16_upcvt/main.cpp:64-86).
 #include "common.hpp"
+
 
 namespace tcl {
 namespace {
@@ -78,12 +83,15 @@ __device__ __forceinline__ void bc_decode_word(const uint2 *lut, uint32_t bm, ui
     }
 }
 
+// ksw > 1: workgroup (strip, blockIdx.y) runs slices blockIdx.y * wps ..
+// + wps - 1 (wps = waves per workgroup); wsum fp32 [ksw][MR][N] sums, cnt one
+// zero-initialised counter per strip (left at zero again).
 template <int MR, bool BF16>
 __global__ void __launch_bounds__(64 * kBcMaxLs)
 k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
               const uint16_t *__restrict__ S, const uint32_t *__restrict__ SR, void *__restrict__ C,
               const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int m0, int N,
-              int K, int ls, int postop, int out_f32) {
+              int K, int ls, int postop, int out_f32, int ksw = 1, float *wsum = nullptr, uint32_t *cnt = nullptr) {
     __shared__ uint2 lut[256];
     __shared__ float red[kBcMaxLs - 1][MR][64];
     bc_build_lut<BF16>(lut);
@@ -94,10 +102,12 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
     const int nc = n < N ? n : N - 1;
     const size_t bw = (size_t)(K >> 5) * N;
     const uint32_t *__restrict__ sg = Bc + bw + N + Bc[bw + nc];
+    const int wps = blockDim.x >> 6, ks = ksw > 1 ? (int)blockIdx.y : 0;
+    const int sl = __builtin_amdgcn_readfirstlane(ks * wps + wave);  // this wave's K slice
     const int slice = K / ls;
-    const int k0 = wave * slice;
+    const int k0 = sl * slice;
     const int chunks = slice >> 6;  // 64-row chunks (K % (64 * ls) == 0)
-    uint32_t R = wave ? SR[(size_t)(wave - 1) * N + nc] : 0u;
+    uint32_t R = sl ? SR[(size_t)(sl - 1) * N + nc] : 0u;
 
     // activation rows m0 .. m0 + MR - 1 as packed pairs (rows past M repeat M - 1)
     const uint32_t *__restrict__ ar[MR];
@@ -194,16 +204,49 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
         }
     }
 
-    // reduce the slices in slice order
-    if (ls > 1) {
+    // reduce the workgroup's slices in slice order
+    if (wps > 1) {
         if (wave > 0)
 #pragma unroll
             for (int r = 0; r < MR; ++r) red[wave - 1][r][lane] = acc[r];
         __syncthreads();
         if (wave > 0) return;
-        for (int j = 0; j < ls - 1; ++j)
+        for (int j = 0; j < wps - 1; ++j)
 #pragma unroll
             for (int r = 0; r < MR; ++r) acc[r] += red[j][r][lane];
+    }
+    if (ksw > 1) {
+        // this workgroup's sums, then the strip's counter; the last of the ksw
+        // workgroups adds them in order (device-scope stores and loads:
+        // coherent across the XCDs' L2s without a cache write-back; the wait
+        // orders the stores before the counter)
+        if (n < N)
+#pragma unroll
+            for (int r = 0; r < MR; ++r)
+                __hip_atomic_store(wsum + ((size_t)ks * MR + r) * N + n, acc[r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        uint32_t prev = 0;
+        if (lane == 0)  // wraps to 0 at the last arrival
+            prev = __builtin_amdgcn_atomic_inc32(cnt + blockIdx.x, (uint32_t)(ksw - 1), __ATOMIC_RELAXED, "agent");
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev != (uint32_t)(ksw - 1)) return;
+        float v[kBcMaxLs][MR];  // every workgroup's sums in flight at once (ksw <= 16), added in order
+#pragma unroll
+        for (int u = 0; u < kBcMaxLs; ++u) {
+            const int s2 = u < ksw ? u : ksw - 1;
+#pragma unroll
+            for (int r = 0; r < MR; ++r)
+                v[u][r] = __hip_atomic_load(wsum + ((size_t)s2 * MR + r) * N + nc, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < kBcMaxLs; ++u) {
+            if (u >= ksw) break;
+#pragma unroll
+            for (int r = 0; r < MR; ++r) acc[r] = u == 0 ? v[u][r] : acc[r] + v[u][r];
+        }
     }
     if (n >= N) return;
     epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
@@ -331,35 +374,63 @@ k_bitcos_to_int2(const uint32_t *__restrict__ Bc, const uint32_t *__restrict__ S
 template <int MR, bool BF16>
 void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
-               int out_f32, hipStream_t st) {
-    hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16>), dim3((N + 63) / 64), dim3(64 * ls), 0, st,
+               int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
+    hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16>), dim3((N + 63) / 64, ksw), dim3(64 * (ls / ksw)), 0, st,
                        (const uint16_t *)A, Bc, (const uint16_t *)S, SR, C, (const uint16_t *)Other, Bias,
-                       M, m0, N, K, ls, postop, out_f32);
+                       M, m0, N, K, ls, postop, out_f32, ksw, part, cnt);
 }
 
 template <bool BF16>
 void bc_launch_rows(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                     const void *Other, const void *Bias, int M, int N, int K, int ls, int postop,
-                    int out_f32, hipStream_t st) {
+                    int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
     for (int m0 = 0; m0 < M; m0 += 4) {
         const int rows = M - m0;
-        if (rows == 1) bc_launch<1, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, st);
-        else if (rows == 2) bc_launch<2, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, st);
-        else bc_launch<4, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, st);
+        if (rows == 1) bc_launch<1, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st);
+        else if (rows == 2) bc_launch<2, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st);
+        else bc_launch<4, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st);
     }
 }
+
+// Workgroups per strip for a launch of N / 64 strips of ls slices: the
+// smallest divisor of ls that puts fewer waves on the busiest CU than one
+// workgroup per strip does, with the workgroups dealt evenly over the 256 CUs
+// (more workgroups cost more than the balance returns: N = 21504, ls = 14,
+// graph-timed at z = .5: 1 per strip 20.9 us, 2 19.0, 7 21.7, 14 22.0).
+int bc_pick_ksw(int N, int ls) {
+    const long strips = (N + 63) / 64;
+    const long base = (strips + 255) / 256 * ls;
+    for (int k = 2; k <= ls; ++k)
+        if (ls % k == 0 && (strips * k + 255) / 256 * (ls / k) < base) return k;
+    return 1;
+}
+
+// Workspace of a split launch: a counter per 64-column strip (256-byte
+// block), then the sums fp32 [ksw][4][N].
+size_t bc_cnt_bytes(int N) { return ((size_t)((N + 63) / 64) * 4 + 255) & ~(size_t)255; }
+size_t bc_split_ws(int N, int ksw) { return ksw > 1 ? bc_cnt_bytes(N) + (size_t)ksw * 4 * N * 4 : 0; }
 
 }  // namespace
 
 int bitcos_max_ls() { return kBcMaxLs; }
 
+// Workspace bytes for the split launch of this shape (0: none helps).
+size_t bitcos_gemv_ws_need(int N, int ls) { return bc_split_ws(N, bc_pick_ksw(N, ls)); }
+
+// ws (16-byte aligned, counters zeroed before the first call, as
+// bitcos_gemv_ws_need): the split launch; without it one workgroup per strip.
 ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, const void *S,
                                const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias,
-                               int M, int N, int K, int postop, int out_f32, hipStream_t st) {
+                               int M, int N, int K, int postop, int out_f32, hipStream_t st, void *ws,
+                               size_t ws_bytes) {
+    int ksw = bc_pick_ksw(N, ls);
+    if (ksw > 1 && !(ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= bc_split_ws(N, ksw))) ksw = 1;
+    uint32_t *cnt = ksw > 1 ? (uint32_t *)ws : nullptr;
+    float *part = ksw > 1 ? (float *)((uint8_t *)ws + bc_cnt_bytes(N)) : nullptr;
     if (dtype == TERNOCL_BF16)
-        bc_launch_rows<true>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, st);
+        bc_launch_rows<true>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st);
     else
-        bc_launch_rows<false>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, st);
+        bc_launch_rows<false>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st);
     return check_launch();
 }
 

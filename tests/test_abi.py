@@ -88,6 +88,16 @@ def test_ws_bytes_query():
     assert T.int2_gemm_ws_bytes(256, 1024, 1024) == 0
 
 
+def test_bitcos_ws_bytes_query():
+    """The split BITCOS launch: a counter per 64-column strip (256-byte block) and
+    fp32 sums [slices][4][N]; none where one workgroup per strip fills the chip."""
+    import ternocl_amd as T
+    assert T.bitcos_gemv_ws_bytes(21504, 14) == 1536 + 2 * 4 * 21504 * 4  # 336 strips: 2 workgroups of 7 waves each
+    assert T.bitcos_gemv_ws_bytes(16384, 14) == 0  # 256 strips of 14 waves: one per CU
+    assert T.bitcos_gemv_ws_bytes(4096, 1) == 0
+    assert T.bitcos_gemv_ws_bytes(4100, 4) == 0  # N % 16
+
+
 @pytest.mark.parametrize("entry", ["ternocl_int2_moe_prefill", "ternocl_int2_moe_prefill_int8",
                                    "ternocl_int2_moe_decode"])
 def test_moe_layer_host_validation(entry):

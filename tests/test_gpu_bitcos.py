@@ -66,7 +66,7 @@ def _bitcos_case(seed, M, K, N, z, bf16):
     return A, codes, S, other, bias_f
 
 
-def _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32):
+def _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32, ws=None):
     dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(buf), dev_dt(S, bf16), dev_dt(other, bf16)
     dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
     T.bitcos_slice_ranks(dB, dSR, K, N, ls)
@@ -76,7 +76,8 @@ def _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, o
     else:
         dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
         dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
-    T.bitcos_fp16_upcvt_gemm(dA, dB, dS, dSR if ls > 1 else None, dC, dO, dBias, M, N, K, ls, postop, out_f32)
+    T.bitcos_fp16_upcvt_gemm(dA, dB, dS, dSR if ls > 1 else None, dC, dO, dBias, M, N, K, ls, postop, out_f32,
+                             ws=ws)
     torch.cuda.synchronize()
     return dC
 
@@ -130,6 +131,33 @@ def test_bitcos_gemv_parity(dev, orc, M, K, N, ls, z, bf16):
     dC = _bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False)
     want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 0, False)
     bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ls", SHAPES)
+def test_bitcos_gemv_split_launch(dev, orc, M, K, N, ls, bf16):
+    """With the workspace a strip's slices may run on several workgroups (here
+    every shape but N = 256 strips' worth: too few strips, or 336 on 256 CUs);
+    the last adds their sums in order.  The gold within 1e-3 + 1e-2 |ref| with
+    the bias + residual epilogue, the same bits on repeated calls, the counters
+    back at zero."""
+    import torch
+    import ternocl_amd as T
+    wsb = T.bitcos_gemv_ws_bytes(N, ls)
+    print(f"bitcos split M={M} K={K} N={N} ls={ls} bf16={bf16} ws={wsb}", flush=True)
+    if ls > 1:
+        assert wsb > 0
+    A, codes, S, other, bias_f = _bitcos_case(6000 + M + K + N + ls, M, K, N, 0.5, bf16)
+    buf = formats.bitcos_pack(codes)
+    ws = torch.zeros(max(wsb, 16), dtype=torch.uint8, device="cuda")
+    outs = [host_u16(_bitcos_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 5, False, ws=ws))
+            for _ in range(3)]
+    assert all(np.array_equal(outs[0], o) for o in outs[1:]), "non-deterministic"
+    cnt_bytes = ((N + 63) // 64 * 4 + 255) // 256 * 256
+    assert not ws[:cnt_bytes].any().item(), "strip counters not left at zero"
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 5, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(outs[0], bf16), formats.dt_to_f32(want, bf16))
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
 
 
