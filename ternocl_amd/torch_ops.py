@@ -164,7 +164,7 @@ def bitcos_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, SR: Optional[
                 out_f32: bool) -> torch.Tensor:
     """C [M, N] of the BITCOS weights B (the common/bitcos.hpp buffer, int32) with slice ranks SR
     for ls slices.  M >= 16 takes the M-tiled path (a workspace of the re-packed weights is
-    allocated per call), smaller M the GEMV."""
+    allocated per call), smaller M the GEMV (with the split launch's workspace where it has one)."""
     _chk_bitcos(A, B, S, SR, ls, N, other, bias, out_f32)
     M, K = A.shape
     C = torch.empty((M, N), dtype=_out_dtype(A, out_f32), device=A.device)
@@ -172,7 +172,9 @@ def bitcos_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, SR: Optional[
         ws = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device=A.device)
         T.bitcos_fp16_upcvt_gemm_mt(A, B, S, SR, C, other, bias, M, N, K, ls, ws, postop, out_f32)
     else:
-        T.bitcos_fp16_upcvt_gemm(A, B, S, SR, C, other, bias, M, N, K, ls, postop, out_f32)
+        wsb = T.bitcos_gemv_ws_bytes(N, ls)  # the split launch's sums / counters (zeroed: counters start at 0)
+        ws = torch.zeros(wsb, dtype=torch.uint8, device=A.device) if wsb else None
+        T.bitcos_fp16_upcvt_gemm(A, B, S, SR, C, other, bias, M, N, K, ls, postop, out_f32, ws=ws)
     return C
 
 
