@@ -470,6 +470,17 @@ def bench_c4(torch, T, synth, formats, orc):
                                  "us": round(us, 2), "TFLOPS": round(flops / us / 1e6, 1),
                                  "mfma_frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                                  "repack_us": round(r_us, 2), "parity_bad": bad, "parity_rows": rows}
+
+    def mt_in_tile():  # the reference's call: no workspace, the tiles decode BITCOS
+        T.bitcos_fp16_upcvt_gemm_mt(dA, dB, dS, dSR, dC, None, None, Mp, N, K, ls, None)
+    mt_in_tile()
+    torch.cuda.synchronize()
+    got = formats.dt_to_f32(dC[:rows].contiguous().view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
+    us = graph_time_us(torch, mt_in_tile, 10)
+    out["prefill_m1024_z0.5"]["in_tile"] = {"us": round(us, 2), "TFLOPS": round(flops / us / 1e6, 1),
+                                            "mfma_frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                            "parity_bad": bad, "parity_rows": rows}
     return out
 
 

@@ -210,11 +210,14 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_ws(int dtype, const void *A, const
 /* ---- BITCOS M-tiled prefill ---------------------------------------------
  * Replaces bitcos_fp16_upcvt_gemm_mt (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:303-305):
  * the same C as ternocl_bitcos_fp16_upcvt_gemm (within the float tolerance) for
- * any M, with the weights streamed once instead of once per 4 rows.  One pass
- * re-packs the BITCOS weights into the int2 format (K * N / 4 bytes of ws,
- * ternocl_bitcos_gemm_mt_ws_bytes), then the int2 prefill GEMM engine runs on
- * them with S as is.  SR / ls as for ternocl_bitcos_fp16_upcvt_gemm (the
- * re-pack splits K into ls slices); the same constraints. */
+ * any M, with the weights streamed once instead of once per 4 rows.
+ * ws = NULL (the reference's call): the int2 prefill GEMM engine's tiles
+ * decode the BITCOS weights themselves, each lane following its column's
+ * sign stream down K (SR unused).  With ws (K * N / 4 bytes,
+ * ternocl_bitcos_gemm_mt_ws_bytes): one pass re-packs the weights into the
+ * int2 format there, then the int2 engine runs on them with S as is (the
+ * re-pack splits K into ls slices).  SR / ls as for
+ * ternocl_bitcos_fp16_upcvt_gemm; the same constraints. */
 size_t ternocl_bitcos_gemm_mt_ws_bytes(int K, int N);
 ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const uint32_t *B,
                                                  const void *S, const uint32_t *SR, int ls, void *C,

@@ -75,6 +75,9 @@ ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, con
                                int M, int N, int K, int postop, int out_f32, hipStream_t st, void *ws = nullptr,
                                size_t ws_bytes = 0);
 size_t bitcos_gemv_ws_need(int N, int ls);
+ternocl_status bitcos_gemm_mt_run(int dtype, const void *A, const uint32_t *Bc, const void *S, void *C,
+                                  const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                  int out_f32, hipStream_t st);
 ternocl_status bitcos_slice_ranks_run(const uint32_t *Bc, uint32_t *SR, int N, int K, int ls,
                                       hipStream_t st);
 ternocl_status bitcos_dequant_run(int dtype, const uint32_t *Bc, const void *S, void *W, int N, int K,
@@ -343,8 +346,13 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const
     ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
     if ((s = check_bitcos_slices(N, K, ls, SR)) != TERNOCL_OK) return s;
+    if (!ws) {  // the tiles decode the BITCOS weights themselves
+        if ((size_t)M * K * 2 >= kMaxBufBytes)
+            FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the M-tiled BITCOS GEMM takes A below 2^31 bytes");
+        return bitcos_gemm_mt_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, (hipStream_t)stream);
+    }
     const size_t need = ternocl_bitcos_gemm_mt_ws_bytes(K, N);
-    if (!ws || ws_bytes < need) FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_bitcos_gemm_mt_ws_bytes(K, N) bytes");
+    if (ws_bytes < need) FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_bitcos_gemm_mt_ws_bytes(K, N) bytes");
     if (((uintptr_t)ws & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "ws must be 16-byte aligned");
     if (need >= kMaxBufBytes || (size_t)M * K * 2 >= kMaxBufBytes)
         FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the M-tiled BITCOS path takes A and the re-packed weights below 2^31 bytes");

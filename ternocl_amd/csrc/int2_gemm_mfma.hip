@@ -152,14 +152,19 @@ template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
 // DUAL: the MoE gate/up pair in one pass over A -- acc from (B, S) is the up
 // projection, acc2 from (B2, S2) the gate; C = DT(silu(gate) * DT(up)), the
 // two-launch sequence's result (up rounded to DT, then POSTOP 1) bit for bit.
-template <class Cfg, bool BF16, bool DUAL = false, bool SHORT = false>
+// BC: B is a BITCOS buffer (bitmap [K/32][N] | offsets [N] | sign streams |
+// pad), decoded in the tile into the int2 words the int2 path loads (the
+// M-tiled BITCOS GEMM with no re-pack); bclut is the 256-byte table of
+// k_bitcos_gemm.  Unsplit only (kseg == K).
+template <class Cfg, bool BF16, bool DUAL = false, bool SHORT = false, bool BC = false>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
                                           const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                           void *__restrict__ C, const uint16_t *__restrict__ Other,
                                           const void *__restrict__ Bias, int crow0, int N, int K, int kseg,
                                           int n0, int postop, int out_f32, uint16_t *lds,
                                           const uint32_t *__restrict__ B2 = nullptr,
-                                          const uint16_t *__restrict__ S2 = nullptr) {
+                                          const uint16_t *__restrict__ S2 = nullptr,
+                                          const uint8_t *__restrict__ bclut = nullptr) {
     constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = SHORT ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
@@ -244,6 +249,66 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
                 sraw[m][cb] = __builtin_amdgcn_raw_buffer_load_b16(m ? rS2 : rS, v + 64 * cb, 0, 0);
     };
 
+    // BC: lane column n (32 cb + c32 of the wave's block), its sign stream and
+    // rank (non-zeros above the next stage to decode), the bitmap words of two
+    // stages (slot = stage & 1, loaded two stages ahead) and the sign words of
+    // the next stage (loaded one stage ahead: their address needs the rank).
+    // Loads past the last stage read the last stage's words and the stream's
+    // pad words, and are never decoded.
+    constexpr int BCC = BC ? CB2 : 1;
+    const size_t bcw = (size_t)(K >> 5) * N;  // bitmap words
+    const uint32_t *bc_sg[BCC];
+    uint32_t bc_r[BCC], bc_bm[2][BCC][2], bc_q[BCC][3];
+    int bc_n[BCC];
+    auto bc_bm_load = [&](int st, int slot) __attribute__((always_inline)) {
+        const size_t kp = (size_t)2 * (st < stages ? st : stages - 1);
+#pragma unroll
+        for (int cb = 0; cb < BCC; ++cb) {
+            bc_bm[slot][cb][0] = B[kp * N + bc_n[cb]];
+            bc_bm[slot][cb][1] = B[(kp + 1) * N + bc_n[cb]];
+        }
+    };
+    auto bc_sg_load = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int cb = 0; cb < BCC; ++cb) {
+            const uint32_t w = bc_r[cb] >> 5;
+            bc_q[cb][0] = bc_sg[cb][w];
+            bc_q[cb][1] = bc_sg[cb][w + 1];
+            bc_q[cb][2] = bc_sg[cb][w + 2];
+        }
+    };
+    // the stage's 64 rows of column cb as four int2 words (16 rows each); the
+    // rank advances.  Lanes l and l + 32 hold the same column: each decodes one
+    // 32-row bitmap word (h = q32) and v_permlane32_swap hands each the other's.
+    auto bc_decode = [&](int slot, uint32_t out[NB][CB2][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int cb = 0; cb < BCC; ++cb) {
+            const uint32_t r0 = bc_r[cb], base = r0 >> 5;
+            const uint32_t b0 = bc_bm[slot][cb][0], b1 = bc_bm[slot][cb][1];
+            const uint32_t bm = q32 ? b1 : b0;
+            const uint32_t r = q32 ? r0 + __builtin_popcount(b0) : r0;
+            const bool up = (r >> 5) != base;  // the window starts in the second sign word
+            const uint32_t sw = __builtin_amdgcn_alignbit(up ? bc_q[cb][2] : bc_q[cb][1],
+                                                          up ? bc_q[cb][1] : bc_q[cb][0], r & 31u);
+            uint32_t w[2] = {0u, 0u}, p = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t m4 = (bm >> (4 * i)) & 15u;
+                const uint32_t s4 = (sw >> p) & 15u;
+                p = __builtin_popcount(m4) + p;
+                w[i >> 2] |= (uint32_t)bclut[(m4 << 4) | s4] << (8 * (i & 3));
+            }
+            // element 0: the words of lanes 0..31 (h = 0) in every lane; element 1: of lanes 32..63
+            const auto x0 = __builtin_amdgcn_permlane32_swap(w[0], w[0], false, false);
+            const auto x1 = __builtin_amdgcn_permlane32_swap(w[1], w[1], false, false);
+            out[0][cb][0] = x0[0];
+            out[0][cb][1] = x1[0];
+            out[0][cb][2] = x0[1];
+            out[0][cb][3] = x1[1];
+            bc_r[cb] = r0 + __builtin_popcount(b0) + __builtin_popcount(b1);
+        }
+    };
+
     f32x16_t acc[MB2][CB2], acc2[DUAL ? MB2 : 1][DUAL ? CB2 : 1];
 #pragma unroll
     for (int mb = 0; mb < MB2; ++mb)
@@ -258,7 +323,20 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
 
     ScaleOp<BF16> sop[NB][CB2];
     a_load(0, 0);
-    b_load();
+    if constexpr (BC) {
+#pragma unroll
+        for (int cb = 0; cb < BCC; ++cb) {
+            const int n = n0 + wn + 32 * cb + c32;
+            bc_n[cb] = n < N ? n : N - 1;
+            bc_sg[cb] = B + bcw + N + B[bcw + bc_n[cb]];
+            bc_r[cb] = 0;
+        }
+        bc_bm_load(0, 0);
+        bc_bm_load(1, 1);
+        bc_sg_load();
+    } else {
+        b_load();
+    }
     s_load(0);
     a_load(1, 1);
     a_store(lds, 0);
@@ -304,12 +382,16 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         const uint16_t *abuf = lds + cur * kBuf;
         const uint32_t nxt = cur == 2 ? 0 : cur + 1;
         uint32_t bwc[NB][CB2][4];
+        if constexpr (BC) {
+            bc_decode(par, bwc);
+        } else {
 #pragma unroll
-        for (int m = 0; m < NB; ++m)
+            for (int m = 0; m < NB; ++m)
 #pragma unroll
-            for (int cb = 0; cb < CB2; ++cb)
+                for (int cb = 0; cb < CB2; ++cb)
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) bwc[m][cb][ks] = bw[m][cb][ks];
+                    for (int ks = 0; ks < 4; ++ks) bwc[m][cb][ks] = bw[m][cb][ks];
+        }
         if (par == 0) {  // a new 128-row scale group
 #pragma unroll
             for (int m = 0; m < NB; ++m)
@@ -321,7 +403,12 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         // are loaded on the group's second stage.  (sched_barrier: the
         // scheduler would otherwise sink the loads below the MFMAs, next to
         // their consumers.)
-        b_load();
+        if constexpr (BC) {
+            bc_sg_load();              // the next stage's signs (its rank is known now)
+            bc_bm_load(st + 2, par);   // the bitmap two stages ahead, into the slot just decoded
+        } else {
+            b_load();
+        }
         s_load((st >> 1) + 1);
         a_load(st + 2, par);
         __builtin_amdgcn_sched_barrier(0);
@@ -503,6 +590,39 @@ k_splitk_reduce(const float *__restrict__ part, int splits, void *__restrict__ C
     });
 }
 
+// The M-tiled BITCOS GEMM (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:279-368)
+// without a re-pack: the prefill engine's tiles decode the BITCOS weights
+// themselves (gemm_tile BC).  The table maps (presence nibble m, next four sign
+// bits s) to the nibble's four 2-bit int2 codes (0 / 1 / 3 = 0 / +1 / -1):
+// row j present takes the next sign bit, 1 = -1.
+template <class Cfg, bool BF16>
+__global__ void __launch_bounds__(Cfg::THREADS)
+k_bitcos_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc, const uint16_t *__restrict__ S,
+              void *__restrict__ C, const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M,
+              int N, int K, int postop, int out_f32) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
+    __shared__ uint8_t lut[256];
+    for (int i = threadIdx.x; i < 256; i += Cfg::THREADS) {
+        const uint32_t m = (uint32_t)i >> 4, sg = (uint32_t)i & 15u;
+        uint32_t taken = 0, out = 0;
+        for (int j = 0; j < 4; ++j) {
+            if (!((m >> j) & 1u)) continue;
+            out |= (((sg >> taken) & 1u) ? 3u : 1u) << (2 * j);
+            ++taken;
+        }
+        lut[i] = (uint8_t)out;
+    }
+    __syncthreads();
+    const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
+    int tm, tn;
+    if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
+    const ARows ar{A + (size_t)tm * Cfg::BM * K, nullptr, 1};
+    const int mrows = min(Cfg::BM, M - tm * Cfg::BM);
+    gemm_tile<Cfg, BF16, false, false, true>(ar, (uint32_t)((size_t)mrows * K * 2), mrows, Bc, S, C, Other, Bias,
+                                             tm * Cfg::BM, N, K, K, tn * Cfg::BN, postop, out_f32, lds, nullptr,
+                                             nullptr, lut);
+}
+
 // Grouped GEMM of the MoE prefill (int2_moe/int2_moe_prefill.cl:72-141): the
 // rows of each expert e are meta[e] .. meta[e+1]-1 of the expert-sorted order,
 // cut into tiles of moe_tile_rows() rows numbered from meta[E+1+e]; workgroup
@@ -611,7 +731,33 @@ void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, c
                        (const uint16_t *)S2_all);
 }
 
+template <class Cfg, bool BF16>
+void bitcos_gemm_launch(const void *A, const uint32_t *Bc, const void *S, void *C, const void *Other,
+                        const void *Bias, int M, int N, int K, int postop, int out_f32, hipStream_t st) {
+    const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
+    hipLaunchKernelGGL((k_bitcos_gemm<Cfg, BF16>), dim3(xcd_ashare_grid(mt, nt)), dim3(Cfg::THREADS), 0, st,
+                       (const uint16_t *)A, Bc, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N, K,
+                       postop, out_f32);
+}
+
 }  // namespace
+
+// The M-tiled BITCOS GEMM decoding the weights in its tiles (no workspace);
+// tile choice as the int2 prefill GEMM's.
+ternocl_status bitcos_gemm_mt_run(int dtype, const void *A, const uint32_t *Bc, const void *S, void *C,
+                                  const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                  int out_f32, hipStream_t st) {
+    const GemmPlan p = gemm_plan(M, N);
+    const bool bf = dtype == TERNOCL_BF16;
+    if (p.wvn == 8) {
+        if (bf) bitcos_gemm_launch<TileCfg<8, 4, 1, 8>, true>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        else bitcos_gemm_launch<TileCfg<8, 4, 1, 8>, false>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    } else {
+        if (bf) bitcos_gemm_launch<TileCfg<4, 4>, true>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        else bitcos_gemm_launch<TileCfg<4, 4>, false>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    }
+    return check_launch();
+}
 
 int moe_tile_rows() { return kMoeTileRows; }
 

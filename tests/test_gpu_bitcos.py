@@ -269,7 +269,9 @@ def test_bitcos_to_int2_bit_exact(dev, orc, K, N, ls, z):
     assert np.array_equal(host_u32(dW), formats.pack_int2(codes))
 
 
-def _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32):
+def _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32, in_tile=False):
+    """The M-tiled entry: in_tile = the reference's call (no workspace, the tiles decode BITCOS),
+    else the re-pack into a workspace."""
     dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(buf), dev_dt(S, bf16), dev_dt(other, bf16)
     dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
     T.bitcos_slice_ranks(dB, dSR, K, N, ls)
@@ -279,7 +281,7 @@ def _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop
     else:
         dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
         dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
-    ws = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device="cuda")
+    ws = None if in_tile else torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device="cuda")
     T.bitcos_fp16_upcvt_gemm_mt(dA, dB, dS, dSR if ls > 1 else None, dC, dO, dBias, M, N, K, ls, ws,
                                 postop, out_f32)
     torch.cuda.synchronize()
@@ -287,33 +289,37 @@ def _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop
 
 
 MT_SHAPES = [(1, 256, 16, 1), (16, 1024, 272, 4), (64, 5376, 1024, 7), (130, 2048, 528, 8),
-             (257, 1536, 96, 6), (1024, 5376, 256, 14)]
+             (257, 1536, 96, 6), (1024, 5376, 256, 14),
+             (2048, 256, 6144, 4)]  # 16 x 12 = 192 tiles of 128 x 512: the wide tile
 
 
+@pytest.mark.parametrize("in_tile", [False, True])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("M,K,N,ls", MT_SHAPES)
-def test_bitcos_gemm_mt_parity(dev, orc, M, K, N, ls, bf16):
-    """Ragged M (1, 130, 257), the reference's M >= 64 prefill range, and the C4 K."""
+def test_bitcos_gemm_mt_parity(dev, orc, M, K, N, ls, bf16, in_tile):
+    """Ragged M (1, 130, 257), the reference's M >= 64 prefill range, the C4 K and a shape on
+    the 128 x 512 tile; both paths (the tiles decoding BITCOS, and the re-pack)."""
     import torch
     import ternocl_amd as T
-    print(f"bitcos mt M={M} K={K} N={N} ls={ls} bf16={bf16}", flush=True)
+    print(f"bitcos mt M={M} K={K} N={N} ls={ls} bf16={bf16} in_tile={in_tile}", flush=True)
     A, codes, S, other, bias_f = _bitcos_case(5000 + M + K + N, M, K, N, 0.5, bf16)
     buf = formats.bitcos_pack(codes)
-    dC = _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False)
+    dC = _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 0, False, in_tile)
     want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 0, False)
     bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
 
 
+@pytest.mark.parametrize("in_tile", [False, True])
 @pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("out_f32", [False, True])
-def test_bitcos_gemm_mt_epilogues(dev, orc, postop, out_f32):
+def test_bitcos_gemm_mt_epilogues(dev, orc, postop, out_f32, in_tile):
     import torch
     import ternocl_amd as T
     M, K, N, ls, bf16 = 96, 1024, 272, 4, True
     A, codes, S, other, bias_f = _bitcos_case(80 + postop, M, K, N, 0.3, bf16)
     buf = formats.bitcos_pack(codes)
-    dC = _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32)
+    dC = _bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, postop, out_f32, in_tile)
     want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, postop, out_f32)
     got = dC.cpu().numpy() if out_f32 else formats.dt_to_f32(host_u16(dC), bf16)
     ref = want if out_f32 else formats.dt_to_f32(want, bf16)
@@ -337,6 +343,24 @@ def test_bitcos_gemm_mt_matches_gemv_path(dev, orc):
     assert np.array_equal(a, again)
 
 
+@pytest.mark.parametrize("z", [0.0, 1.0])
+def test_bitcos_gemm_mt_in_tile_extremes(dev, orc, z):
+    """The tiles' decode with every weight non-zero (a sign bit per row, the rank crossing every
+    sign word) and with none (empty sign streams), and the same bits as the re-pack path, which
+    runs the same int2 engine on the re-packed words."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, ls, bf16 = 160, 2048, 336, 8, False
+    A, codes, S, other, bias_f = _bitcos_case(90 + int(z), M, K, N, z, bf16)
+    buf = formats.bitcos_pack(codes)
+    a = host_u16(_bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 5, False, True))
+    b = host_u16(_bitcos_mt_run(T, torch, A, buf, S, other, bias_f, M, K, N, ls, bf16, 5, False, False))
+    assert np.array_equal(a, b)
+    want = _bitcos_gold(orc, A, buf, S, other, bias_f, M, K, N, bf16, 5, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(a, bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
 def test_bitcos_gemm_mt_rejects_small_workspace(dev):
     import torch
     import ternocl_amd as T
@@ -348,5 +372,8 @@ def test_bitcos_gemm_mt_rejects_small_workspace(dev):
     small = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N) - 4, dtype=torch.uint8, device="cuda")
     with pytest.raises(T.TernoclError):
         T.bitcos_fp16_upcvt_gemm_mt(A, B, S, None, C, None, None, M, N, K, 1, small)
-    with pytest.raises(T.TernoclError):
-        T.bitcos_fp16_upcvt_gemm_mt(A, B, S, None, C, None, None, M, N, K, 1, None)
+    # no workspace: the tiles decode the (all-zero) weights themselves
+    C.fill_(1.0)
+    T.bitcos_fp16_upcvt_gemm_mt(A, B, S, None, C, None, None, M, N, K, 1, None)
+    torch.cuda.synchronize()
+    assert not C.any().item()
