@@ -151,19 +151,12 @@ __device__ __forceinline__ uint32_t q8_bits(uint32_t h, float sa) {
 
 // QA = false: A tiles come from Aq (int8, written by quant_a: the reference's
 // QMODE 0).  QA = true: from the DT activations A, quantized while staged.
-// GRP (the int8 MoE prefill's grouped GEMM, int2_moe/int2_moe_prefill_int8.cl:
-// 86-176): M = G sorted rows, SA [K/128][ldsa(G)]; expert e owns rows meta[e]
-// .. meta[e+1]-1 cut into BM-row tiles numbered from meta[E+1+e] (BM equals the
-// route's tile rows); workgroup (tile, column block) finds its expert by binary
-// search and runs the GEMM on its segment: weights B + e (K/16) N, SB + e
-// (K/128) N, and A, SA's columns, C and Other shifted to the segment's rows.
-template <class TC, bool BF16, bool QA, bool GRP = false>
+template <class TC, bool BF16, bool QA>
 __global__ void __launch_bounds__(TC::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
                  const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB,
                  void *__restrict__ C, const uint16_t *__restrict__ Other,
-                 const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32,
-                 const int *__restrict__ meta = nullptr, int E = 0) {
+                 const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
     constexpr int MB = TC::MB, CB = TC::CB, BM = TC::BM, BN = TC::BN, AP = TC::A_PER_THREAD;
     // LDS: two A tiles [BM][QA_PITCH] and two 1 / SA vectors [BM] while K runs,
     // then the epilogue's per-wave transposition blocks
@@ -172,33 +165,10 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
     float (*lds_inv)[BM] = (float (*)[BM])(lds + 2 * BM * QA_PITCH);
 
     constexpr int ES0 = QA ? 2 : 1;
-    int tm, tn, sa_off = 0;
-    const int lda = ldsa_of(M);  // (GRP: of all G rows)
-    if constexpr (GRP) {
-        const int ntn = (N + BN - 1) / BN;
-        const int tile = blockIdx.x / ntn;
-        tn = blockIdx.x - tile * ntn;
-        if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
-        int lo = 0, hi = E - 1;
-        while (lo < hi) {  // the last expert whose first tile is <= tile
-            const int mid = (lo + hi + 1) >> 1;
-            if (meta[E + 1 + mid] <= tile) lo = mid;
-            else hi = mid - 1;
-        }
-        const int e = lo, row0 = meta[e];
-        tm = tile - meta[E + 1 + e];
-        M = meta[e + 1] - row0;
-        Asrc = (const uint8_t *)Asrc + (size_t)row0 * K * ES0;
-        sa_off = row0;
-        SA += row0;
-        B += (size_t)e * (K / 16) * N;
-        SB += (size_t)e * (K / kGS) * N;
-        C = (uint8_t *)C + (size_t)row0 * N * (out_f32 ? 4 : 2);
-        if (Other) Other += (size_t)row0 * N;
-    } else {
-        const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
-        if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
-    }
+    int tm, tn;
+    const int lda = ldsa_of(M);
+    const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+    if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
     const int m0 = tm * BM, n0 = tn * BN;
     const int mrows = min(BM, M - m0);
     const int groups = K / kGS;
@@ -237,7 +207,7 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
             }
     };
     // 1 / SA of the tile's rows (thread tid < BM: row tid)
-    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - sa_off - m0) * 2));
+    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - m0) * 2));
     // QA: SA of the rows this thread stages (row clamped below mrows)
     uint32_t vsq[QA ? AP : 1], sq_raw[QA ? AP : 1];
     if constexpr (QA) {
@@ -451,8 +421,12 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
 //   * each block's dot products run from zero over the group's four k-chunks
 //     in int32 and are folded into the fp32 accumulators as in the 128 x 128
 //     engine.
-// GRP: the int8 MoE prefill's grouped GEMM, as k_int2_int8_gemm<..., GRP>
-// (workgroup (row tile, column block), its expert found by binary search).
+// GRP (the int8 MoE prefill's grouped GEMM, int2_moe/int2_moe_prefill_int8.cl:
+// 86-176): M = G sorted rows, SA [K/128][ldsa(G)]; expert e owns rows meta[e]
+// .. meta[e+1]-1 cut into BM-row tiles numbered from meta[E+1+e] (BM equals the
+// route's tile rows); workgroup (tile, column block) finds its expert by binary
+// search and runs the GEMM on its segment: weights B + e (K/16) N, SB + e
+// (K/128) N, and Aq, SA's columns, C and Other shifted to the segment's rows.
 template <int RMB_, int WVN_> struct WTile {
     static constexpr int RMB = RMB_, WVN = WVN_;
     static constexpr int THREADS = 64 * WVN;
@@ -746,50 +720,33 @@ static hipError_t int8_gemm_w_launch(int dtype, const int8_t *Aq, const void *SA
 }
 
 // The int8 MoE prefill's grouped GEMM on the expert-sorted rows: Aq [G][K]
-// int8 from quant_a (upfront: the wide-tile engine), or, Aq NULL, the DT rows
-// A quantized while staged (the 128 x 128 engine); SA [K/128][ldsa(G)].
-// Grid: an upper bound of the row tiles (each expert's ragged tail adds at
-// most one) times the column blocks.  Both engines' tiles have the route's
-// 128 rows.
-static hipError_t int8_moe_launch(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
+// int8 from quant_a, the wide-tile engine; SA [K/128][ldsa(G)].  Grid: an
+// upper bound of the row tiles (each expert's ragged tail adds at most one)
+// times the column blocks.  Its tiles have the route's 128 rows.
+static hipError_t int8_moe_launch(int dtype, const int *meta, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G,
                                   int N, int K, int postop, int out_f32, hipStream_t st) {
     const bool bf = dtype == TERNOCL_BF16;
     const uint16_t *sa = (const uint16_t *)SA, *sb = (const uint16_t *)SB, *oth = (const uint16_t *)Other;
-    if (Aq) {
-        typedef WideTile TC;
-        const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
-        const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
-        if (bf)
-            hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
-                               nullptr, G, N, K, postop, out_f32, meta, E);
-        else
-            hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
-                               nullptr, G, N, K, postop, out_f32, meta, E);
-    } else {
-        typedef QTile<4, 4, 2, 2> TC;
-        const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
-        const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
-        if (bf)
-            hipLaunchKernelGGL((k_int2_int8_gemm<TC, true, true, true>), grid, block, 0, st, A, sa, B, sb, C, oth,
-                               nullptr, G, N, K, postop, out_f32, meta, E);
-        else
-            hipLaunchKernelGGL((k_int2_int8_gemm<TC, false, true, true>), grid, block, 0, st, A, sa, B, sb, C, oth,
-                               nullptr, G, N, K, postop, out_f32, meta, E);
-    }
+    typedef WideTile TC;
+    const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
+    const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
+    if (bf)
+        hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
+                           nullptr, G, N, K, postop, out_f32, meta, E);
+    else
+        hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
+                           nullptr, G, N, K, postop, out_f32, meta, E);
     return hipGetLastError();
 }
 
-ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
-                                 const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G, int N,
-                                 int K, int postop, int out_f32, hipStream_t st) {
-    return launch_status(int8_moe_launch(dtype, meta, A, Aq, SA, B, SB, C, Other, E, G, N, K, postop, out_f32, st));
+ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const int8_t *Aq, const void *SA, const uint32_t *B,
+                                 const void *SB, void *C, const void *Other, int E, int G, int N, int K, int postop,
+                                 int out_f32, hipStream_t st) {
+    return launch_status(int8_moe_launch(dtype, meta, Aq, SA, B, SB, C, Other, E, G, N, K, postop, out_f32, st));
 }
 
-int int8_moe_tile_rows() {
-    static_assert(QTile<4, 4, 2, 2>::BM == WideTile::BM, "both grouped engines tile the route's rows");
-    return WideTile::BM;
-}
+int int8_moe_tile_rows() { return WideTile::BM; }
 
 // Tile planner: the 128 x 512 wide tile whenever it yields at least 192 tiles
 // (three quarters of the 256 CUs, one workgroup each); else 128 x 128 tiles

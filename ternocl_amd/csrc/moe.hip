@@ -283,9 +283,9 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
 // (int2_int8.hip)
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
                            const int *perm = nullptr, int topk = 1, const int *nrows = nullptr);
-ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const void *A, const int8_t *Aq, const void *SA,
-                                 const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G, int N,
-                                 int K, int postop, int out_f32, hipStream_t st);
+ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const int8_t *Aq, const void *SA, const uint32_t *B,
+                                 const void *SB, void *C, const void *Other, int E, int G, int N, int K, int postop,
+                                 int out_f32, hipStream_t st);
 
 // Workspace: meta | perm | inv | SA1 [H/128][ldsa(G)] | U DT [G][I] |
 // Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [G][H] | Hq int8
@@ -327,12 +327,12 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
     ternocl_status s;
     if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
     if ((s = quant_a_run(dtype, X, SA1, Xq, G, H, st, perm, topk, meta + E)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK)
+    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK)
         return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK)
+    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK)
         return s;
     if ((s = quant_a_run(dtype, Hs, SA2, Hq, G, I, st, nullptr, 1, meta + E)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, nullptr, Hq, SA2, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK)
+    if ((s = int8_moe_gemm_run(dtype, meta, Hq, SA2, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK)
         return s;
     return moe_combine_run(dtype, Y, inv, RW, O, T, topk, H, st);
 }
