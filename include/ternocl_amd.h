@@ -169,6 +169,18 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
                                       const uint32_t *B, const void *SB, void *C,
                                       const void *Other, const void *Bias, int M, int N, int K,
                                       int postop, int out_f32, void *stream);
+/* The same call with device scratch (no reference counterpart: the
+ * reference's int2_int8_gemm_mt takes none).  Upfront mode (Aq) on shapes
+ * whose 128 x 512 tiles would leave CUs idle (M = 1024, K = 14336, N = 4096)
+ * runs those tiles over 2, 4 or 8 K slices into fp32 partials there, then a
+ * reduction adds the slices in order and applies the epilogue: the same bits
+ * on every run.  ws: ternocl_int2_int8_gemm_ws_bytes(M, N, K) bytes (0: none
+ * used), 16-byte aligned; NULL or short: the call above. */
+size_t ternocl_int2_int8_gemm_ws_bytes(int M, int N, int K);
+ternocl_status ternocl_int2_int8_gemm_ws(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                         const uint32_t *B, const void *SB, void *C, const void *Other,
+                                         const void *Bias, int M, int N, int K, int postop, int out_f32, void *ws,
+                                         size_t ws_bytes, void *stream);
 
 /* Bit-exact test hook of the s8 x s2 GEMM's B decode: D[word][i] (4 dwords per
  * B word, [K/16][N][4] uint32), byte b of dword i = int8 value of row 4b + i

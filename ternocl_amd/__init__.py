@@ -24,7 +24,7 @@ __all__ = [
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
     "int2_gemv_decode", "int2_gemv_stream_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
     "int2_pack", "int2_unpack", "bitcos_pack", "bitcos_unpack", "bitcos_slice_ranks_host",
-    "ldsa", "quant_a", "int2_int8_gemm", "int2_s8_decode",
+    "ldsa", "quant_a", "int2_int8_gemm", "int2_int8_gemm_ws_bytes", "int2_s8_decode",
     "bitcos_fp16_upcvt_gemm", "bitcos_gemv_ws_bytes", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
     "moe_tile_rows", "int2_moe_route", "int2_moe_gather", "int2_moe_gemm", "int2_moe_combine",
@@ -233,15 +233,21 @@ def quant_a(A, SA, Aq, M: int, K: int, stream=None) -> None:
     _check(lib().ternocl_quant_a(_dtype_of(A), _ptr(A), _ptr(SA), _ptr(Aq), M, K, _stream(stream)))
 
 
+def int2_int8_gemm_ws_bytes(M: int, N: int, K: int) -> int:
+    """Scratch bytes of int2_int8_gemm's K-split path (0: none used)."""
+    return lib().ternocl_int2_int8_gemm_ws_bytes(M, N, K)
+
+
 def int2_int8_gemm(A, Aq, SA, B, SB, C, Other, Bias, M: int, N: int, K: int, postop: int = 0,
-                   out_f32: bool = False, stream=None) -> None:
+                   out_f32: bool = False, ws=None, stream=None) -> None:
     """int2_int8_gemm_mt(A, Aq, SA, B, SB, C, Other, Bias, M, N, K) of int2_int8_dpas.cl:316.
     With Aq given: upfront quantization (QMODE 0; A is not read and may be None).  With
     Aq=None: A's tiles are quantized while staged (QMODE 1), bit-identical q.  The dtype
-    comes from SB."""
-    _check(lib().ternocl_int2_int8_gemm(_dtype_of(SB), _ptr(A), _ptr(Aq), _ptr(SA), _ptr(B), _ptr(SB),
-                                        _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
-                                        int(bool(out_f32)), _stream(stream)))
+    comes from SB.  ``ws`` (int2_int8_gemm_ws_bytes): the deterministic K split where the
+    wide tiles alone leave CUs idle."""
+    _check(lib().ternocl_int2_int8_gemm_ws(_dtype_of(SB), _ptr(A), _ptr(Aq), _ptr(SA), _ptr(B), _ptr(SB),
+                                           _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                           int(bool(out_f32)), _ptr(ws), _nbytes(ws), _stream(stream)))
 
 
 def int2_s8_decode(B, D, K: int, N: int, stream=None) -> None:

@@ -34,6 +34,8 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_ldsa": (I, [I]),
     "ternocl_quant_a": (I, [I, P, P, P, I, I, P]),
     "ternocl_int2_int8_gemm": (I, [I, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
+    "ternocl_int2_int8_gemm_ws": (I, [I, P, P, P, P, P, P, P, P, I, I, I, I, I, P, Z, P]),
+    "ternocl_int2_int8_gemm_ws_bytes": (Z, [I, I, I]),
     "ternocl_int2_s8_decode": (I, [P, P, I, I, P]),
     "ternocl_bitcos_fp16_upcvt_gemm": (I, [I, P, P, P, P, I, P, P, P, I, I, I, I, I, P]),
     "ternocl_bitcos_fp16_upcvt_gemm_ws": (I, [I, P, P, P, P, I, P, P, P, I, I, I, I, I, P, Z, P]),

@@ -66,7 +66,7 @@ ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M
 ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
-                                  hipStream_t st);
+                                  hipStream_t st, void *ws = nullptr, size_t ws_bytes = 0);
 ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (bitcos.hip)
 int bitcos_max_ls();
@@ -271,10 +271,10 @@ ternocl_status ternocl_quant_a(int dtype, const void *A, void *SA, int8_t *Aq, i
     return quant_a_run(dtype, A, SA, Aq, M, K, (hipStream_t)stream);
 }
 
-ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq, const void *SA,
-                                      const uint32_t *B, const void *SB, void *C,
-                                      const void *Other, const void *Bias, int M, int N, int K,
-                                      int postop, int out_f32, void *stream) {
+ternocl_status ternocl_int2_int8_gemm_ws(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                         const uint32_t *B, const void *SB, void *C, const void *Other,
+                                         const void *Bias, int M, int N, int K, int postop, int out_f32, void *ws,
+                                         size_t ws_bytes, void *stream) {
     if (!Aq && !A) FAIL(TERNOCL_ERR_INVALID_ARG, "Aq (upfront quantization) or A (in-GEMM quantization) must be non-null");
     ternocl_status s = check_gemm_common(dtype, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
@@ -282,7 +282,20 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
         return int2_int8_gemv_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
                                   (hipStream_t)stream);
     return int2_int8_gemm_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
-                              (hipStream_t)stream);
+                              (hipStream_t)stream, ws, ws_bytes);
+}
+
+ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq, const void *SA,
+                                      const uint32_t *B, const void *SB, void *C,
+                                      const void *Other, const void *Bias, int M, int N, int K,
+                                      int postop, int out_f32, void *stream) {
+    return ternocl_int2_int8_gemm_ws(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, nullptr, 0,
+                                     stream);
+}
+
+size_t ternocl_int2_int8_gemm_ws_bytes(int M, int N, int K) {
+    if (M <= 4 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;  // (M <= 4: the GEMV)
+    return int2_gemm_ws_need(M, N, K);
 }
 
 ternocl_status ternocl_int2_s8_decode(const uint32_t *B, uint32_t *D, int K, int N, void *stream) {

@@ -833,6 +833,20 @@ int gemm_splits(int M, int N, int K) {
     return 1;
 }
 
+// The split-K reduction: C = ct(epi(sum of the slices in order)) (also the
+// int8 GEMM's, int2_int8.hip).
+hipError_t splitk_reduce_launch(int dtype, const float *part, int splits, void *C, const void *Other,
+                                const void *Bias, int M, int N, int postop, int out_f32, hipStream_t st) {
+    const unsigned blocks = (unsigned)(((size_t)M * N / 4 + 255) / 256);
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(blocks), dim3(256), 0, st, part, splits, C,
+                           (const uint16_t *)Other, Bias, M, N, postop, out_f32);
+    else
+        hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(blocks), dim3(256), 0, st, part, splits, C,
+                           (const uint16_t *)Other, Bias, M, N, postop, out_f32);
+    return hipGetLastError();
+}
+
 // Workspace of the split-K path: the fp32 partial tiles of every slice.
 size_t int2_gemm_ws_need(int M, int N, int K) {
     const int s = gemm_splits(M, N, K);
@@ -859,13 +873,7 @@ ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, c
         else
             hipLaunchKernelGGL((k_int2_gemm<Cfg, false>), grid, dim3(Cfg::THREADS), 0, st, (const uint16_t *)A, B,
                                (const uint16_t *)S, C, nullptr, nullptr, M, N, K, 0, 1, splits, part);
-        const unsigned blocks = (unsigned)(((size_t)M * N / 4 + 255) / 256);
-        if (bf)
-            hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(blocks), dim3(256), 0, st, part, splits, C,
-                               (const uint16_t *)Other, Bias, M, N, postop, out_f32);
-        else
-            hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(blocks), dim3(256), 0, st, part, splits, C,
-                               (const uint16_t *)Other, Bias, M, N, postop, out_f32);
+        splitk_reduce_launch(dtype, part, splits, C, Other, Bias, M, N, postop, out_f32, st);
         return check_launch();
     }
     const GemmPlan p = gemm_plan(M, N);

@@ -41,6 +41,10 @@
 #include <cfloat>
 
 namespace tcl {
+// (int2_gemm_mfma.hip: the split-K slice count and reduction of the prefill GEMM)
+int gemm_splits(int M, int N, int K);
+hipError_t splitk_reduce_launch(int dtype, const float *part, int splits, void *C, const void *Other,
+                                const void *Bias, int M, int N, int postop, int out_f32, hipStream_t st);
 namespace {
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -455,7 +459,8 @@ __global__ void __launch_bounds__(TC::THREADS) __attribute__((amdgpu_waves_per_e
 k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
                    const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB, void *__restrict__ C,
                    const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N, int K,
-                   int postop, int out_f32, const int *__restrict__ meta = nullptr, int E = 0) {
+                   int postop, int out_f32, const int *__restrict__ meta = nullptr, int E = 0, int splits = 1,
+                   float *part = nullptr) {
     constexpr int RMB = TC::RMB, BM = TC::BM, BN = TC::BN, AP = TC::AP, TH = TC::THREADS;
     __shared__ __attribute__((aligned(16))) uint8_t lds[TC::LDS_BYTES];
     int tm, tn, sa_off = 0;
@@ -482,12 +487,31 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         SB += (size_t)e * (K / kGS) * N;
         C = (uint8_t *)C + (size_t)row0 * N * (out_f32 ? 4 : 2);
         if (Other) Other += (size_t)row0 * N;
-    } else {
+    }
+    // splits > 1 (deterministic split-K, the dense mode): workgroup (tile,
+    // slice sl) runs groups [sl gs, (sl + 1) gs) and stores its fp32 tile into
+    // part + sl M N with no epilogue; a reduction kernel adds the slices in
+    // order.  (slice values kept in scalar registers: the buffer descriptors
+    // built from them stay scalar)
+    int g0 = 0, groups = K / kGS;
+    if constexpr (!GRP) {
         const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
-        if (!xcd_tile_ashare(blockIdx.x, mt, nt, tm, tn)) return;  // whole workgroup: padding
+        int tns;
+        if (!xcd_tile_ashare(blockIdx.x, mt, nt * splits, tm, tns)) return;  // whole workgroup: padding
+        tn = __builtin_amdgcn_readfirstlane(tns / splits);
+        const int sl = __builtin_amdgcn_readfirstlane(tns - tn * splits);
+        groups = __builtin_amdgcn_readfirstlane(groups / splits);
+        g0 = sl * groups;
+        if (splits > 1) {
+            C = part + (size_t)sl * M * N;
+            Other = nullptr;
+            Bias = nullptr;
+            postop = 0;
+            out_f32 = 1;
+        }
     }
     const int m0 = tm * BM, n0 = tn * BN;
-    const int mrows = min(BM, M - m0), groups = K / kGS;
+    const int mrows = min(BM, M - m0);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c32 = lane & 31, h = lane >> 5;
@@ -505,7 +529,7 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     }
     uint4 av[AP];
     auto a_load = [&](int g) __attribute__((always_inline)) {
-        const int gc = g < groups ? g : groups - 1;
+        const int gc = g0 + (g < groups ? g : groups - 1);
 #pragma unroll
         for (int u = 0; u < AP; ++u) {
             const i32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rA, va[u], gc * kGS, 0);
@@ -515,12 +539,12 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     // 1 / SA of the tile's rows: threads t, t + BM, ... stage row t % BM (rows
     // past mrows load row mrows - 1, as the last group's row m0 + srow may lie
     // past SA's end and the SGPR offset is not range-checked, and store 0)
-    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)groups * lda - sa_off - m0) * 2));
+    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)(K / kGS) * lda - sa_off - m0) * 2));
     const int srow = tid & (BM - 1);
     const uint32_t vsa = (uint32_t)min(srow, mrows - 1) * 2;
     uint32_t sa_raw = 0;
     auto sa_load = [&](int g) __attribute__((always_inline)) {
-        const int gc = g < groups ? g : groups - 1;
+        const int gc = g0 + (g < groups ? g : groups - 1);
         sa_raw = __builtin_amdgcn_raw_buffer_load_b16(rSA, vsa, gc * lda * 2, 0);
     };
     auto a_store = [&](int buf) __attribute__((always_inline)) {
@@ -542,8 +566,11 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     // a group per load, so the loads past the last group (and a block past N
     // in the last word row) return 0; a block past N elsewhere reads the next
     // row's words, in range, feeding outputs that are not stored.
-    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + n0, (uint32_t)(((size_t)(K / 16) * N - n0) * 4));
-    const __amdgpu_buffer_rsrc_t rSB = buf_rsrc(SB + n0, (uint32_t)(((size_t)groups * N - n0) * 2));
+    // (a slice's loads past its last group read the next slice's words, in
+    // range, or past the weights' end 0; never used)
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + (size_t)g0 * 8 * N + n0,
+                                               (uint32_t)(((size_t)(K / 16 - 8 * g0) * N - n0) * 4));
+    const __amdgpu_buffer_rsrc_t rSB = buf_rsrc(SB + (size_t)g0 * N + n0, (uint32_t)(((size_t)(K / kGS - g0) * N - n0) * 2));
     uint32_t vb[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) vb[kc] = (uint32_t)(((2 * kc + h) * N + wn + c32) * 4);
@@ -701,22 +728,26 @@ static hipError_t int8_gemm_launch(int dtype, const void *Asrc, const void *SA, 
     return hipGetLastError();
 }
 
-// The wide-tile engine (QMODE 0: int8 Aq from quant_a).
+// The wide-tile engine (QMODE 0: int8 Aq from quant_a); splits > 1: K slices
+// into part (fp32 [splits][M][N]), then the in-order reduction.
 static hipError_t int8_gemm_w_launch(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
                                      const void *SB, void *C, const void *Other, const void *Bias, int M, int N,
-                                     int K, int postop, int out_f32, hipStream_t st) {
+                                     int K, int postop, int out_f32, hipStream_t st, int splits = 1,
+                                     float *part = nullptr) {
     typedef WideTile TC;
     const int mt = (M + TC::BM - 1) / TC::BM, nt = (N + TC::BN - 1) / TC::BN;
-    const dim3 grid(xcd_ashare_grid(mt, nt)), block(TC::THREADS);
+    const dim3 grid(xcd_ashare_grid(mt, nt * splits)), block(TC::THREADS);
     if (dtype == TERNOCL_BF16)
         hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
                            (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32,
-                           nullptr, 0);
+                           nullptr, 0, splits, part);
     else
         hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false>), grid, block, 0, st, Aq, (const uint16_t *)SA, B,
                            (const uint16_t *)SB, C, (const uint16_t *)Other, Bias, M, N, K, postop, out_f32,
-                           nullptr, 0);
-    return hipGetLastError();
+                           nullptr, 0, splits, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    return splitk_reduce_launch(dtype, part, splits, C, Other, Bias, M, N, postop, out_f32, st);
 }
 
 // The int8 MoE prefill's grouped GEMM on the expert-sorted rows: Aq [G][K]
@@ -757,13 +788,19 @@ int int8_moe_tile_rows() { return WideTile::BM; }
 ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
-                                  hipStream_t st) {
+                                  hipStream_t st, void *ws, size_t ws_bytes) {
     typedef QTile<4, 4, 2, 2> Tile;
     const size_t es = Aq ? 1 : 2;
     if ((size_t)M * K * es >= (1u << 31) || (size_t)(K / 16) * N * 4 >= (1u << 31)) {
         set_error("int2_int8_gemm: the A operand and B must each be below 2^31 bytes");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
+    // the wide tile over K slices where its tiles alone leave CUs idle and the
+    // caller gives the partials' workspace (the fp16 prefill GEMM's rule)
+    const int splits = Aq ? gemm_splits(M, N, K) : 1;
+    if (splits > 1 && ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= (size_t)splits * M * N * 4)
+        return launch_status(int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st,
+                                                splits, (float *)ws));
     const bool wide = Aq && (size_t)((M + WideTile::BM - 1) / WideTile::BM) * ((N + WideTile::BN - 1) / WideTile::BN) >= 192;
     const hipError_t e =
         wide  ? int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)

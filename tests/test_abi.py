@@ -88,6 +88,14 @@ def test_ws_bytes_query():
     assert T.int2_gemm_ws_bytes(256, 1024, 1024) == 0
 
 
+def test_int8_ws_bytes_query():
+    """The s8 x s2 GEMM's K split: the fp16 prefill GEMM's slices and partials; none for the GEMV."""
+    import ternocl_amd as T
+    assert T.int2_int8_gemm_ws_bytes(1024, 4096, 14336) == 4 * 1024 * 4096 * 4
+    assert T.int2_int8_gemm_ws_bytes(1024, 14336, 4096) == 0  # 224 wide tiles
+    assert T.int2_int8_gemm_ws_bytes(4, 4096, 14336) == 0  # the decode GEMV
+
+
 def test_bitcos_ws_bytes_query():
     """The split BITCOS launch: a counter per 64-column strip (256-byte block) and
     fp32 sums [slices][4][N]; none where one workgroup per strip fills the chip."""

@@ -90,18 +90,40 @@ def _upcvt_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
     return _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
 
 
-def _int8_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
+def _int8_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0, split=False):
+    """split: with the K-split workspace -- the same bits on a second call, and within the rule
+    of the call without it."""
     import torch
     import ternocl_amd as T
-    print(f"int8 M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32}", flush=True)
+    print(f"int8 M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32} split={split}", flush=True)
     A, B, SB, other, bias_f = _inputs(seed + 50000 + M + K + N, M, K, N, bf16)
     dA = dev_dt(A, bf16)
     dSA = torch.zeros((K // 128, T.ldsa(M)), dtype=dA.dtype, device="cuda")
     dAq = torch.zeros((M, K), dtype=torch.int8, device="cuda")
     dO, dBias, dC = _device_io(torch, SB, other, bias_f, M, N, bf16, out_f32)
     T.quant_a(dA, dSA, dAq, M, K)
-    T.int2_int8_gemm(None, dAq, dSA, dev_raw(B), dev_dt(SB, bf16), dC, dO, dBias, M, N, K, postop, out_f32)
+    dB, dSB = dev_raw(B), dev_dt(SB, bf16)
+    ws = None
+    if split:
+        need = T.int2_int8_gemm_ws_bytes(M, N, K)
+        assert need > 0, "this shape should split"
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
     torch.cuda.synchronize()
+    if split:
+        first = dC.clone()
+        T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(first, dC), "split-K results differ between runs"
+        _, _, dC2 = _device_io(torch, SB, other, bias_f, M, N, bf16, out_f32)
+        T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC2, dO, dBias, M, N, K, postop, out_f32)
+        torch.cuda.synchronize()
+        if out_f32:
+            a, b = host_f32(dC), host_f32(dC2)
+        else:
+            a, b = formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(host_u16(dC2), bf16)
+        bad_nows, _ = allclose_report(a, b)
+        assert bad_nows == 0, f"{bad_nows} elements differ from the unsplit GEMM beyond the rule"
     rows = sample_rows(M)
     Ar = np.ascontiguousarray(A[rows])
     SA = orc.scale_a(Ar, rows.size, K, bf16)
@@ -189,6 +211,23 @@ def test_splitk_parity(dev, orc, M, K, N, bf16):
     bad, dmax, bad_nows = _splitk_case(dev, orc, M, K, N, bf16)
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
     assert bad_nows == 0, f"{bad_nows} elements differ from the unsplit GEMM beyond the rule"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", SPLITK_SHAPES)
+def test_int8_splitk_parity(dev, orc, M, K, N, bf16):
+    """The s8 x s2 GEMM's K split (ternocl_int2_int8_gemm_ws) on the same shapes."""
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16, split=True)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_int8_splitk_epilogues(dev, orc, bf16, postop, out_f32):
+    M, K, N = SPLITK_SHAPES[-1]
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop, split=True)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
 @pytest.mark.parametrize("bf16", [False, True])
