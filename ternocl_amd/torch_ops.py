@@ -135,7 +135,9 @@ def int2_int8_gemm(Aq: torch.Tensor, SA: torch.Tensor, B: torch.Tensor, SB: torc
     M, K = Aq.shape
     N = B.shape[1]
     C = torch.empty((M, N), dtype=_out_dtype(SB, out_f32), device=Aq.device)
-    T.int2_int8_gemm(None, Aq, SA, B, SB, C, other, bias, M, N, K, postop, out_f32)
+    wsb = T.int2_int8_gemm_ws_bytes(M, N, K)  # the K split's partials, where it splits
+    ws = torch.empty(wsb, dtype=torch.uint8, device=Aq.device) if wsb else None
+    T.int2_int8_gemm(None, Aq, SA, B, SB, C, other, bias, M, N, K, postop, out_f32, ws=ws)
     return C
 
 
