@@ -595,17 +595,19 @@ def bench_c7(torch, T, synth, formats, orc):
         dAq = torch.empty((M, K), dtype=torch.int8, device="cuda")
         dC = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         T.quant_a(dA, dSA, dAq, M, K)
+        wsb = T.int2_int8_gemm_ws_bytes(M, N, K)  # the K split's strip counters and slice sums
+        ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda") if wsb else None
         it = [0]
 
         def upfront():
             b, sb = W[it[0] % sets]
             it[0] += 1
-            T.int2_int8_gemm(None, dAq, dSA, b, sb, dC, None, None, M, N, K)
+            T.int2_int8_gemm(None, dAq, dSA, b, sb, dC, None, None, M, N, K, ws=ws)
 
         def in_gemv():
             b, sb = W[it[0] % sets]
             it[0] += 1
-            T.int2_int8_gemm(dA, None, dSA, b, sb, dC, None, None, M, N, K)
+            T.int2_int8_gemm(dA, None, dSA, b, sb, dC, None, None, M, N, K, ws=ws)
         upfront()
         torch.cuda.synchronize()
         want = orc.int8_gold(A, B, orc.scale_a(A, M, K, bf16), SB, M, K, N, bf16)
@@ -619,7 +621,7 @@ def bench_c7(torch, T, synth, formats, orc):
         out[f"m1_k{K}_n{N}"] = {"gemv_us": round(u_us, 2), "gemv_GB/s": round(nbytes / u_us / 1e3, 1),
                                 "hbm_frac": round(nbytes / u_us / 1e3 / HBM_PEAK_GBS, 4),
                                 "in_gemv_quant_us": round(i_us, 2), "quant_a_scales_only_us": round(q_us, 2),
-                                "parity_bad": bad, "layers_rotated": sets}
+                                "ws_bytes": wsb, "parity_bad": bad, "layers_rotated": sets}
     return out
 
 

@@ -170,12 +170,17 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
                                       const void *Other, const void *Bias, int M, int N, int K,
                                       int postop, int out_f32, void *stream);
 /* The same call with device scratch (no reference counterpart: the
- * reference's int2_int8_gemm_mt takes none).  Upfront mode (Aq) on shapes
- * whose 128 x 512 tiles would leave CUs idle (M = 1024, K = 14336, N = 4096)
- * runs those tiles over 2, 4 or 8 K slices into fp32 partials there, then a
- * reduction adds the slices in order and applies the epilogue: the same bits
- * on every run.  ws: ternocl_int2_int8_gemm_ws_bytes(M, N, K) bytes (0: none
- * used), 16-byte aligned; NULL or short: the call above. */
+ * reference's int2_int8_gemm_mt and int2_int8_gemv take none).  Upfront mode
+ * (Aq) on shapes whose 128 x 512 tiles would leave CUs idle (M = 1024,
+ * K = 14336, N = 4096) runs those tiles over 2, 4 or 8 K slices into fp32
+ * partials there, then a reduction adds the slices in order and applies the
+ * epilogue.  The decode GEMV (M <= 4, both modes) splits long K (>= 8192)
+ * over narrow N (< 6144 columns) the same way, a counter per 16-column strip
+ * electing the workgroup that adds the slices in order.  Either way the same
+ * bits on every run.  ws: ternocl_int2_int8_gemm_ws_bytes(M, N, K) bytes (0:
+ * none used), 16-byte aligned, zeroed once before its first use (the GEMV's
+ * counters return to zero by themselves; calls that share ws must not
+ * overlap); NULL or short: the call above. */
 size_t ternocl_int2_int8_gemm_ws_bytes(int M, int N, int K);
 ternocl_status ternocl_int2_int8_gemm_ws(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                          const uint32_t *B, const void *SB, void *C, const void *Other,

@@ -243,8 +243,8 @@ def int2_int8_gemm(A, Aq, SA, B, SB, C, Other, Bias, M: int, N: int, K: int, pos
     """int2_int8_gemm_mt(A, Aq, SA, B, SB, C, Other, Bias, M, N, K) of int2_int8_dpas.cl:316.
     With Aq given: upfront quantization (QMODE 0; A is not read and may be None).  With
     Aq=None: A's tiles are quantized while staged (QMODE 1), bit-identical q.  The dtype
-    comes from SB.  ``ws`` (int2_int8_gemm_ws_bytes): the deterministic K split where the
-    wide tiles alone leave CUs idle."""
+    comes from SB.  ``ws`` (int2_int8_gemm_ws_bytes, zeroed once): the deterministic K split
+    where the wide tiles (or, at M <= 4, the GEMV's strips) alone leave CUs idle."""
     _check(lib().ternocl_int2_int8_gemm_ws(_dtype_of(SB), _ptr(A), _ptr(Aq), _ptr(SA), _ptr(B), _ptr(SB),
                                            _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
                                            int(bool(out_f32)), _ptr(ws), _nbytes(ws), _stream(stream)))

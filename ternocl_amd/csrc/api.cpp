@@ -44,7 +44,8 @@ bool int2_int8_gemv_supports(int M, int N, int K, const void *A, const int8_t *A
 ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
-                                  hipStream_t st);
+                                  hipStream_t st, void *ws, size_t ws_bytes);
+size_t int2_int8_gemv_ws_need(int M, int N, int K);
 ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                 const void *Other, const void *Bias, int M, int N, int K, int postop,
                                 int out_f32, int waves, int cpl, int gpw, int ks, void *ws, size_t ws_bytes,
@@ -280,7 +281,7 @@ ternocl_status ternocl_int2_int8_gemm_ws(int dtype, const void *A, const int8_t 
     if (s != TERNOCL_OK) return s;
     if (int2_int8_gemv_supports(M, N, K, A, Aq))  // decode: the fp8 x fp4 block-scaled GEMV
         return int2_int8_gemv_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
-                                  (hipStream_t)stream);
+                                  (hipStream_t)stream, ws, ws_bytes);
     return int2_int8_gemm_run(dtype, A, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32,
                               (hipStream_t)stream, ws, ws_bytes);
 }
@@ -294,7 +295,8 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
 }
 
 size_t ternocl_int2_int8_gemm_ws_bytes(int M, int N, int K) {
-    if (M <= 4 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;  // (M <= 4: the GEMV)
+    if (M < 1 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    if (M <= 4) return int2_int8_gemv_ws_need(M, N, K);  // the decode GEMV's K split
     return int2_gemm_ws_need(M, N, K);
 }
 

@@ -873,8 +873,8 @@ ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, c
         else
             hipLaunchKernelGGL((k_int2_gemm<Cfg, false>), grid, dim3(Cfg::THREADS), 0, st, (const uint16_t *)A, B,
                                (const uint16_t *)S, C, nullptr, nullptr, M, N, K, 0, 1, splits, part);
-        splitk_reduce_launch(dtype, part, splits, C, Other, Bias, M, N, postop, out_f32, st);
-        return check_launch();
+        // (an error of the slices' launch stays pending for the reduction's check)
+        return launch_status(splitk_reduce_launch(dtype, part, splits, C, Other, Bias, M, N, postop, out_f32, st));
     }
     const GemmPlan p = gemm_plan(M, N);
     if (bf) gemm_dispatch<true>(p, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);

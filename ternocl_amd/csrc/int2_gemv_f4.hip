@@ -402,7 +402,7 @@ struct F4Group {
 // [ldsa] the activation scales, A int8 (QM 1) or DT quantized while staged (QM
 // 2); per group and column acc += float(dot) * (SB * (1 / SA)), the int32 dot
 // exact (piece rows 4m, 4m + 1 sum to 2 dot).
-// ksn > 1 (the plain DT GEMV, grid.y = ksn): K slice blockIdx.y; part fp32
+// ksn > 1 (the plain GEMV, DT or int8, grid.y = ksn): K slice blockIdx.y; part fp32
 // [ksn][M][N] slice sums, cnt one zero-initialised counter per strip (left at
 // zero again).
 template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0, bool DS = false>
@@ -423,12 +423,15 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int c = lane & 15, q = lane >> 4;
     int groups = K / kGS;
     int ks = 0;
-    if constexpr (QM == 0 && !GRP && !DS) {
+    constexpr bool SPLIT = (QM == 0 || QM == 1 || QM == 2) && !GRP && !DS;
+    if constexpr (SPLIT) {
         if (ksn > 1) {  // slice ks: groups [ks gps, ks gps + gps) (the host keeps every slice non-empty)
             ks = blockIdx.y;
             const int gps = (groups + ksn - 1) / ksn, g_lo = ks * gps;
             groups = min(gps, groups - g_lo);
-            A += (size_t)g_lo * kGS;
+            if constexpr (QM == 1) A = (const uint16_t *)((const int8_t *)A + (size_t)g_lo * kGS);  // int8 rows
+            else A += (size_t)g_lo * kGS;
+            if constexpr (I8) SA += (size_t)g_lo * ldsa;
             B += (size_t)g_lo * 8 * N;
             S += (size_t)g_lo * N;
         }
@@ -616,7 +619,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 for (int h = 0; h < OPL; ++h) out[j][h] += red[((w2 - 1) * CPL + j) * JS + (q * 16 + c) * OPL + h];
     }
     if (!live) return;
-    if constexpr (QM == 0 && !GRP && !DS) {
+    if constexpr (SPLIT) {
         if (ksn > 1) {
             // This slice's sums, then the strip's counter; the last of the ksn
             // workgroups adds the slices in order.  The sums are stored and
@@ -834,9 +837,9 @@ hipError_t f4q_launch_t(const F4Plan &p, const void *A, const void *SA, int ldsa
                         int postop, int out_f32, hipStream_t st) {
     const int strips = N / (16 * CPL);
     const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
-    hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QM>), dim3(strips), dim3(64 * p.waves), p.lds,
-                       st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M, N,
-                       K, postop, out_f32, swz, F4Group{}, (const uint16_t *)SA, ldsa);
+    hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QM>), dim3(strips, p.ks), dim3(64 * p.waves),
+                       p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M,
+                       N, K, postop, out_f32, swz, F4Group{}, (const uint16_t *)SA, ldsa, p.ks, p.part, p.cnt);
     return hipGetLastError();
 }
 
@@ -869,13 +872,13 @@ hipError_t f4q_launch(const F4Plan &p, const void *A, const void *SA, int ldsa, 
     }
 }
 
-// The s8 x s2 GEMV's tile: the automatic one (<= 2 columns per lane, <= 4
-// groups per wave; 16 waves only with 1 column per lane and M = 1, which the
-// kernel's launch bounds allow).
-F4Plan f4q_plan(int M, int N, int K) {
-    F4Plan p = f4_plan(false, M, N, K, 0, 0, 0);
+// The s8 x s2 GEMV's tile: the automatic one for ks K slices (<= 2 columns
+// per lane, <= 4 groups per wave; 16 waves only with 1 column per lane and
+// M = 1, which the kernel's launch bounds allow).
+F4Plan f4q_plan(int M, int N, int K, int cpl = 0, int ks = 1) {
+    F4Plan p = f4_plan(false, M, N, K, 0, cpl, 0, ks);
     if (p.cpl > 2 || p.gpw > 4)
-        p = f4_plan(false, M, N, K, p.waves, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw);
+        p = f4_plan(false, M, N, K, p.waves, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw, ks);
     return p;
 }
 
@@ -911,20 +914,23 @@ int f4_slices(int groups, int ks) {
 }
 
 // Automatic K split (when the caller gives the workspace), from graph-timed
-// sweeps of M = 1..8 on K x N = 4096 x 14336, 14336 x 4096 and 4096 x 4096:
-// a split pays only where the unsplit plan has fewer than 384 strips (one
-// workgroup each) and K is long (>= 64 groups), or M is 5..8 (its staging
-// grows with M); about 28 groups per slice, 16-column-wide MFMA operands
-// shared by 4 columns per lane at M >= 5 (2 below).  K = 14336, N = 4096:
-// M = 1 7.9 -> 7.3 us, M = 8 23.2 -> 12.2 us; K = N = 4096, M = 8: 8.6 -> 7.1.
+// sweeps of M = 1..8 over K = 4096..16384 and N = 1024..14336: a split pays
+// only where the unsplit plan has fewer than 384 strips (one workgroup each)
+// and K is long: >= 104 groups at M = 1, >= 64 at M = 2..4, >= 16 at M = 5..8
+// (the staging grows with M).  About 28 groups per slice, at least 4 slices
+// from 64 groups on; 16-column-wide MFMA operands shared by 4 columns per
+// lane at M >= 5 (2 below).  N = 4096: K = 14336, M = 1 8.4 -> 7.6 us, M = 4
+// 14.2 -> 10.4, M = 8 23.2 -> 12.2; K = 8192, M = 4 9.2 -> 7.5; K = 4096, M = 8
+// 8.6 -> 7.1.  (M = 1, K = 8192..12288 loses: 5.8 -> 6.4 us at K = 8192.)
 void f4_auto_split(int M, int N, int K, int cpl_req, int &cpl, int &ks) {
     const int groups = K / kGS, MR = f4_mr(M);
     const int cpl_u = cpl_req > 0 ? cpl_req : ((N % 32 == 0 && N / 32 >= 384) ? 2 : 1);
     cpl = cpl_u;
     ks = 1;
-    if (N / (16 * cpl_u) >= 384 || groups < 16 || (MR < 8 && groups < 64)) return;
+    const int gmin = MR >= 8 ? 16 : MR >= 2 ? 64 : 104;
+    if (N / (16 * cpl_u) >= 384 || groups < gmin) return;
     const int c = cpl_req > 0 ? cpl_req : (MR >= 8 && groups >= 64 && N % 64 == 0 ? 4 : (N % 32 == 0 ? 2 : 1));
-    int k = 2;  // the power of two nearest groups / 28 (log scale), 2 .. 16
+    int k = groups >= 64 ? 4 : 2;  // the power of two nearest groups / 28 (log scale), 2 .. 16
     while (k < 16 && (double)groups / 28.0 > k * 1.4142) k *= 2;
     cpl = c;
     ks = f4_slices(groups, k);
@@ -1041,15 +1047,47 @@ bool int2_int8_gemv_supports(int M, int N, int K, const void *A, const int8_t *A
     return N % (16 * p.cpl) == 0 && p.lds <= kF4MaxLds;
 }
 
+// The automatic K split of the s8 x s2 GEMV: the DT GEMV's rule (M <= 4
+// keeps it to <= 2 columns per lane); 1 where it does not split.
+static int f4q_auto_split(int M, int N, int K, int &cpl) {
+    int ks;
+    f4_auto_split(M, N, K, 0, cpl, ks);
+    if (ks > 1 && (cpl > 2 || N % (16 * cpl))) {
+        cpl = 0;
+        ks = 1;
+    }
+    if (ks == 1) cpl = 0;
+    return ks;
+}
+
+size_t int2_int8_gemv_ws_need(int M, int N, int K) {
+    if (M < 1 || M > kF4MaxMI8 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    int cpl;
+    return f4_split_ws(M, N, f4q_auto_split(M, N, K, cpl));
+}
+
+// ws (16-byte aligned, int2_int8_gemv_ws_need bytes, zeroed once before its
+// first use): the automatic K split; NULL or short: one slice.
 ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
-                                  hipStream_t st) {
+                                  hipStream_t st, void *ws, size_t ws_bytes) {
     if (!int2_int8_gemv_supports(M, N, K, A, Aq)) {
         set_error("the s8 x s2 GEMV takes M <= 4, N % 16 == 0 and aligned activations");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
-    const F4Plan p = f4q_plan(M, N, K);
+    int cpl = 0, ks = f4q_auto_split(M, N, K, cpl);
+    if (ks > 1 && !(ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= f4_split_ws(M, N, ks))) {
+        ks = 1;
+        cpl = 0;
+    }
+    F4Plan p = f4q_plan(M, N, K, cpl, ks);
+    if (ks > 1 && p.lds <= kF4MaxLds) {
+        p.cnt = (uint32_t *)ws;
+        p.part = (float *)((uint8_t *)ws + f4_cnt_bytes(N));
+    } else if (ks > 1) {
+        p = f4q_plan(M, N, K);
+    }
     const int ldsa = (M + 31) & ~31;
     const bool bf16 = dtype == TERNOCL_BF16;
     hipError_t e;

@@ -168,7 +168,6 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
     uint8_t (*lds_a)[BM * QA_PITCH] = (uint8_t (*)[BM * QA_PITCH])lds;
     float (*lds_inv)[BM] = (float (*)[BM])(lds + 2 * BM * QA_PITCH);
 
-    constexpr int ES0 = QA ? 2 : 1;
     int tm, tn;
     const int lda = ldsa_of(M);
     const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;

@@ -135,8 +135,8 @@ def int2_int8_gemm(Aq: torch.Tensor, SA: torch.Tensor, B: torch.Tensor, SB: torc
     M, K = Aq.shape
     N = B.shape[1]
     C = torch.empty((M, N), dtype=_out_dtype(SB, out_f32), device=Aq.device)
-    wsb = T.int2_int8_gemm_ws_bytes(M, N, K)  # the K split's partials, where it splits
-    ws = torch.empty(wsb, dtype=torch.uint8, device=Aq.device) if wsb else None
+    wsb = T.int2_int8_gemm_ws_bytes(M, N, K)  # the K split's counters and partials, where it splits
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=Aq.device) if wsb else None
     T.int2_int8_gemm(None, Aq, SA, B, SB, C, other, bias, M, N, K, postop, out_f32, ws=ws)
     return C
 

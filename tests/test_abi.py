@@ -76,6 +76,8 @@ def test_ws_bytes_query():
     assert T.int2_gemm_ws_bytes(8, 4096, 14336) == 1024 + 4 * 8 * 4096 * 4  # 64 strips x 4 slices
     assert T.int2_gemm_ws_bytes(8, 4096, 4096) == 1024 + 2 * 8 * 4096 * 4  # 128 strips x 2 slices
     assert T.int2_gemm_ws_bytes(4, 4096, 4096) == 0  # 32 groups: unsplit below M = 5
+    assert T.int2_gemm_ws_bytes(1, 2048, 8192) == 0  # 64 groups: unsplit at M = 1
+    assert T.int2_gemm_ws_bytes(4, 2048, 8192) == 512 + 4 * 4 * 2048 * 4  # 64 groups: 4 slices at M = 4
     assert T.int2_gemm_ws_bytes(5, 14336, 4096) == 0  # 448 strips
     assert T.int2_gemm_ws_bytes(8, 4096, 512) == 0  # 4 groups: too short to slice
     assert T.int2_gemm_ws_bytes(9, 4096, 14336) == 0  # the bf16/fp16 MFMA GEMV keeps no scratch
@@ -89,11 +91,15 @@ def test_ws_bytes_query():
 
 
 def test_int8_ws_bytes_query():
-    """The s8 x s2 GEMM's K split: the fp16 prefill GEMM's slices and partials; none for the GEMV."""
+    """The s8 x s2 GEMM's K split: the fp16 prefill GEMM's slices and partials; the decode
+    GEMV's (M <= 4) counter block (a counter per 16-column strip, 256-byte rounded) and
+    fp32 slice sums where K is long and the strips are few."""
     import ternocl_amd as T
     assert T.int2_int8_gemm_ws_bytes(1024, 4096, 14336) == 4 * 1024 * 4096 * 4
     assert T.int2_int8_gemm_ws_bytes(1024, 14336, 4096) == 0  # 224 wide tiles
-    assert T.int2_int8_gemm_ws_bytes(4, 4096, 14336) == 0  # the decode GEMV
+    assert T.int2_int8_gemm_ws_bytes(4, 4096, 14336) == 1024 + 4 * 4 * 4096 * 4  # 112 groups: 4 slices
+    assert T.int2_int8_gemm_ws_bytes(1, 4096, 4096) == 0  # 32 groups
+    assert T.int2_int8_gemm_ws_bytes(1, 14336, 4096) == 0  # 448 strips of 32 columns
 
 
 def test_bitcos_ws_bytes_query():

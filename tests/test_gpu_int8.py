@@ -331,6 +331,68 @@ def test_int8_gemv_parity(dev, orc, M, K, N, bf16):
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
+# Long K over few strips: the GEMV's K split (a workspace of int2_int8_gemm_ws_bytes),
+# 16- and 32-column strips, a last slice shorter than the others (K = 8320: 65 groups).
+GEMV_SPLIT_SHAPES = [(1, 14336, 4096), (2, 14336, 4096), (3, 8320, 1040), (4, 16384, 2048), (1, 14336, 528)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", GEMV_SPLIT_SHAPES)
+def test_int8_gemv_k_slices(dev, orc, M, K, N, bf16):
+    """With the workspace: the oracle's gold within 1e-3 + 1e-2 |ref|; both quantization
+    modes bit for bit; the same bits on a second call (the counters back at zero); the call
+    without the workspace within the same rule."""
+    import torch
+    import ternocl_amd as T
+    need = T.int2_int8_gemm_ws_bytes(M, N, K)
+    print(f"int8 gemv split M={M} K={K} N={N} bf16={bf16} ws={need}", flush=True)
+    assert need > 0, "this shape should split"
+    A, B, SB, other, bias_f = _int8_case(5200 + M + N, M, K, N, bf16, ref_dist=True, all_codes=True)
+    dA, dSA, dAq = _quant(T, torch, A, M, K, bf16)
+    dB, dSB = dev_raw(B), dev_dt(SB, bf16)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for a, aq in ((None, dAq), (dA, None), (None, dAq), (None, None)):
+        C = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+        if a is None and aq is None:  # no workspace: the unsplit launch
+            T.int2_int8_gemm(None, dAq, dSA, dB, dSB, C, None, None, M, N, K, 0, False)
+        else:
+            T.int2_int8_gemm(a, aq, dSA, dB, dSB, C, None, None, M, N, K, 0, False, ws=ws)
+        torch.cuda.synchronize()
+        outs.append(host_u16(C))
+    assert np.array_equal(outs[0], outs[1]), "the two quantization modes differ"
+    assert np.array_equal(outs[0], outs[2]), "split results differ between runs"
+    assert not ws[: (N // 16) * 4].any().item(), "the strip counters did not return to zero"
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, 0, False)
+    for got in (outs[0], outs[3]):
+        bad, dmax = allclose_report(formats.dt_to_f32(got, bf16), formats.dt_to_f32(want, bf16))
+        assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_int8_gemv_split_epilogues(dev, orc, bf16, postop, out_f32):
+    """Every epilogue after the in-order slice sum (M = 3, K = 8320, N = 1040)."""
+    import torch
+    import ternocl_amd as T
+    M, K, N = 3, 8320, 1040
+    print(f"int8 gemv split epilogue postop={postop} f32={out_f32} bf16={bf16}", flush=True)
+    A, B, SB, other, bias_f = _int8_case(80 + postop, M, K, N, bf16)
+    dA, dSA, dAq = _quant(T, torch, A, M, K, bf16)
+    dB, dSB = dev_raw(B), dev_dt(SB, bf16)
+    dO = dev_dt(other, bf16)
+    dBias = torch.from_numpy(bias_f).cuda() if out_f32 else dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+    ws = torch.zeros(T.int2_int8_gemm_ws_bytes(M, N, K), dtype=torch.uint8, device="cuda")
+    C = torch.zeros((M, N), dtype=torch.float32 if out_f32 else dSB.dtype, device="cuda")
+    T.int2_int8_gemm(None, dAq, dSA, dB, dSB, C, dO, dBias, M, N, K, postop, out_f32, ws=ws)
+    torch.cuda.synchronize()
+    got = C.cpu().numpy() if out_f32 else host_u16(C)
+    want = _int8_gold(orc, A, B, SB, other, bias_f, M, K, N, bf16, postop, out_f32)
+    bad, dmax = allclose_report(_as_f32(got, out_f32, bf16), _as_f32(want, out_f32, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("out_f32", [False, True])
