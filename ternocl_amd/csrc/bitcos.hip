@@ -17,11 +17,11 @@
 // spread over ksw workgroups (grid.y), so that the launch fills the CUs evenly
 // (N = 21504: 336 strips of 14 waves leave 80 CUs with twice the work); each
 // writes its sums to the workspace and the last of a strip's workgroups (a
-// device-scope counter) adds them in order and applies the epilogue.  Per 64-row chunk a lane loads the column's two
-// bitmap words and three sign words (the chunk consumes at most 64 sign bits
-// from the column's rank onwards); loads run four chunks (bitmap) and three
-// chunks (signs, whose address needs the rank, i.e. the previous bitmap words)
-// ahead.
+// device-scope counter) adds them in order and applies the epilogue.  Per
+// 64-row chunk a lane loads the column's two bitmap words and three sign words
+// (the chunk consumes at most 64 sign bits from the column's rank onwards), in
+// blocks of up to 8 chunks: a block's bitmap words one block ahead, then its
+// ranks, then all of its sign words at once (their addresses need the ranks).
 // Decode per 32-row word: the word's sign window is funnel-shifted out of the
 // three sign words (v_alignbit); each 4-row nibble m and the next four window
 // bits s index a 256-entry LDS table of four DT codes +1 / -1 / 0 (a 4-bit
@@ -86,7 +86,7 @@ __device__ __forceinline__ void bc_decode_word(const uint2 *lut, uint32_t bm, ui
 // ksw > 1: workgroup (strip, blockIdx.y) runs slices blockIdx.y * wps ..
 // + wps - 1 (wps = waves per workgroup); wsum fp32 [ksw][MR][N] sums, cnt one
 // zero-initialised counter per strip (left at zero again).
-template <int MR, bool BF16>
+template <int MR, bool BF16, int BC>
 __global__ void __launch_bounds__(64 * kBcMaxLs)
 k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
               const uint16_t *__restrict__ S, const uint32_t *__restrict__ SR, void *__restrict__ C,
@@ -114,29 +114,22 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
 #pragma unroll
     for (int r = 0; r < MR; ++r) ar[r] = (const uint32_t *)(A + (size_t)min(m0 + r, M - 1) * K);
 
-    // Loads run ahead of the decode in a ring of kL chunk slots: bitmap words
-    // kL chunks ahead, sign words kL - 1 chunks ahead (a chunk's sign address
-    // needs the ranks of the chunks before it, i.e. their bitmap words), group
-    // scales likewise, all unconditionally (a load under a branch is waited
-    // for at once, and with it -- vmcnt counts in order -- every load issued
-    // before it).  The chunk loop is unrolled by kL so each slot is a fixed
-    // register set: copying a register whose load is in flight would wait for
-    // it.  Bitmap words of chunks past the slice read as 0, so the rank stops
-    // there and the sign loads repeat the last window (inside the stream and
-    // its pad words).
-    constexpr int kL = 4;
+    // Blocks of BC 64-row chunks.  A block's bitmap words are loaded one block
+    // ahead (the first block's with the slice rank and the stream offset);
+    // the block's ranks then follow from them at once, and all of its sign
+    // and scale loads go out together before its decode, so a slice of at
+    // most BC chunks waits on two memory round trips (bitmaps, then signs)
+    // rather than one per few chunks.  All loads are unconditional (a load
+    // under a branch is waited for at once, and with it -- vmcnt counts in
+    // order -- every load issued before it).  Bitmap words of chunks past
+    // the slice read as 0, so the rank stops there and their sign loads
+    // repeat the last window (inside the stream and its pad words).
     auto bm_load = [&](int c, uint32_t b[2]) {
         const int cc = c < chunks ? c : chunks - 1;
         const size_t kp = (size_t)((k0 >> 5) + 2 * cc);
         const uint32_t x = Bc[kp * N + nc], y = Bc[(kp + 1) * N + nc];
         b[0] = c < chunks ? x : 0u;
         b[1] = c < chunks ? y : 0u;
-    };
-    auto sg_load = [&](uint32_t r, uint32_t q[3]) {
-        const uint32_t w = r >> 5;
-        q[0] = sg[w];
-        q[1] = sg[w + 1];
-        q[2] = sg[w + 2];
     };
     const int groups = K / kGS;
     auto s_load = [&](int c) {
@@ -148,38 +141,37 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
 #pragma unroll
     for (int r = 0; r < MR; ++r) acc[r] = part[r] = 0.0f;
 
-    // slot u holds chunk c with c % kL == u
-    uint32_t bm[kL][2], q[kL][3], rs[kL], sc[kL];
+    uint32_t bm[BC][2];
 #pragma unroll
-    for (int i = 0; i < kL; ++i) bm_load(i, bm[i]);
+    for (int i = 0; i < BC; ++i) bm_load(i, bm[i]);
+    for (int b0 = 0; b0 < chunks; b0 += BC) {
+        uint32_t rs[BC], q[BC][3], sc[BC], nb[BC][2];
 #pragma unroll
-    for (int i = 0; i + 1 < kL; ++i) {
-        rs[i] = i ? rs[i - 1] + __builtin_popcount(bm[i - 1][0]) + __builtin_popcount(bm[i - 1][1]) : R;
-        sg_load(rs[i], q[i]);
-        sc[i] = s_load(i);
-    }
-    for (int c0 = 0; c0 < chunks; c0 += kL) {
+        for (int i = 0; i < BC; ++i) rs[i] = i ? rs[i - 1] + __builtin_popcount(bm[i - 1][0]) + __builtin_popcount(bm[i - 1][1]) : R;
+        R = rs[BC - 1] + __builtin_popcount(bm[BC - 1][0]) + __builtin_popcount(bm[BC - 1][1]);
 #pragma unroll
-        for (int u = 0; u < kL; ++u) {
-            const int c = c0 + u;
+        for (int i = 0; i < BC; ++i) {
+            const uint32_t w = rs[i] >> 5;
+            q[i][0] = sg[w];
+            q[i][1] = sg[w + 1];
+            q[i][2] = sg[w + 2];
+        }
+#pragma unroll
+        for (int i = 0; i < BC; ++i) sc[i] = s_load(b0 + i);
+#pragma unroll
+        for (int i = 0; i < BC; ++i) bm_load(b0 + BC + i, nb[i]);
+#pragma unroll
+        for (int u = 0; u < BC; ++u) {
+            const int c = b0 + u;
             if (c >= chunks) break;  // uniform
-            const int un = (u + kL - 1) % kL, up = (u + kL - 2) % kL;  // slots of chunks c + kL - 1, c + kL - 2
-            const uint32_t b0 = bm[u][0], b1 = bm[u][1];
-            const uint32_t r0 = rs[u], r1 = __builtin_popcount(b0) + r0;
-            const uint32_t qc[3] = {q[u][0], q[u][1], q[u][2]};
-            const uint32_t scu = sc[u];
-            // chunk c + kL - 1: rank (from chunk c + kL - 2), signs, scale; chunk c + kL: bitmap
-            rs[un] = rs[up] + __builtin_popcount(bm[up][0]) + __builtin_popcount(bm[up][1]);
-            sg_load(rs[un], q[un]);
-            sc[un] = s_load(c + kL - 1);
-            bm_load(c + kL, bm[u]);
-
+            const uint32_t b0w = bm[u][0], b1w = bm[u][1];
+            const uint32_t r0 = rs[u], r1 = __builtin_popcount(b0w) + r0;
             const int k = k0 + 64 * c;
             const uint32_t base = r0 >> 5;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 uint2 e[8];
-                bc_decode_word(lut, h ? b1 : b0, bc_window(qc, base, h ? r1 : r0), e);
+                bc_decode_word(lut, h ? b1w : b0w, bc_window(q[u], base, h ? r1 : r0), e);
                 const int kd = (k + 32 * h) >> 1;  // first activation pair of the word
 #pragma unroll
                 for (int r = 0; r < MR; ++r) {
@@ -194,13 +186,18 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
             }
             // group end (or slice end mid-group): apply the group's scale
             if (((k + 64) & (kGS - 1)) == 0 || c + 1 == chunks) {
-                const float s = dt2f<BF16>(scu);
+                const float s = dt2f<BF16>(sc[u]);
 #pragma unroll
                 for (int r = 0; r < MR; ++r) {
                     acc[r] += part[r] * s;
                     part[r] = 0.0f;
                 }
             }
+        }
+#pragma unroll
+        for (int i = 0; i < BC; ++i) {
+            bm[i][0] = nb[i][0];
+            bm[i][1] = nb[i][1];
         }
     }
 
@@ -371,13 +368,35 @@ k_bitcos_to_int2(const uint32_t *__restrict__ Bc, const uint32_t *__restrict__ S
     }
 }
 
+// Chunks per block: the slice's own count up to 8 (from 2, 4, 6, 8), else 6
+// where that divides it, else 8.
+int bc_block(int chunks) {
+    if (chunks <= 8) return chunks <= 2 ? 2 : chunks <= 4 ? 4 : chunks <= 6 ? 6 : 8;
+    return chunks % 6 == 0 ? 6 : 8;
+}
+
+template <int MR, bool BF16, int BC>
+void bc_launch_b(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
+                 const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
+                 int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
+    hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16, BC>), dim3((N + 63) / 64, ksw), dim3(64 * (ls / ksw)), 0, st,
+                       (const uint16_t *)A, Bc, (const uint16_t *)S, SR, C, (const uint16_t *)Other, Bias,
+                       M, m0, N, K, ls, postop, out_f32, ksw, part, cnt);
+}
+
 template <int MR, bool BF16>
 void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
                int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
-    hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16>), dim3((N + 63) / 64, ksw), dim3(64 * (ls / ksw)), 0, st,
-                       (const uint16_t *)A, Bc, (const uint16_t *)S, SR, C, (const uint16_t *)Other, Bias,
-                       M, m0, N, K, ls, postop, out_f32, ksw, part, cnt);
+#define TCL_BC_B(BC) \
+    bc_launch_b<MR, BF16, BC>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st)
+    switch (bc_block(K / ls / 64)) {
+    case 2: TCL_BC_B(2); break;
+    case 4: TCL_BC_B(4); break;
+    case 6: TCL_BC_B(6); break;
+    default: TCL_BC_B(8); break;
+    }
+#undef TCL_BC_B
 }
 
 template <bool BF16>
