@@ -71,6 +71,7 @@ ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, co
 ternocl_status int2_s8_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 // kernels (bitcos.hip)
 int bitcos_max_ls();
+int bitcos_pick_ls(int N, int K);
 ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, const void *S,
                                const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias,
                                int M, int N, int K, int postop, int out_f32, hipStream_t st, void *ws = nullptr,
@@ -387,11 +388,9 @@ ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K
 }
 
 int ternocl_bitcos_pick_ls(int M, int N, int K) {
-    (void)M; (void)N;
-    int best = 1;
-    for (int ls = 1; ls <= bitcos_max_ls(); ++ls)
-        if (K % (64 * ls) == 0 && K / (64 * ls) >= 6) best = ls;
-    return best;
+    (void)M;
+    if (N < 1 || K < 64) return 1;
+    return bitcos_pick_ls(N, K);
 }
 
 ternocl_status ternocl_bitcos_dequant(int dtype, const uint32_t *B, const void *S, void *W, int K,

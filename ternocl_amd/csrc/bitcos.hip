@@ -411,17 +411,24 @@ void bc_launch_rows(const void *A, const uint32_t *Bc, const void *S, const uint
     }
 }
 
-// Workgroups per strip for a launch of N / 64 strips of ls slices: the
-// smallest divisor of ls that puts fewer waves on the busiest CU than one
-// workgroup per strip does, with the workgroups dealt evenly over the 256 CUs
-// (more workgroups cost more than the balance returns: N = 21504, ls = 14,
-// graph-timed at z = .5: 1 per strip 20.9 us, 2 19.0, 7 21.7, 14 22.0).
-int bc_pick_ksw(int N, int ls) {
+// Relative cost of a launch with k workgroups per 64-column strip (each over
+// K / k rows), dealt evenly over the 256 CUs: the busiest CU's workgroups,
+// each costing its share of K plus a fixed part (the table build, the
+// slice-sum exchange) worth 2.55% of a whole K.  Fitted to graph-timed runs
+// at K = 5376, z = .5, N = 21504 (336 strips): ls = 12 with k = 1, 2, 3, 4, 6
+// 20.6 / 19.3 / 16.9 / 19.1 / 18.2 us, ls = 14 with k = 1, 2, 7 20.9 / 17.7 /
+// 19.4 us.
+double bc_cost(int N, int k) {
     const long strips = (N + 63) / 64;
-    const long base = (strips + 255) / 256 * ls;
+    return (double)((strips * k + 255) / 256) * (1.0 / k + 0.0255);
+}
+
+// Workgroups per strip for ls slices: the divisor of ls of least cost.
+int bc_pick_ksw(int N, int ls) {
+    int best = 1;
     for (int k = 2; k <= ls; ++k)
-        if (ls % k == 0 && (strips * k + 255) / 256 * (ls / k) < base) return k;
-    return 1;
+        if (ls % k == 0 && bc_cost(N, k) < bc_cost(N, best)) best = k;
+    return best;
 }
 
 // Workspace of a split launch: a counter per 64-column strip (256-byte
@@ -432,6 +439,25 @@ size_t bc_split_ws(int N, int ksw) { return ksw > 1 ? bc_cnt_bytes(N) + (size_t)
 }  // namespace
 
 int bitcos_max_ls() { return kBcMaxLs; }
+
+// The slice count whose best split (bc_pick_ksw) costs least, among ls <= 16
+// with K % (64 * ls) == 0 and >= 6 sixty-four-row chunks per slice (the larger
+// ls on a tie).  K = 5376: N = 21504 takes 12 (3 workgroups of 4 waves per
+// strip: 16.9 us against 17.7 at 14 split in 2), N = 16384 takes 14 (one
+// workgroup per strip).
+int bitcos_pick_ls(int N, int K) {
+    int best = 0;
+    double best_cost = 0.0;
+    for (int ls = 1; ls <= kBcMaxLs; ++ls) {
+        if (K % (64 * ls) || K / (64 * ls) < 6) continue;
+        const double c = bc_cost(N, bc_pick_ksw(N, ls));
+        if (best == 0 || c <= best_cost) {
+            best = ls;
+            best_cost = c;
+        }
+    }
+    return best ? best : 1;
+}
 
 // Workspace bytes for the split launch of this shape (0: none helps).
 size_t bitcos_gemv_ws_need(int N, int ls) { return bc_split_ws(N, bc_pick_ksw(N, ls)); }
