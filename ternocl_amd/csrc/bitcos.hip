@@ -229,20 +229,25 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
             prev = __builtin_amdgcn_atomic_inc32(cnt + blockIdx.x, (uint32_t)(ksw - 1), __ATOMIC_RELAXED, "agent");
         prev = __builtin_amdgcn_readfirstlane(prev);
         if (prev != (uint32_t)(ksw - 1)) return;
-        float v[kBcMaxLs][MR];  // every workgroup's sums in flight at once (ksw <= 16), added in order
+        // 16 / MR workgroups' sums in flight at a time (past ksw clamped, loaded
+        // and not added), added in order
+        constexpr int U = 16 / MR;
+        for (int u0 = 0; u0 < ksw; u0 += U) {
+            float v[U][MR];
 #pragma unroll
-        for (int u = 0; u < kBcMaxLs; ++u) {
-            const int s2 = u < ksw ? u : ksw - 1;
+            for (int u = 0; u < U; ++u) {
+                const int s2 = u0 + u < ksw ? u0 + u : ksw - 1;
 #pragma unroll
-            for (int r = 0; r < MR; ++r)
-                v[u][r] = __hip_atomic_load(wsum + ((size_t)s2 * MR + r) * N + nc, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-        }
+                for (int r = 0; r < MR; ++r)
+                    v[u][r] = __hip_atomic_load(wsum + ((size_t)s2 * MR + r) * N + nc, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+            }
 #pragma unroll
-        for (int u = 0; u < kBcMaxLs; ++u) {
-            if (u >= ksw) break;
+            for (int u = 0; u < U; ++u) {
+                if (u0 + u >= ksw) break;
 #pragma unroll
-            for (int r = 0; r < MR; ++r) acc[r] = u == 0 ? v[u][r] : acc[r] + v[u][r];
+                for (int r = 0; r < MR; ++r) acc[r] = u0 + u == 0 ? v[u][r] : acc[r] + v[u][r];
+            }
         }
     }
     if (n >= N) return;
@@ -394,7 +399,10 @@ void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t 
     case 2: TCL_BC_B(2); break;
     case 4: TCL_BC_B(4); break;
     case 6: TCL_BC_B(6); break;
-    default: TCL_BC_B(8); break;
+    default:
+        if constexpr (MR == 4) TCL_BC_B(4);  // (8 chunks of 4 rows need more than 128 VGPRs)
+        else TCL_BC_B(8);
+        break;
     }
 #undef TCL_BC_B
 }
