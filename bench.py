@@ -687,9 +687,11 @@ def main():
         dSR = torch.zeros(max(ls - 1, 1) * Nb, dtype=torch.int32, device="cuda")
         T.bitcos_slice_ranks(dBc, dSR, Kb, Nb, ls)
         dCb = torch.empty((1, Nb), dtype=torch.float16, device="cuda")
+        wsb = T.bitcos_gemv_ws_bytes(Nb, ls)  # the split launch, as the c4 leg runs it
+        dws = torch.zeros(max(wsb, 16), dtype=torch.uint8, device="cuda")
         for _ in range(args.probe):
-            T.bitcos_fp16_upcvt_gemm(x, dBc, dSc, dSR, dCb, None, None, 1, Nb, Kb, ls)
-        del x, dBc, dSc, dSR, dCb
+            T.bitcos_fp16_upcvt_gemm(x, dBc, dSc, dSR, dCb, None, None, 1, Nb, Kb, ls, ws=dws)
+        del x, dBc, dSc, dSR, dCb, dws
         # one int2 MoE prefill layer, T=2048 E=64 top-8 H=2048 I=1408 bf16
         Tk, E, topk, H, I = 2048, 64, 8, 2048, 1408
         g = synth.rng(55)
