@@ -345,15 +345,16 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
                                         size_t ws_bytes, void *stream);
 
 /* Replaces the int8 MoE prefill (int2_moe/int2_moe_prefill_int8.cl:1-191, the
- * sequence of int2_moe/prefill.cpp:243-279 run with --int8 0): route, gather
- * the token rows into expert order, quant_a of the gathered rows
- * (ternocl_quant_a semantics, G rows), up = s8 x s2 per expert segment (POSTOP
- * 0), h = silu(gate) * up (POSTOP 1, Other = up), quant_a of h, down
- * (fp32), combine; quant_a writes the int8 rows once (the reference's QMODE 0,
- * whose int8 values its QMODE 1 reproduces).  Arguments as
- * ternocl_int2_moe_prefill; ws >= ternocl_int2_moe_prefill_int8_ws_bytes(T,
- * E, topk, H, I) bytes, 256-byte aligned.  The gathered rows (T topk H 4
- * bytes) and each expert's packed weights must be below 2^31 bytes.  The
+ * sequence of int2_moe/prefill.cpp:243-279 run with --int8 0): route, quant_a
+ * of the T token rows (ternocl_quant_a semantics, the reference's quant_x),
+ * up = s8 x s2 per expert segment (POSTOP 0) and h = silu(gate) * up (POSTOP
+ * 1, Other = up), both gathering their int8 rows through the route's perm
+ * (its gather_q, inside the GEMM), quant_a of h, down (fp32), combine; the
+ * int8 values are the reference's QMODE 0 ones, which its QMODE 1
+ * reproduces.  Arguments as ternocl_int2_moe_prefill; ws >=
+ * ternocl_int2_moe_prefill_int8_ws_bytes(T, E, topk, H, I) bytes, 256-byte
+ * aligned.  The expert-sorted rows (T topk H 4 bytes) and each expert's packed
+ * weights must be below 2^31 bytes.  The
  * reference's pass rule for this layer is rel < 5e-2 (prefill.cpp:318). */
 size_t ternocl_int2_moe_prefill_int8_ws_bytes(int T, int E, int topk, int H, int I);
 ternocl_status ternocl_int2_moe_prefill_int8(int dtype, const void *X, const int *ids, const void *RW,

@@ -430,6 +430,9 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
 // route's tile rows); workgroup (tile, column block) finds its expert by binary
 // search and runs the GEMM on its segment: weights B + e (K/16) N, SB + e
 // (K/128) N, and Aq, SA's columns, C and Other shifted to the segment's rows.
+// With perm, the A rows are gathered instead: sorted row p reads row
+// perm[p] / topk of Aq [arows][K] and its column of SA [K/128][ldsa(arows)]
+// (the token rows quantized once, as the reference's quant_x + gather_q).
 template <int RMB_, int WVN_> struct WTile {
     static constexpr int RMB = RMB_, WVN = WVN_;
     static constexpr int THREADS = 64 * WVN;
@@ -459,11 +462,13 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
                    const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB, void *__restrict__ C,
                    const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N, int K,
                    int postop, int out_f32, const int *__restrict__ meta = nullptr, int E = 0, int splits = 1,
-                   float *part = nullptr) {
+                   float *part = nullptr, const int *__restrict__ perm = nullptr, int topk = 1, int arows = 0) {
     constexpr int RMB = TC::RMB, BM = TC::BM, BN = TC::BN, AP = TC::AP, TH = TC::THREADS;
     __shared__ __attribute__((aligned(16))) uint8_t lds[TC::LDS_BYTES];
     int tm, tn, sa_off = 0;
-    const int lda = ldsa_of(M);  // (GRP: of all G rows)
+    const bool gat = GRP && perm != nullptr;  // (uniform) A rows gathered through perm
+    const int lda = ldsa_of(gat ? arows : M);  // (GRP: of all G rows, or of the arows gathered from)
+    [[maybe_unused]] const int *prow = nullptr;  // gat: perm of the segment's rows
     if constexpr (GRP) {
         const int ntn = (N + BN - 1) / BN;
         const int tile = blockIdx.x / ntn;
@@ -479,9 +484,13 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         const int e = __builtin_amdgcn_readfirstlane(lo), row0 = __builtin_amdgcn_readfirstlane(meta[e]);
         tm = __builtin_amdgcn_readfirstlane(tile - meta[E + 1 + e]);
         M = __builtin_amdgcn_readfirstlane(meta[e + 1] - row0);
-        Aq += (size_t)row0 * K;
-        sa_off = row0;
-        SA += row0;
+        if (gat) {
+            prow = perm + row0;
+        } else {
+            Aq += (size_t)row0 * K;
+            sa_off = row0;
+            SA += row0;
+        }
         B += (size_t)e * (K / 16) * N;
         SB += (size_t)e * (K / kGS) * N;
         C = (uint8_t *)C + (size_t)row0 * N * (out_f32 ? 4 : 2);
@@ -519,12 +528,16 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     // A staging: chunk id = tid + THREADS u -> row id >> 3, 16-byte chunk id & 7
     // of the stage's 128 bytes; rows past mrows lie past the buffer's end and
     // load as 0; the stage index is clamped, so every load is in range.
-    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(Aq + (size_t)m0 * K, (uint32_t)((size_t)mrows * K));
+    // (gat: the buffer is all arows rows; rows past mrows re-read the tile's
+    // last row, whose outputs are never stored)
+    const __amdgpu_buffer_rsrc_t rA = gat ? buf_rsrc(Aq, (uint32_t)((size_t)arows * K))
+                                          : buf_rsrc(Aq + (size_t)m0 * K, (uint32_t)((size_t)mrows * K));
     uint32_t va[AP];
 #pragma unroll
     for (int u = 0; u < AP; ++u) {
         const int id = tid + TH * u;
-        va[u] = (uint32_t)((id >> 3) * K + 16 * (id & 7));
+        const int r = gat ? prow[m0 + min(id >> 3, mrows - 1)] / topk : id >> 3;
+        va[u] = (uint32_t)(r * K + 16 * (id & 7));
     }
     uint4 av[AP];
     auto a_load = [&](int g) __attribute__((always_inline)) {
@@ -538,9 +551,10 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     // 1 / SA of the tile's rows: threads t, t + BM, ... stage row t % BM (rows
     // past mrows load row mrows - 1, as the last group's row m0 + srow may lie
     // past SA's end and the SGPR offset is not range-checked, and store 0)
-    const __amdgpu_buffer_rsrc_t rSA = buf_rsrc(SA + m0, (uint32_t)(((size_t)(K / kGS) * lda - sa_off - m0) * 2));
+    const __amdgpu_buffer_rsrc_t rSA = gat ? buf_rsrc(SA, (uint32_t)((size_t)(K / kGS) * lda * 2))
+                                           : buf_rsrc(SA + m0, (uint32_t)(((size_t)(K / kGS) * lda - sa_off - m0) * 2));
     const int srow = tid & (BM - 1);
-    const uint32_t vsa = (uint32_t)min(srow, mrows - 1) * 2;
+    const uint32_t vsa = (uint32_t)(gat ? prow[m0 + min(srow, mrows - 1)] / topk : min(srow, mrows - 1)) * 2;
     uint32_t sa_raw = 0;
     auto sa_load = [&](int g) __attribute__((always_inline)) {
         const int gc = g0 + (g < groups ? g : groups - 1);
@@ -755,7 +769,8 @@ static hipError_t int8_gemm_w_launch(int dtype, const int8_t *Aq, const void *SA
 // times the column blocks.  Its tiles have the route's 128 rows.
 static hipError_t int8_moe_launch(int dtype, const int *meta, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other, int E, int G,
-                                  int N, int K, int postop, int out_f32, hipStream_t st) {
+                                  int N, int K, int postop, int out_f32, hipStream_t st, const int *perm, int topk,
+                                  int arows) {
     const bool bf = dtype == TERNOCL_BF16;
     const uint16_t *sa = (const uint16_t *)SA, *sb = (const uint16_t *)SB, *oth = (const uint16_t *)Other;
     typedef WideTile TC;
@@ -763,17 +778,20 @@ static hipError_t int8_moe_launch(int dtype, const int *meta, const int8_t *Aq, 
     const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
     if (bf)
         hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
-                           nullptr, G, N, K, postop, out_f32, meta, E);
+                           nullptr, G, N, K, postop, out_f32, meta, E, 1, nullptr, perm, topk, arows);
     else
         hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
-                           nullptr, G, N, K, postop, out_f32, meta, E);
+                           nullptr, G, N, K, postop, out_f32, meta, E, 1, nullptr, perm, topk, arows);
     return hipGetLastError();
 }
 
+// perm (optional): the A rows gathered from Aq [arows][K] (row perm[p] / topk
+// for sorted row p), SA [K/128][ldsa(arows)].
 ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const int8_t *Aq, const void *SA, const uint32_t *B,
                                  const void *SB, void *C, const void *Other, int E, int G, int N, int K, int postop,
-                                 int out_f32, hipStream_t st) {
-    return launch_status(int8_moe_launch(dtype, meta, Aq, SA, B, SB, C, Other, E, G, N, K, postop, out_f32, st));
+                                 int out_f32, hipStream_t st, const int *perm, int topk, int arows) {
+    return launch_status(int8_moe_launch(dtype, meta, Aq, SA, B, SB, C, Other, E, G, N, K, postop, out_f32, st,
+                                         perm, topk, arows));
 }
 
 int int8_moe_tile_rows() { return WideTile::BM; }

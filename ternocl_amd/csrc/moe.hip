@@ -285,34 +285,36 @@ ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M
                            const int *perm = nullptr, int topk = 1, const int *nrows = nullptr);
 ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const int8_t *Aq, const void *SA, const uint32_t *B,
                                  const void *SB, void *C, const void *Other, int E, int G, int N, int K, int postop,
-                                 int out_f32, hipStream_t st);
+                                 int out_f32, hipStream_t st, const int *perm = nullptr, int topk = 1,
+                                 int arows = 0);
 
-// Workspace: meta | perm | inv | SA1 [H/128][ldsa(G)] | U DT [G][I] |
-// Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [G][H] | Hq int8
+// Workspace: meta | perm | inv | SA1 [H/128][ldsa(T)] | U DT [G][I] |
+// Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [T][H] | Hq int8
 // [G][I], each 256-byte aligned.
 MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
-    const size_t G = (size_t)T * topk, lda = ((size_t)G + 31) & ~(size_t)31;
+    const size_t G = (size_t)T * topk, lda = ((size_t)G + 31) & ~(size_t)31, ldt = ((size_t)T + 31) & ~(size_t)31;
     MoeI8Ws w;
     size_t o = 0;
     w.meta = o; o = align_up(o + (size_t)(2 * E + 2) * 4, 256);
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
-    w.sa1 = o;  o = align_up(o + (size_t)(H / 128) * lda * 2, 256);
+    w.sa1 = o;  o = align_up(o + (size_t)(H / 128) * ldt * 2, 256);
     w.u = o;    o = align_up(o + G * I * 2, 256);
     w.h = o;    o = align_up(o + G * I * 2, 256);
     w.sa2 = o;  o = align_up(o + (size_t)(I / 128) * lda * 2, 256);
     w.y = o;    o = align_up(o + G * H * 4, 256);
-    w.xq = o;   o = align_up(o + G * H, 256);
+    w.xq = o;   o = align_up(o + (size_t)T * H, 256);
     w.hq = o;   o = align_up(o + G * I, 256);
     w.total = o;
     return w;
 }
 
-// route; quant_a of the token rows in expert order (SA1, Xq: the gather
-// fused into the quantization); up = s8 x s2 (POSTOP 0); h = silu(gate) * up (POSTOP 1,
-// Other = up); quant_a of h (SA2, Hq); Y = s8 x s2 down (fp32); combine.  The
-// int8 rows are written once (the reference's QMODE 0 with WRITE_Q); its
-// QMODE 1, quantizing in each GEMM, gives the same int8 values.
+// route; quant_a of the T token rows (SA1, Xq: each token quantized once, the
+// reference's quant_x); up = s8 x s2 (POSTOP 0) and h = silu(gate) * up (POSTOP 1,
+// Other = up), both gathering their A rows from Xq through perm (the
+// reference's gather_q, fused into the A loads); quant_a of h (SA2, Hq); Y =
+// s8 x s2 down (fp32); combine.  The int8 values are quant_a's of each row,
+// wherever it is quantized: the reference's QMODE 0 and QMODE 1 give the same.
 ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
                                     int topk, int H, int I, const uint32_t *Bg, const void *Sg,
                                     const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
@@ -326,10 +328,12 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
     const int G = T * topk;
     ternocl_status s;
     if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
-    if ((s = quant_a_run(dtype, X, SA1, Xq, G, H, st, perm, topk, meta + E)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st)) != TERNOCL_OK)
+    if ((s = quant_a_run(dtype, X, SA1, Xq, T, H, st)) != TERNOCL_OK) return s;
+    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st, perm, topk, T)) !=
+        TERNOCL_OK)
         return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st)) != TERNOCL_OK)
+    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st, perm, topk, T)) !=
+        TERNOCL_OK)
         return s;
     if ((s = quant_a_run(dtype, Hs, SA2, Hq, G, I, st, nullptr, 1, meta + E)) != TERNOCL_OK) return s;
     if ((s = int8_moe_gemm_run(dtype, meta, Hq, SA2, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK)
