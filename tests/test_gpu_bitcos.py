@@ -42,6 +42,30 @@ def test_fwht_bit_exact(dev, orc, HB, bf16, rows, K, use_signs):
     assert np.array_equal(host_u16(dy), want)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("case", ["tail4", "tail8", "offset", "tail256_hb4096"])
+def test_fwht_both_kernels_bit_exact(dev, orc, bf16, case):
+    """The register kernel (aligned rows, K % 8 == 0, a tail of 0 or >= 8) and the LDS
+    kernel (everything else: a 4-element tail, rows that are not 16-byte aligned) give
+    the oracle's bits; the 8-element tail is the register kernel's smallest block."""
+    import torch
+    import ternocl_amd as T
+    rows, K, HB, off = {"tail4": (2, 1028, 1024, 0), "tail8": (2, 520, 512, 0), "offset": (3, 4096, 512, 1),
+                        "tail256_hb4096": (1, 4352, 4096, 0)}[case]
+    print(f"fwht kernels case={case} rows={rows} K={K} HB={HB} bf16={bf16}", flush=True)
+    g = synth.rng(K + HB + off)
+    x = synth.activations(g, (rows, K), bf16)
+    s = (g.integers(0, 2, K, dtype=np.int8) * 2 - 1).astype(np.int8)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    xb = torch.zeros(rows * K + off, dtype=dt, device="cuda")  # off: x and y start one element in
+    yb = torch.zeros(rows * K + off, dtype=dt, device="cuda")
+    xb[off:].copy_(dev_dt(x, bf16).reshape(-1))
+    T.hadamard_fwht(xb[off:], dev_raw(s), yb[off:], rows, K, HB, True)
+    torch.cuda.synchronize()
+    want = orc.fwht(x, s, rows, K, HB, True, bf16)
+    assert np.array_equal(host_u16(yb[off:]).reshape(rows, K), want)
+
+
 def test_fwht_rejects_bad_shapes(dev):
     import torch
     import ternocl_amd as T
