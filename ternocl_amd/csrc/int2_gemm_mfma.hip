@@ -72,6 +72,9 @@ template <> struct ScaleOp<false> {
 };
 template <> struct ScaleOp<true> {
     uint32_t lo, hi;
+    // the decode's mask and bits: registers (gemm_tile pins them), so that
+    // the mask-and-set is one v_and_or_b32 (a VOP3 takes no literal here)
+    uint32_t km = 0x03030303u, ko = 0x04000400u;
     __device__ __forceinline__ void set(uint32_t s) {
         const uint32_t l = s & 0xffu, h = (s >> 8) & 0xffu;
         lo = (l << 8) | (l << 24);
@@ -93,12 +96,16 @@ __device__ __forceinline__ void frag(uint32_t w, int h, const ScaleOp<false> &sc
         __builtin_memcpy(&b[i], &r, 4);
     }
 }
+// bf16: the byte selector of dword i is (c, c + 4, c', c' + 4) for the codes c,
+// c' of rows j, j + 8: bytes h and h + 2 of the word (rows 4h .. 4h + 3 and
+// 4h + 8 .. 4h + 11) are spread to (b, b, b', b') once, then each dword takes
+// its 2-bit field of every byte and sets bit 2 of bytes 1 and 3 (three
+// operations per dword).
 __device__ __forceinline__ void frag(uint32_t w, int h, const ScaleOp<true> &sc, uint32_t b[4]) {
+    const uint32_t t = __builtin_amdgcn_perm(w, w, h ? 0x03030101u : 0x02020000u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int j = 4 * h + i;
-        const uint32_t x = (w >> (2 * j)) & 0x00030003u;  // codes of rows j (byte 0), j+8 (byte 2)
-        const uint32_t sel = __umul24(x, 0x101u) + 0x04000400u;  // v_mad_u32_u24
+        const uint32_t sel = ((t >> (2 * i)) & sc.km) | sc.ko;  // v_and_or_b32
         b[i] = __builtin_amdgcn_perm(sc.hi, sc.lo, sel);
     }
 }
@@ -322,6 +329,18 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     }
 
     ScaleOp<BF16> sop[NB][CB2];
+    if constexpr (BF16) {  // the decode's constants in registers (opaque to constant folding)
+        uint32_t km = 0x03030303u, ko = 0x04000400u;
+        asm("" : "+v"(km));
+        asm("" : "+s"(ko));
+#pragma unroll
+        for (int m = 0; m < NB; ++m)
+#pragma unroll
+            for (int cb = 0; cb < CB2; ++cb) {
+                sop[m][cb].km = km;
+                sop[m][cb].ko = ko;
+            }
+    }
     a_load(0, 0);
     if constexpr (BC) {
 #pragma unroll
