@@ -376,9 +376,13 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // blocks of this wave that hold tile rows.  Its MFMAs and A fragment reads
     // stop there (none: the wave still stages A and meets the barriers); the
     // loop is compiled per count, so no branch sits inside it.  (uniform)
+    // A wave is dead when its rows all lie past the tile's end (WVM > 1) or
+    // its columns all lie past N (the last column tile of an N that is not a
+    // multiple of BN, as the MoE gate/up's I = 1408 on 256-column tiles).
     const int lmb = SHORT ? max(0, min(MB2, (mrows - wm + 31) / 32)) : MB2;
-    constexpr bool kDeadWaves = SHORT && Cfg::WVM > 1;  // a wave's rows can all lie past the tile's end
-    if (kDeadWaves && lmb == 0) {
+    constexpr bool kDeadWaves = SHORT;
+    const bool dead = (Cfg::WVM > 1 && lmb == 0) || n0 + wn >= N;
+    if (kDeadWaves && dead) {
     } else if (lmb == 1 && MB2 > 1) {
         a_frags(lds, 0, af0, std::integral_constant<int, 1>{});
     } else {
@@ -474,7 +478,7 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
         }
     };
     if constexpr (SHORT) {
-        if (kDeadWaves && lmb == 0) run(std::integral_constant<int, 0>{});
+        if (kDeadWaves && dead) run(std::integral_constant<int, 0>{});
         else if (MB2 > 1 && lmb == 1) run(std::integral_constant<int, 1>{});
         else run(std::integral_constant<int, MB2>{});
     } else {
