@@ -33,10 +33,16 @@ __device__ __forceinline__ float dt2f(uint32_t h) {
 template <bool BF16>
 __device__ __forceinline__ uint32_t f2dt(float f) {
     if constexpr (BF16) {
-        uint32_t u = __float_as_uint(f);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // NaN
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return u >> 16;
+        // v_cvt_pk_bf16_f32 (round to nearest even; a NaN keeps its sign and
+        // upper payload bits and gets the quiet bit): the bits of the
+        // reference's fromf (common/dt16.hpp:30-36), (u + 0x7fff + lsb) >> 16
+        // and (u >> 16) | 0x40 for a NaN, in one instruction per two values
+        // instead of five per value
+        asm volatile("" : "+v"(f));
+        const __bf16 x = (__bf16)f;
+        uint16_t b;
+        __builtin_memcpy(&b, &x, 2);
+        return b;
     } else {
         // Materialise the fp32 value first: otherwise a product feeding the
         // conversion fuses into v_fma_mixlo_f16, which rounds once straight to
@@ -68,8 +74,14 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t a, float c) {
 // ---- fused epilogue: common/epilogue.clh:22-48, common/epilogue.hpp:82 ----
 // postop 0 none, 1 silu(acc)*other, 2 acc+other, 3 acc+bias, 4 sigmoid,
 // 5 (acc+bias)+other (bias add + residual add, an extension).
+// The sigmoid as the reference's kernels compute it (common/epilogue.clh:22-25:
+// native_recip(native_exp(-x) + 1), 0 for x <= -10): the hardware's 2^x
+// (v_exp_f32) of -x log2(e) and its reciprocal (v_rcp_f32), each within about
+// an ulp; four VALU operations instead of ~20 for expf and an IEEE division.
+// x = +inf gives 1, -inf 0 and NaN NaN, as the exact form does.
 __device__ __forceinline__ float sigmoid_ref(float x) {
-    return x <= -10.0f ? 0.0f : 1.0f / (expf(-x) + 1.0f);
+    const float e = __builtin_amdgcn_exp2f(-x * 1.44269504088896341f);
+    return x <= -10.0f ? 0.0f : __builtin_amdgcn_rcpf(e + 1.0f);
 }
 
 __host__ __device__ constexpr bool postop_needs_other(int p) { return p == 1 || p == 2 || p == 5; }

@@ -169,6 +169,50 @@ def test_moe_combine_bit_exact(dev, orc, bf16):
     assert np.array_equal(host_u16(dO), orc.moe_combine(Y, inv.cpu().numpy(), RW, Tk, topk, N, bf16))
 
 
+def _special_f32_bits(g, n):
+    """fp32 bit patterns of every class the DT rounding meets: ties and near-ties at the bf16 and
+    fp16 rounding points, fp32 and DT denormals, the largest finite values and those that round to
+    the DT's infinity, signed zeros, infinities, NaNs, then random patterns to fill n."""
+    hi = g.integers(0, 1 << 16, 512, dtype=np.uint64)
+    pats = [(hi << 16) | lo for lo in (0x0000, 0x7FFF, 0x8000, 0x8001, 0xFFFF)]  # bf16 ties / near-ties
+    e = g.integers(0x33, 0x48, 512, dtype=np.uint64) << 23  # exponents 2^-26 .. 2^16: fp16 denormals to overflow
+    m = g.integers(0, 1 << 10, 512, dtype=np.uint64) << 13
+    pats += [e | m | lo for lo in (0x0000, 0x0FFF, 0x1000, 0x1001)]  # fp16 ties / near-ties
+    pats.append(np.array([0, 1, 0x7FFFFF, 0x8000, 0x18000, 0x17FFF, 0x7F7FFFFF, 0x7F7F8000, 0x7F7F7FFF,
+                          0x477FE000, 0x477FEFFF, 0x477FF000, 0x477FF001, 0x387FE000, 0x33800000, 0x33000001,
+                          0x7F800000, 0x7FC00000, 0x7F800001, 0x7FBFFFFF, 0x7FFFFFFF, 0x3F808000, 0x3F818000],
+                         dtype=np.uint64))
+    base = np.concatenate(pats)
+    base = np.concatenate([base, base | (1 << 31)])  # both signs
+    rnd = g.integers(0, 1 << 32, max(0, n - base.size), dtype=np.uint64)
+    return np.concatenate([base, rnd])[:n].astype(np.uint32)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_moe_combine_rounding_special_values(dev, orc, bf16):
+    """The output rounding to DT (one expert, top-1, weight 1.0: O = DT(0 + 1.0 * Y)) bit for bit
+    against the oracle's restatement of the reference's fromf (common/dt16.hpp:30-36) on every class
+    of fp32 value; a NaN stays a NaN of its sign (its payload through the fp32 arithmetic is the
+    platform's)."""
+    import torch
+    import ternocl_amd as T
+    Tk, N = 16, 2048
+    Yb = _special_f32_bits(synth.rng(9), Tk * N)
+    Y = Yb.view(np.float32).reshape(Tk, N)
+    _, _, inv = _route(T, np.zeros(Tk, np.int32), Tk, 1)
+    RW = formats.f32_to_dt(np.ones(Tk, np.float32), bf16)
+    dO = torch.zeros((Tk, N), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
+    T.int2_moe_combine(torch.from_numpy(Y.copy()).cuda(), inv, dev_dt(RW, bf16), dO, Tk, 1, N)
+    torch.cuda.synchronize()
+    got = host_u16(dO)
+    want = orc.moe_combine(Y, inv.cpu().numpy(), RW, Tk, 1, N, bf16)
+    nan = np.isnan(Y)
+    assert nan.any() and np.isinf(Y).any()
+    assert np.array_equal(got[~nan], want[~nan])
+    gf = formats.dt_to_f32(got, bf16)
+    assert np.isnan(gf[nan]).all() and np.array_equal(np.signbit(gf[nan]), np.signbit(Y[nan]))
+
+
 def _layer(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16):
     (Bg, Sg), (Bu, Su), (Bd, Sd) = W
     dO = torch.zeros((Tk, H), dtype=torch.bfloat16 if bf16 else torch.float16, device="cuda")
