@@ -160,6 +160,13 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
         for (int i = 0; i < BC; ++i) sc[i] = s_load(b0 + i);
 #pragma unroll
         for (int i = 0; i < BC; ++i) bm_load(b0 + BC + i, nb[i]);
+        // Pin the block's sign and scale words here: without a use at this
+        // point the compiler sinks each chunk's loads past the early exit
+        // below into that chunk's decode, one memory round trip per chunk.
+        // (The wait this implies covers these loads only: the bitmap loads
+        // just issued stay in flight.)
+#pragma unroll
+        for (int i = 0; i < BC; ++i) asm volatile("" : "+v"(q[i][0]), "+v"(q[i][1]), "+v"(q[i][2]), "+v"(sc[i]));
 #pragma unroll
         for (int u = 0; u < BC; ++u) {
             const int c = b0 + u;
