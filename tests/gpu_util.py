@@ -36,7 +36,7 @@ def host_f32(t) -> np.ndarray:
 
 
 def allclose_report(got: np.ndarray, ref: np.ndarray, rtol=1e-2, atol=1e-3):
-    """The north-star float rule: |got - ref| <= atol + rtol * |ref| element-wise."""
+    """The floating-point parity rule: |got - ref| <= atol + rtol * |ref| element-wise."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     d = np.abs(got - ref)
