@@ -642,7 +642,7 @@ def main():
                          "prefill layer (T=2048 E=64 top-8 H=2048 I=1408); prints one line")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+        print(f"bench.py measures one GPU: the library has no multi-GPU path (asked for --gpus {args.gpus}). "
               "Each GEMV would shard by output columns with no exchange; run --gpus 1.", file=sys.stderr)
         sys.exit(2)
 

@@ -1,7 +1,7 @@
 /*
  * ternocl_oracle.c -- CPU restatement of TernOCL's host reference numerics.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP library.  Only tests/,
+ * TEST INFRASTRUCTURE ONLY: results of the HIP library are checked against it.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
  *
  * Built with gcc -O2 -fopenmp -ffp-contract=off and no -march flags, so that

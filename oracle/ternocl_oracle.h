@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
  * Python mirror of the kernel interface) may call, link or load this code:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * and only as the checker.
+ * and only to check results against.
  *
  * Every function cites the reference file:line whose behaviour it restates.
  * Values of the 16-bit activation / scale / output dtype ("DT") travel as raw
