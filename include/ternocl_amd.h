@@ -348,8 +348,9 @@ ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids
  * sequence of int2_moe/prefill.cpp:243-279 run with --int8 0): route, quant_a
  * of the T token rows (ternocl_quant_a semantics, the reference's quant_x),
  * up = s8 x s2 per expert segment (POSTOP 0) and h = silu(gate) * up (POSTOP
- * 1, Other = up), both gathering their int8 rows through the route's perm
- * (its gather_q, inside the GEMM), quant_a of h, down (fp32), combine; the
+ * 1, Other = up) in one pass that gathers the int8 rows through the route's
+ * perm (its gather_q, inside the GEMM; up stays in registers, the bits of the
+ * two launches), quant_a of h, down (fp32), combine; the
  * int8 values are the reference's QMODE 0 ones, which its QMODE 1
  * reproduces.  Arguments as ternocl_int2_moe_prefill; ws >=
  * ternocl_int2_moe_prefill_int8_ws_bytes(T, E, topk, H, I) bytes, 256-byte

@@ -213,7 +213,7 @@ struct MoeWs {
 };
 // The int8 MoE prefill layer's workspace (byte offsets, each 256-byte aligned).
 struct MoeI8Ws {
-    size_t meta, perm, inv, sa1, u, h, sa2, y, xq, hq, total;
+    size_t meta, perm, inv, sa1, h, sa2, y, xq, hq, total;
 };
 // Records the HIP error text for ternocl_last_error() and maps it to a status.
 // Scratch bytes of the allocation-free MoE decode entry (moe.hip).

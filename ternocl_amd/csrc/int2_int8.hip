@@ -433,6 +433,11 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
 // With perm, the A rows are gathered instead: sorted row p reads row
 // perm[p] / topk of Aq [arows][K] and its column of SA [K/128][ldsa(arows)]
 // (the token rows quantized once, as the reference's quant_x + gather_q).
+// DUAL (the int8 MoE layer's up and gate in one pass over the gathered rows,
+// int2_moe/prefill.cpp:268-279 with --int8 1): each wave's two 32-column
+// blocks are the same 32 columns of B (up) and B2 (gate), BN = 32 WVN; C =
+// DT(silu(gate) * DT(up)), the bits of the up launch (postop 0, DT out)
+// followed by the gate launch (postop 1 with Other = that DT output).
 template <int RMB_, int WVN_> struct WTile {
     static constexpr int RMB = RMB_, WVN = WVN_;
     static constexpr int THREADS = 64 * WVN;
@@ -456,14 +461,18 @@ __device__ __forceinline__ i32x16_t mfma_i8_32(const i32x4_t &a, const i32x4_t &
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-template <class TC, bool BF16, bool GRP = false>
+template <class TC, bool BF16, bool GRP = false, bool DUAL = false>
 __global__ void __launch_bounds__(TC::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ SA,
                    const uint32_t *__restrict__ B, const uint16_t *__restrict__ SB, void *__restrict__ C,
                    const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int N, int K,
                    int postop, int out_f32, const int *__restrict__ meta = nullptr, int E = 0, int splits = 1,
-                   float *part = nullptr, const int *__restrict__ perm = nullptr, int topk = 1, int arows = 0) {
-    constexpr int RMB = TC::RMB, BM = TC::BM, BN = TC::BN, AP = TC::AP, TH = TC::THREADS;
+                   float *part = nullptr, const int *__restrict__ perm = nullptr, int topk = 1, int arows = 0,
+                   const uint32_t *__restrict__ B2 = nullptr, const uint16_t *__restrict__ SB2 = nullptr) {
+    static_assert(!DUAL || GRP, "the dual mode is the grouped MoE GEMM's");
+    constexpr int RMB = TC::RMB, BM = TC::BM, AP = TC::AP, TH = TC::THREADS;
+    constexpr int WCOLS = DUAL ? 32 : 64;  // output columns per wave
+    constexpr int BN = WCOLS * TC::WVN;
     __shared__ __attribute__((aligned(16))) uint8_t lds[TC::LDS_BYTES];
     int tm, tn, sa_off = 0;
     const bool gat = GRP && perm != nullptr;  // (uniform) A rows gathered through perm
@@ -493,6 +502,10 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         }
         B += (size_t)e * (K / 16) * N;
         SB += (size_t)e * (K / kGS) * N;
+        if constexpr (DUAL) {
+            B2 += (size_t)e * (K / 16) * N;
+            SB2 += (size_t)e * (K / kGS) * N;
+        }
         C = (uint8_t *)C + (size_t)row0 * N * (out_f32 ? 4 : 2);
         if (Other) Other += (size_t)row0 * N;
     }
@@ -523,7 +536,7 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c32 = lane & 31, h = lane >> 5;
-    const int wn = 64 * wave;
+    const int wn = WCOLS * wave;
 
     // A staging: chunk id = tid + THREADS u -> row id >> 3, 16-byte chunk id & 7
     // of the stage's 128 bytes; rows past mrows lie past the buffer's end and
@@ -584,6 +597,12 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B + (size_t)g0 * 8 * N + n0,
                                                (uint32_t)(((size_t)(K / 16 - 8 * g0) * N - n0) * 4));
     const __amdgpu_buffer_rsrc_t rSB = buf_rsrc(SB + (size_t)g0 * N + n0, (uint32_t)(((size_t)(K / kGS - g0) * N - n0) * 2));
+    // DUAL: the second column block reads the gate weights at the same columns
+    [[maybe_unused]] __amdgpu_buffer_rsrc_t rB2 = rB, rSB2 = rSB;
+    if constexpr (DUAL) {
+        rB2 = buf_rsrc(B2 + (size_t)g0 * 8 * N + n0, (uint32_t)(((size_t)(K / 16 - 8 * g0) * N - n0) * 4));
+        rSB2 = buf_rsrc(SB2 + (size_t)g0 * N + n0, (uint32_t)(((size_t)(K / kGS - g0) * N - n0) * 2));
+    }
     uint32_t vb[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) vb[kc] = (uint32_t)(((2 * kc + h) * N + wn + c32) * 4);
@@ -594,9 +613,12 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc)
-                bw[cb][kc] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb[kc] + 128 * cb, 0, 0);
+                bw[cb][kc] = DUAL ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(cb ? rB2 : rB, vb[kc], 0, 0)
+                                  : (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb[kc] + 128 * cb, 0, 0);
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) sraw[cb] = __builtin_amdgcn_raw_buffer_load_b16(rSB, vsb + 64 * cb, 0, 0);
+        for (int cb = 0; cb < 2; ++cb)
+            sraw[cb] = DUAL ? __builtin_amdgcn_raw_buffer_load_b16(cb ? rSB2 : rSB, vsb, 0, 0)
+                            : __builtin_amdgcn_raw_buffer_load_b16(rSB, vsb + 64 * cb, 0, 0);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) vb[kc] += (uint32_t)(32 * N);
         vsb += (uint32_t)(2 * N);
@@ -669,12 +691,23 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     // (8 lanes per row of 32 columns) for epi_store4_c.
     constexpr int EP = TC::EP_PITCH;
     float *ct = (float *)lds + (size_t)wave * 16 * RMB * EP;
+    // DUAL: h = DT(silu(gate) * DT(up)) in place of the up sums, as a float
+    // that DT-rounds back to the same bits, then block 0 goes out with postop 0
+    if constexpr (DUAL) {
+#pragma unroll
+        for (int mb = 0; mb < RMB; ++mb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float up = dt2f<BF16>(f2dt<BF16>(acc[mb][0][v]));
+                acc[mb][0][v] = dt2f<BF16>(f2dt<BF16>(epi_apply_c<1>(acc[mb][1][v], up, 0.0f)));
+            }
+    }
     __syncthreads();  // the stage buffers are free
-    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+    auto epilogue = [&](auto P_, auto F_) __attribute__((always_inline)) {
         constexpr int P = decltype(P_)::value;
         constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
+        for (int cb = 0; cb < (DUAL ? 1 : 2); ++cb) {
             const int n = n0 + wn + 32 * cb + 4 * (lane & 7);
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
@@ -696,7 +729,9 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
                 __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes
             }
         }
-    });
+    };
+    if constexpr (DUAL) epilogue(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+    else epi_dispatch(postop, out_f32, epilogue);
 }
 
 // Test hook: the MFMA B fragment each word decodes to (4 dwords per word).
@@ -792,6 +827,26 @@ ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const int8_t *Aq, c
                                  int out_f32, hipStream_t st, const int *perm, int topk, int arows) {
     return launch_status(int8_moe_launch(dtype, meta, Aq, SA, B, SB, C, Other, E, G, N, K, postop, out_f32, st,
                                          perm, topk, arows));
+}
+
+// The int8 MoE layer's up and gate in one launch (DUAL): Hs = DT(silu(A x Bg)
+// * DT(A x Bu)) over the sorted rows, the bits of int8_moe_gemm_run(up,
+// postop 0) followed by int8_moe_gemm_run(gate, postop 1, Other = up).
+ternocl_status int8_moe_dual_run(int dtype, const int *meta, const int8_t *Aq, const void *SA,
+                                 const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
+                                 int E, int G, int N, int K, hipStream_t st, const int *perm, int topk, int arows) {
+    typedef WideTile TC;
+    constexpr int BN = 32 * TC::WVN;
+    const int ntn = (N + BN - 1) / BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
+    const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
+    const uint16_t *sa = (const uint16_t *)SA, *su = (const uint16_t *)Su, *sg = (const uint16_t *)Sg;
+    if (dtype == TERNOCL_BF16)
+        hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true, true, true>), grid, block, 0, st, Aq, sa, Bu, su, Hs,
+                           nullptr, nullptr, G, N, K, 0, 0, meta, E, 1, nullptr, perm, topk, arows, Bg, sg);
+    else
+        hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, false, true, true>), grid, block, 0, st, Aq, sa, Bu, su, Hs,
+                           nullptr, nullptr, G, N, K, 0, 0, meta, E, 1, nullptr, perm, topk, arows, Bg, sg);
+    return launch_status(hipGetLastError());
 }
 
 int int8_moe_tile_rows() { return WideTile::BM; }

@@ -287,10 +287,13 @@ ternocl_status int8_moe_gemm_run(int dtype, const int *meta, const int8_t *Aq, c
                                  const void *SB, void *C, const void *Other, int E, int G, int N, int K, int postop,
                                  int out_f32, hipStream_t st, const int *perm = nullptr, int topk = 1,
                                  int arows = 0);
+ternocl_status int8_moe_dual_run(int dtype, const int *meta, const int8_t *Aq, const void *SA,
+                                 const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
+                                 int E, int G, int N, int K, hipStream_t st, const int *perm, int topk, int arows);
 
-// Workspace: meta | perm | inv | SA1 [H/128][ldsa(T)] | U DT [G][I] |
-// Hs DT [G][I] | SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [T][H] | Hq int8
-// [G][I], each 256-byte aligned.
+// Workspace: meta | perm | inv | SA1 [H/128][ldsa(T)] | Hs DT [G][I] |
+// SA2 [I/128][ldsa(G)] | Y fp32 [G][H] | Xq int8 [T][H] | Hq int8 [G][I], each
+// 256-byte aligned.
 MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     const size_t G = (size_t)T * topk, lda = ((size_t)G + 31) & ~(size_t)31, ldt = ((size_t)T + 31) & ~(size_t)31;
     MoeI8Ws w;
@@ -299,7 +302,6 @@ MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
     w.sa1 = o;  o = align_up(o + (size_t)(H / 128) * ldt * 2, 256);
-    w.u = o;    o = align_up(o + G * I * 2, 256);
     w.h = o;    o = align_up(o + G * I * 2, 256);
     w.sa2 = o;  o = align_up(o + (size_t)(I / 128) * lda * 2, 256);
     w.y = o;    o = align_up(o + G * H * 4, 256);
@@ -311,7 +313,7 @@ MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
 
 // route; quant_a of the T token rows (SA1, Xq: each token quantized once, the
 // reference's quant_x); up = s8 x s2 (POSTOP 0) and h = silu(gate) * up (POSTOP 1,
-// Other = up), both gathering their A rows from Xq through perm (the
+// Other = up) in one launch, gathering the A rows from Xq through perm (the
 // reference's gather_q, fused into the A loads); quant_a of h (SA2, Hq); Y =
 // s8 x s2 down (fp32); combine.  The int8 values are quant_a's of each row,
 // wherever it is quantized: the reference's QMODE 0 and QMODE 1 give the same.
@@ -322,17 +324,15 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
     const MoeI8Ws w = moe_i8_ws_layout(T, E, topk, H, I);
     char *b = (char *)ws;
     int *meta = (int *)(b + w.meta), *perm = (int *)(b + w.perm), *inv = (int *)(b + w.inv);
-    void *SA1 = b + w.sa1, *U = b + w.u, *Hs = b + w.h, *SA2 = b + w.sa2;
+    void *SA1 = b + w.sa1, *Hs = b + w.h, *SA2 = b + w.sa2;
     float *Y = (float *)(b + w.y);
     int8_t *Xq = (int8_t *)(b + w.xq), *Hq = (int8_t *)(b + w.hq);
     const int G = T * topk;
     ternocl_status s;
     if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
     if ((s = quant_a_run(dtype, X, SA1, Xq, T, H, st)) != TERNOCL_OK) return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bu, Su, U, nullptr, E, G, I, H, 0, 0, st, perm, topk, T)) !=
-        TERNOCL_OK)
-        return s;
-    if ((s = int8_moe_gemm_run(dtype, meta, Xq, SA1, Bg, Sg, Hs, U, E, G, I, H, 1, 0, st, perm, topk, T)) !=
+    // up and gate in one pass over the gathered int8 rows (U never leaves the registers)
+    if ((s = int8_moe_dual_run(dtype, meta, Xq, SA1, Bu, Su, Bg, Sg, Hs, E, G, I, H, st, perm, topk, T)) !=
         TERNOCL_OK)
         return s;
     if ((s = quant_a_run(dtype, Hs, SA2, Hq, G, I, st, nullptr, 1, meta + E)) != TERNOCL_OK) return s;
