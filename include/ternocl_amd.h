@@ -28,6 +28,8 @@
  *   0 none, 1 silu(acc)*other, 2 acc+other, 3 acc+bias[n], 4 sigmoid(acc)
  *   (0 for acc <= -10), and 5 = (acc + bias[n]) + other[m,n] (an extension:
  *   bias add and residual add fused in one pass; no reference counterpart).
+ *   The sigmoid is the reference kernels' native form (common/epilogue.clh:25,
+ *   the hardware's exp2 and reciprocal), within ~1e-6 relative of the exact one.
  */
 #ifndef TERNOCL_AMD_H
 #define TERNOCL_AMD_H
