@@ -255,7 +255,8 @@ ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K
 /* A slice count for ternocl_bitcos_fp16_upcvt_gemm at this shape: among the
  * ls <= 16 with K % (64 * ls) == 0 that keep >= 6 sixty-four-row chunks per
  * slice, the one whose slices spread best over the CUs with the _ws entry's
- * split (the larger ls on a tie; K = 5376: 12 at N = 21504, 14 at N = 16384). */
+ * split (on a tie: slices of at most 8 sixty-four-row chunks, the most such
+ * chunks, else the larger ls; K = 5376: 12 at N = 21504 and at N = 16384). */
 int ternocl_bitcos_pick_ls(int M, int N, int K);
 /* Bit-exact test hook of the BITCOS decode: W[k][n] = 0 / S / S ^ 0x8000 for
  * code 0 / +1 / -1 (the B operand the reference builds, bitcos_fp16_upcvt.cl:153-175),

@@ -456,17 +456,24 @@ size_t bc_split_ws(int N, int ksw) { return ksw > 1 ? bc_cnt_bytes(N) + (size_t)
 int bitcos_max_ls() { return kBcMaxLs; }
 
 // The slice count whose best split (bc_pick_ksw) costs least, among ls <= 16
-// with K % (64 * ls) == 0 and >= 6 sixty-four-row chunks per slice (the larger
-// ls on a tie).  K = 5376: N = 21504 takes 12 (3 workgroups of 4 waves per
-// strip: 16.9 us against 17.7 at 14 split in 2), N = 16384 takes 14 (one
-// workgroup per strip).
+// with K % (64 * ls) == 0 and >= 6 sixty-four-row chunks per slice.  On a tie:
+// a slice of at most 8 chunks (one block of loads: two round trips), the most
+// chunks among those, else the larger ls.  K = 5376: N = 21504 takes 12 (3
+// workgroups of 4 waves per strip: 14.5 us, against 17.5 at 14 split in 2);
+// N = 16384 takes 12 (one workgroup per strip, 7 chunks per slice: 11.9 us,
+// against 12.4 at 14 and 13.1 at 7).
 int bitcos_pick_ls(int N, int K) {
     int best = 0;
     double best_cost = 0.0;
+    auto tie_prefers = [K](int a, int b) {  // ls a over ls b at equal cost
+        const int ca = K / (64 * a), cb = K / (64 * b);
+        if ((ca <= 8) != (cb <= 8)) return ca <= 8;
+        return ca <= 8 ? ca > cb : a > b;
+    };
     for (int ls = 1; ls <= kBcMaxLs; ++ls) {
         if (K % (64 * ls) || K / (64 * ls) < 6) continue;
         const double c = bc_cost(N, bc_pick_ksw(N, ls));
-        if (best == 0 || c <= best_cost) {
+        if (best == 0 || c < best_cost || (c == best_cost && tie_prefers(ls, best))) {
             best = ls;
             best_cost = c;
         }
