@@ -60,41 +60,42 @@ template <bool BF16>
 __global__ void __launch_bounds__(256)
 k_quant_a(const uint16_t *__restrict__ A, uint16_t *__restrict__ SA, int8_t *__restrict__ Aq, int M,
           int K, const int *__restrict__ perm = nullptr, int topk = 1, const int *__restrict__ nrows = nullptr) {
-    const int cpr = K >> 3;  // 8-element chunks per row (a multiple of 16)
+    const int cpr = K >> 4;  // 16-element chunks per row (a multiple of 8)
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    // the 16 chunks of a group are 16 aligned consecutive threads: they leave together
+    // the 8 chunks of a group are 8 aligned consecutive threads: they leave together
     if (t >= (size_t)M * cpr) return;
     const int m = (int)(t / cpr), c = (int)(t - (size_t)m * cpr);
     // nrows (the MoE layer): only the *nrows rows the route kept are read and
     // written; perm: row m of the output is row perm[m] / topk of A
     if (nrows && m >= *nrows) return;
     const int src = perm ? perm[m] / topk : m;
-    const uint4 v = *(const uint4 *)(A + (size_t)src * K + 8 * (size_t)c);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    float a[8];
+    const uint16_t *row = A + (size_t)src * K + 16 * (size_t)c;
+    const uint4 v0 = *(const uint4 *)row, v1 = *(const uint4 *)(row + 8);
+    const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float a[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
         a[2 * i] = dt2f<BF16>(w[i] & 0xffffu);
         a[2 * i + 1] = dt2f<BF16>(w[i] >> 16);
     }
     float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(a[i]));
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(a[i]));
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+    for (int o = 4; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 8));
     const uint32_t sh = f2dt<BF16>(127.0f / fmaxf(mx, kEps));
-    if ((c & 15) == 0) SA[(size_t)(c >> 4) * ldsa_of(M) + m] = (uint16_t)sh;
+    if ((c & 7) == 0) SA[(size_t)(c >> 3) * ldsa_of(M) + m] = (uint16_t)sh;
     const float s = dt2f<BF16>(sh);
-    uint32_t q[2] = {0u, 0u};
+    uint32_t q[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 16; ++i) {
         // exact product, rounded to nearest even and saturated; NaN (0 * inf
         // when an fp16 scale overflows) gives 0, as convert_char8_sat_rte
         const float p = a[i] * s;
         const float r = p == p ? fminf(fmaxf(__builtin_rintf(p), -128.0f), 127.0f) : 0.0f;
         q[i >> 2] |= ((uint32_t)(int)r & 0xffu) << (8 * (i & 3));
     }
-    if (Aq) *(uint2 *)(Aq + (size_t)m * K + 8 * (size_t)c) = make_uint2(q[0], q[1]);
+    if (Aq) *(uint4 *)(Aq + (size_t)m * K + 16 * (size_t)c) = make_uint4(q[0], q[1], q[2], q[3]);
 }
 
 // ---- s8 x s2 GEMM ------------------------------------------------------------
@@ -750,7 +751,7 @@ __global__ void k_int2_s8_decode(const uint32_t *__restrict__ B, uint32_t *__res
 // quantization.
 ternocl_status quant_a_run(int dtype, const void *A, void *SA, int8_t *Aq, int M, int K, hipStream_t st,
                            const int *perm, int topk, const int *nrows) {
-    const size_t threads = (size_t)M * (K / 8);
+    const size_t threads = (size_t)M * (K / 16);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     if (dtype == TERNOCL_BF16)
         hipLaunchKernelGGL(k_quant_a<true>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)A,
