@@ -10,7 +10,7 @@
 //
 // with v the 2-bit two's-complement value of the code ({0,1,2,3} = {0,1,-2,-1}).
 //
-// quant_a is HBM-bound: one thread per 8 activations (one 16-byte load), the 16
+// quant_a is HBM-bound: one thread per 16 activations (two 16-byte loads), the 8
 // threads of a 128-group reduce the absmax with cross-lane xor shuffles.  The
 // scale is 127 / x with a correctly rounded fp32 divide (the reference builds
 // with -cl-fp32-correctly-rounded-divide-sqrt), q = rint(a * sa) saturated; the
