@@ -51,6 +51,17 @@ typedef enum {
 
 typedef enum { TERNOCL_FP16 = 0, TERNOCL_BF16 = 1 } ternocl_dtype;
 
+/* Workspaces.  Every entry that takes a device scratch (ws, ws_bytes) keeps
+ * the same first TERNOCL_WS_HEADER_BYTES of it for its cross-workgroup
+ * counters and writes nothing else there; its partial sums, re-packed weights
+ * and MoE buffers lie after that header, and every *_ws_bytes() function
+ * counts it.  Zero a scratch once (ternocl_workspace_zero) before its first
+ * use: every call leaves the counters at zero again, so one scratch can serve
+ * any sequence of calls of any entries and shapes, as long as calls that
+ * share it do not overlap.  A K split whose counters would not fit the header
+ * (more than 16384 column strips) runs unsplit instead. */
+#define TERNOCL_WS_HEADER_BYTES ((size_t)64 << 10)
+
 /* Human-readable status and the last HIP error text seen by this thread. */
 const char *ternocl_status_string(int status);
 const char *ternocl_last_error(void);
@@ -136,6 +147,14 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
  * C: fp32 [M, N]; M <= 8, N % 16 == 0, K % 128 == 0. */
 ternocl_status ternocl_int2_gemv_stream_probe(int dtype, const uint32_t *B, const void *S, void *C, int M,
                                              int N, int K, void *stream);
+
+/* Measurement hook, no GEMV: a plain streaming read of the first bytes & ~15
+ * bytes of src (16-byte aligned), every lane issuing four coalesced 16-byte
+ * loads of one 16 KiB block per workgroup before using any; it stores to the
+ * one word at sink only if the XOR of all words read equals a fixed constant.
+ * Its duration is what one launch reading that many bytes takes: the
+ * per-launch ceiling a decode GEMV of the same bytes can approach. */
+ternocl_status ternocl_stream_read_probe(const void *src, size_t bytes, void *sink, void *stream);
 
 /* ---- int2 x int8 prefill ---------------------------------------------------
  * Replaces quant_a (int2_via_int2_x_int8_dpas/int2_int8_dpas.cl:105-106):
@@ -232,10 +251,10 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_ws(int dtype, const void *A, const
  * any M, with the weights streamed once instead of once per 4 rows.
  * ws = NULL (the reference's call): the int2 prefill GEMM engine's tiles
  * decode the BITCOS weights themselves, each lane following its column's
- * sign stream down K (SR unused).  With ws (K * N / 4 bytes,
- * ternocl_bitcos_gemm_mt_ws_bytes): one pass re-packs the weights into the
- * int2 format there, then the int2 engine runs on them with S as is (the
- * re-pack splits K into ls slices).  SR / ls as for
+ * sign stream down K (SR unused).  With ws (ternocl_bitcos_gemm_mt_ws_bytes:
+ * the workspace header, then K * N / 4 bytes): one pass re-packs the weights
+ * into the int2 format after the header, then the int2 engine runs on them
+ * with S as is (the re-pack splits K into ls slices).  SR / ls as for
  * ternocl_bitcos_fp16_upcvt_gemm; the same constraints. */
 size_t ternocl_bitcos_gemm_mt_ws_bytes(int K, int N);
 ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const uint32_t *B,

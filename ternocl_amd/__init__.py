@@ -20,9 +20,9 @@ from pathlib import Path
 from . import _abi
 
 __all__ = [
-    "TernoclError", "lib", "library_path", "FP16", "BF16",
+    "TernoclError", "lib", "library_path", "FP16", "BF16", "WS_HEADER_BYTES",
     "int2_gemm_ws_bytes", "workspace_zero", "int2_fp16_upcvt_gemm", "int2_dequant",
-    "int2_gemv_decode", "int2_gemv_stream_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
+    "int2_gemv_decode", "int2_gemv_stream_probe", "stream_read_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
     "int2_pack", "int2_unpack", "bitcos_pack", "bitcos_unpack", "bitcos_slice_ranks_host",
     "ldsa", "quant_a", "int2_int8_gemm", "int2_int8_gemm_ws_bytes", "int2_s8_decode",
     "bitcos_fp16_upcvt_gemm", "bitcos_gemv_ws_bytes", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
@@ -32,6 +32,9 @@ __all__ = [
 ]
 
 FP16, BF16 = 0, 1
+# TERNOCL_WS_HEADER_BYTES: the front of every workspace, where the K splits keep
+# their counters (zero between calls); all other workspace data lies after it.
+WS_HEADER_BYTES = 64 << 10
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libternocl_amd.so"
 _lib = None
 
@@ -147,6 +150,12 @@ def int2_gemv_decode(B, D, K: int, N: int, bf16: bool, engine: int = MFMA, strea
 
 
 # ---- int2 x int8 (int2_via_int2_x_int8_dpas/int2_int8_dpas.cl) ------------
+
+def stream_read_probe(src, nbytes: int, sink, stream=None) -> None:
+    """Plain streaming read of the first nbytes (rounded down to 16) of the device tensor
+    src (measurement hook: the per-launch read ceiling; sink: a tensor of >= 4 bytes)."""
+    _check(lib().ternocl_stream_read_probe(_ptr(src), nbytes, _ptr(sink), _stream(stream)))
+
 
 def int2_gemv_stream_probe(B, S, C, M: int, N: int, K: int, stream=None) -> None:
     """The decode GEMV (engine 4) with the decode removed: streams B and S as the GEMV

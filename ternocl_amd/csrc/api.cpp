@@ -52,6 +52,7 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
                                 hipStream_t st);
 size_t int2_gemv_f4_ws_need(int M, int N, int K);
 ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
+ternocl_status stream_read_run(const void *src, size_t bytes, void *sink, hipStream_t st);  // misc.hip
 ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const void *S, void *C, int M, int N,
                                           int K, hipStream_t st);
 // kernels (int2_gemm_mfma.hip)
@@ -251,6 +252,13 @@ ternocl_status ternocl_int2_gemv_decode(int dtype, int engine, const uint32_t *B
     return int2_gemv_decode_run(dtype, B, D, K, N, (hipStream_t)stream);
 }
 
+ternocl_status ternocl_stream_read_probe(const void *src, size_t bytes, void *sink, void *stream) {
+    if (!src || !sink) FAIL(TERNOCL_ERR_INVALID_ARG, "src and sink must be non-null");
+    if (((uintptr_t)src & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "src must be 16-byte aligned");
+    if (bytes / 16 / 1024 >= 0x7fffffffu) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "bytes too large for one launch");
+    return stream_read_run(src, bytes, sink, (hipStream_t)stream);
+}
+
 ternocl_status ternocl_int2_gemv_stream_probe(int dtype, const uint32_t *B, const void *S, void *C, int M,
                                              int N, int K, void *stream) {
     ternocl_status s = check_dtype(dtype);
@@ -343,7 +351,7 @@ static ternocl_status check_bitcos_slices(int N, int K, int ls, const uint32_t *
 
 size_t ternocl_bitcos_gemm_mt_ws_bytes(int K, int N) {
     if (K < 16 || N < 1) return 0;
-    return (size_t)(K / 16) * (size_t)N * 4;
+    return kWsHeader + (size_t)(K / 16) * (size_t)N * 4;  // the header, then the re-packed words
 }
 
 ternocl_status ternocl_bitcos_to_int2(const uint32_t *B, const uint32_t *SR, int ls, uint32_t *W2, int K,
@@ -370,11 +378,12 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_mt(int dtype, const void *A, const
     const size_t need = ternocl_bitcos_gemm_mt_ws_bytes(K, N);
     if (ws_bytes < need) FAIL(TERNOCL_ERR_WORKSPACE, "ws must hold ternocl_bitcos_gemm_mt_ws_bytes(K, N) bytes");
     if (((uintptr_t)ws & 15) != 0) FAIL(TERNOCL_ERR_INVALID_ARG, "ws must be 16-byte aligned");
-    if (need >= kMaxBufBytes || (size_t)M * K * 2 >= kMaxBufBytes)
+    if (need - kWsHeader >= kMaxBufBytes || (size_t)M * K * 2 >= kMaxBufBytes)
         FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the M-tiled BITCOS path takes A and the re-packed weights below 2^31 bytes");
     const hipStream_t st = (hipStream_t)stream;
-    if ((s = bitcos_to_int2_run(B, SR, ls, (uint32_t *)ws, N, K, st)) != TERNOCL_OK) return s;
-    return int2_gemm_mfma_run(dtype, A, (const uint32_t *)ws, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    uint32_t *W2 = (uint32_t *)((uint8_t *)ws + kWsHeader);
+    if ((s = bitcos_to_int2_run(B, SR, ls, W2, N, K, st)) != TERNOCL_OK) return s;
+    return int2_gemm_mfma_run(dtype, A, W2, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
 ternocl_status ternocl_bitcos_slice_ranks(const uint32_t *B, uint32_t *SR, int K, int N, int ls,

@@ -231,11 +231,9 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
                                    __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_s_waitcnt(0);
-        uint32_t prev = 0;
-        if (lane == 0)  // wraps to 0 at the last arrival
-            prev = __builtin_amdgcn_atomic_inc32(cnt + blockIdx.x, (uint32_t)(ksw - 1), __ATOMIC_RELAXED, "agent");
-        prev = __builtin_amdgcn_readfirstlane(prev);
+        const uint32_t prev = split_arrive(cnt + blockIdx.x, ksw, lane);
         if (prev != (uint32_t)(ksw - 1)) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // only the workgroup that adds the sums
         // 16 / MR workgroups' sums in flight at a time (past ksw clamped, loaded
         // and not added), added in order
         constexpr int U = 16 / MR;
@@ -448,8 +446,9 @@ int bc_pick_ksw(int N, int ls) {
 
 // Workspace of a split launch: a counter per 64-column strip (256-byte
 // block), then the sums fp32 [ksw][4][N].
-size_t bc_cnt_bytes(int N) { return ((size_t)((N + 63) / 64) * 4 + 255) & ~(size_t)255; }
-size_t bc_split_ws(int N, int ksw) { return ksw > 1 ? bc_cnt_bytes(N) + (size_t)ksw * 4 * N * 4 : 0; }
+// counters (one per 64-column strip) in the workspace header, sums after it
+bool bc_cnt_fit(int N) { return (size_t)((N + 63) / 64) * 4 <= kWsHeader; }
+size_t bc_split_ws(int N, int ksw) { return ksw > 1 ? kWsHeader + (size_t)ksw * 4 * N * 4 : 0; }
 
 }  // namespace
 
@@ -491,9 +490,9 @@ ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, con
                                int M, int N, int K, int postop, int out_f32, hipStream_t st, void *ws,
                                size_t ws_bytes) {
     int ksw = bc_pick_ksw(N, ls);
-    if (ksw > 1 && !(ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= bc_split_ws(N, ksw))) ksw = 1;
+    if (ksw > 1 && !(ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= bc_split_ws(N, ksw) && bc_cnt_fit(N))) ksw = 1;
     uint32_t *cnt = ksw > 1 ? (uint32_t *)ws : nullptr;
-    float *part = ksw > 1 ? (float *)((uint8_t *)ws + bc_cnt_bytes(N)) : nullptr;
+    float *part = ksw > 1 ? (float *)((uint8_t *)ws + kWsHeader) : nullptr;
     if (dtype == TERNOCL_BF16)
         bc_launch_rows<true>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st);
     else

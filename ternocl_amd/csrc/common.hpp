@@ -12,6 +12,9 @@
 namespace tcl {
 
 constexpr int kGS = 128;  // scale group size (K rows per scale)
+// Front of every caller workspace: the cross-workgroup counters of the K
+// splits (zero between calls); partials and buffers start after it.
+constexpr size_t kWsHeader = TERNOCL_WS_HEADER_BYTES;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
@@ -53,6 +56,23 @@ __device__ __forceinline__ uint32_t f2dt(float f) {
         __builtin_memcpy(&b, &x, 2);
         return b;
     }
+}
+
+// A K-split workgroup's arrival at its column strip's counter (lane 0's atomic,
+// broadcast): the value before this arrival.  atomic_inc wraps to 0 at the
+// last of ksn arrivals, so the counters return to zero after every call.  A
+// counter found above ksn - 1 holds no value any call leaves there (a
+// workspace that was never zeroed): the increment has just reset it to 0, and
+// this workgroup arrives once more, so the ksn increments from 0 still elect
+// exactly the last arrival, after every slice's sums are stored.  (A stale
+// value in 1 .. ksn - 1 cannot be told apart from a live count.)
+__device__ __forceinline__ uint32_t split_arrive(uint32_t *c, int ksn, int lane) {
+    uint32_t prev = 0;
+    if (lane == 0) {
+        prev = __builtin_amdgcn_atomic_inc32(c, (uint32_t)(ksn - 1), __ATOMIC_RELAXED, "agent");
+        if (prev > (uint32_t)(ksn - 1)) prev = __builtin_amdgcn_atomic_inc32(c, (uint32_t)(ksn - 1), __ATOMIC_RELAXED, "agent");
+    }
+    return __builtin_amdgcn_readfirstlane(prev);
 }
 
 // c + w.lo * a.lo + w.hi * a.hi on packed DT pairs (v_dot2_f32_{f16,bf16})

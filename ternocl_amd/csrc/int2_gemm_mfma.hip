@@ -870,10 +870,11 @@ hipError_t splitk_reduce_launch(int dtype, const float *part, int splits, void *
     return hipGetLastError();
 }
 
-// Workspace of the split-K path: the fp32 partial tiles of every slice.
+// Workspace of the split-K path: the header, then the fp32 partial tiles of
+// every slice.
 size_t int2_gemm_ws_need(int M, int N, int K) {
     const int s = gemm_splits(M, N, K);
-    return s > 1 ? (size_t)s * M * N * 4 : 0;
+    return s > 1 ? kWsHeader + (size_t)s * M * N * 4 : 0;
 }
 
 // With a workspace of int2_gemm_ws_need bytes (16-byte aligned), shapes that
@@ -888,7 +889,7 @@ ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, c
     if (splits > 1 && ws && ws_bytes >= int2_gemm_ws_need(M, N, K) && ((uintptr_t)ws & 15) == 0) {
         typedef TileCfg<8, 4, 1, 8> Cfg;
         const int mt = (M + Cfg::BM - 1) / Cfg::BM, nt = (N + Cfg::BN - 1) / Cfg::BN;
-        float *part = (float *)ws;
+        float *part = (float *)((uint8_t *)ws + kWsHeader);
         const dim3 grid(xcd_ashare_grid(mt, nt * splits));
         if (bf)
             hipLaunchKernelGGL((k_int2_gemm<Cfg, true>), grid, dim3(Cfg::THREADS), 0, st, (const uint16_t *)A, B,

@@ -622,12 +622,14 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     if constexpr (SPLIT) {
         if (ksn > 1) {
             // This slice's sums, then the strip's counter; the last of the ksn
-            // workgroups adds the slices in order.  The sums are stored and
-            // loaded with device-scope accesses (coherent across the XCDs' L2
-            // caches by themselves, no cache write-back or invalidate, which
-            // a device-scope fence would do in every workgroup); the wait for
-            // the stores to complete orders them before the counter, and the
-            // last workgroup's loads follow the counter's result.
+            // workgroups adds the slices in order.  Release side: the sums are
+            // agent-scope stores (global_store sc1, written through to the
+            // point of coherence of all XCDs), and s_waitcnt(0) waits for
+            // their completion before the counter's atomic is issued -- the
+            // ordering a release would give without the L2 write-back
+            // (buffer_wbl2) an agent-scope release costs every workgroup.
+            // Acquire side: only the elected workgroup pays an agent-scope
+            // acquire (buffer_inv) before it loads the sums.
 #pragma unroll
             for (int h = 0; h < OPL; ++h) {
                 const int m = q + 4 * h;
@@ -639,11 +641,9 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_s_waitcnt(0);
-            uint32_t prev = 0;
-            if (lane == 0)  // wraps to 0 at the last arrival
-                prev = __builtin_amdgcn_atomic_inc32(cnt + strip, (uint32_t)(ksn - 1), __ATOMIC_RELAXED, "agent");
-            prev = __builtin_amdgcn_readfirstlane(prev);
+            const uint32_t prev = split_arrive(cnt + strip, ksn, lane);
             if (prev != (uint32_t)(ksn - 1)) return;
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             // four slices' loads in flight at a time (rows and slices past the
             // end clamped, loaded and not added), then added in slice order
             for (int s0 = 0; s0 < ksn; s0 += 4) {
@@ -902,10 +902,11 @@ bool int2_gemv_f4_supports(int M, int N, const void *A) {
     return M >= 1 && M <= kF4MaxM && ((uintptr_t)A & 15) == 0 && (size_t)M * N * 4 < 0x7ff00000u;
 }
 
-// Workspace of a K split: one counter per 16-column strip (a 256-byte
-// block), then the slice sums fp32 [ks][M][N].
-size_t f4_cnt_bytes(int N) { return ((size_t)(N / 16) * 4 + 255) & ~(size_t)255; }
-size_t f4_split_ws(int M, int N, int ks) { return ks > 1 ? f4_cnt_bytes(N) + (size_t)ks * M * N * 4 : 0; }
+// Workspace of a K split: one counter per column strip (at most N / 16 of
+// them) in the workspace header, then the slice sums fp32 [ks][M][N] after it.
+// A split whose counters would not fit the header is not taken.
+bool f4_cnt_fit(int N) { return (size_t)(N / 16) * 4 <= kWsHeader; }
+size_t f4_split_ws(int M, int N, int ks) { return ks > 1 ? kWsHeader + (size_t)ks * M * N * 4 : 0; }
 
 // Slices that leave none empty: ceil(G / ceil(G / ks)).
 int f4_slices(int groups, int ks) {
@@ -928,7 +929,7 @@ void f4_auto_split(int M, int N, int K, int cpl_req, int &cpl, int &ks) {
     cpl = cpl_u;
     ks = 1;
     const int gmin = MR >= 8 ? 16 : MR >= 2 ? 64 : 104;
-    if (N / (16 * cpl_u) >= 384 || groups < gmin) return;
+    if (N / (16 * cpl_u) >= 384 || groups < gmin || !f4_cnt_fit(N)) return;
     const int c = cpl_req > 0 ? cpl_req : (MR >= 8 && groups >= 64 && N % 64 == 0 ? 4 : (N % 32 == 0 ? 2 : 1));
     int k = groups >= 64 ? 4 : 2;  // the power of two nearest groups / 28 (log scale), 2 .. 16
     while (k < 16 && (double)groups / 28.0 > k * 1.4142) k *= 2;
@@ -990,6 +991,9 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
             pk = 1;
             pc = cpl;
         }
+    } else if (pk > 1 && !f4_cnt_fit(N)) {
+        set_error("k_slices > 1 takes at most 16384 column strips (the workspace header's counters)");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     } else if (pk > 1 && !(ws_ok && ws_bytes >= f4_split_ws(M, N, pk))) {
         set_error("k_slices > 1 needs a 16-byte aligned workspace of ternocl_int2_gemm_ws_bytes() bytes "
                   "for that split");
@@ -998,7 +1002,7 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
     F4Plan p = f4_plan(bf16, M, N, K, waves, pc, gpw, pk);
     if (pk > 1) {
         p.cnt = (uint32_t *)ws;
-        p.part = (float *)((uint8_t *)ws + f4_cnt_bytes(N));
+        p.part = (float *)((uint8_t *)ws + kWsHeader);
     }
     if (p.waves > f4_max_waves(p.mr, p.cpl)) {
         set_error("more than 8 waves per workgroup only for M = 1 with 16-column strips (cols_per_lane 1)");
@@ -1084,7 +1088,7 @@ ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, co
     F4Plan p = f4q_plan(M, N, K, cpl, ks);
     if (ks > 1 && p.lds <= kF4MaxLds) {
         p.cnt = (uint32_t *)ws;
-        p.part = (float *)((uint8_t *)ws + f4_cnt_bytes(N));
+        p.part = (float *)((uint8_t *)ws + kWsHeader);
     } else if (ks > 1) {
         p = f4q_plan(M, N, K);
     }

@@ -871,9 +871,9 @@ ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, co
     // the wide tile over K slices where its tiles alone leave CUs idle and the
     // caller gives the partials' workspace (the fp16 prefill GEMM's rule)
     const int splits = Aq ? gemm_splits(M, N, K) : 1;
-    if (splits > 1 && ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= (size_t)splits * M * N * 4)
+    if (splits > 1 && ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= kWsHeader + (size_t)splits * M * N * 4)
         return launch_status(int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st,
-                                                splits, (float *)ws));
+                                                splits, (float *)((uint8_t *)ws + kWsHeader)));
     const bool wide = Aq && (size_t)((M + WideTile::BM - 1) / WideTile::BM) * ((N + WideTile::BN - 1) / WideTile::BN) >= 192;
     const hipError_t e =
         wide  ? int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)

@@ -1,5 +1,6 @@
 // misc.hip -- small utility kernels: workspace zero-fill (used instead of
-// hipMemsetAsync so a call stays capturable in a HIP graph).
+// hipMemsetAsync so a call stays capturable in a HIP graph), and the plain
+// streaming read that measures what one launch can pull from HBM.
 #include "common.hpp"
 
 namespace tcl {
@@ -16,7 +17,39 @@ __global__ void k_fill_zero_bytes(uint8_t *__restrict__ p, size_t n) {
     if (i < n) p[i] = 0u;
 }
 
+// Plain streaming read: workgroup b reads the 16 KiB block b of src as four
+// coalesced 16-byte loads per lane, all issued before any is used, and XORs
+// the words.  The sum is stored only if it equals an arbitrary constant, so
+// the loads stay live and the kernel writes (almost) nothing: its duration is
+// the read alone.
+constexpr int kReadU = 4, kReadThreads = 256;
+__global__ void __launch_bounds__(kReadThreads) k_stream_read(const uint4 *__restrict__ src, size_t n16,
+                                                              uint32_t *__restrict__ sink) {
+    const size_t base = (size_t)blockIdx.x * (kReadU * kReadThreads) + threadIdx.x;
+    uint4 v[kReadU];
+#pragma unroll
+    for (int u = 0; u < kReadU; ++u) {
+        const size_t i = base + (size_t)u * kReadThreads;
+        v[u] = i < n16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (int u = 0; u < kReadU; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (x == 0x9e3779b9u) sink[0] = x;
+}
+
 }  // namespace
+
+// Reads the first bytes & ~15 bytes of src (16-byte aligned); sink: one
+// writable word.
+ternocl_status stream_read_run(const void *src, size_t bytes, void *sink, hipStream_t st) {
+    const size_t n16 = bytes / 16, per = (size_t)kReadU * kReadThreads;
+    const size_t blocks = (n16 + per - 1) / per;
+    if (blocks == 0) return TERNOCL_OK;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)blocks), dim3(kReadThreads), 0, st, (const uint4 *)src, n16,
+                       (uint32_t *)sink);
+    return check_launch();
+}
 
 ternocl_status fill_zero_run(void *p, size_t bytes, hipStream_t st) {
     const size_t words = bytes / 4, tail = bytes % 4;

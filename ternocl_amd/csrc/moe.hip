@@ -246,11 +246,12 @@ ternocl_status moe_combine_run(int dtype, const float *Y, const int *inv, const 
     return check_launch();
 }
 
-// Workspace of the layer: meta | perm | inv | Hs | Y, each 256-byte aligned.
+// Workspace of the layer: the header (counters of other entries sharing the
+// workspace; untouched), then meta | perm | inv | Hs | Y, each 256-byte aligned.
 MoeWs moe_ws_layout(int T, int E, int topk, int H, int I) {
     const size_t G = (size_t)T * topk;
     MoeWs w;
-    size_t o = 0;
+    size_t o = kWsHeader;
     w.meta = o; o = align_up(o + (size_t)(2 * E + 2) * 4, 256);
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
@@ -297,7 +298,7 @@ ternocl_status int8_moe_dual_run(int dtype, const int *meta, const int8_t *Aq, c
 MoeI8Ws moe_i8_ws_layout(int T, int E, int topk, int H, int I) {
     const size_t G = (size_t)T * topk, lda = ((size_t)G + 31) & ~(size_t)31, ldt = ((size_t)T + 31) & ~(size_t)31;
     MoeI8Ws w;
-    size_t o = 0;
+    size_t o = kWsHeader;
     w.meta = o; o = align_up(o + (size_t)(2 * E + 2) * 4, 256);
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
@@ -348,11 +349,11 @@ ternocl_status int2_gemv_f4_group_run(int dtype, const void *A, const int *ids, 
                                       float *C, int N, int K, const void *RW, void *O, int mode,
                                       hipStream_t st);
 
-// Workspace: gate/up fp32 [2G][I] | Y fp32 [G][H] (used when topk > 16), each
-// 256-byte aligned.
+// Workspace: the header (untouched), then gate/up fp32 [2G][I] | Y fp32 [G][H]
+// (used when topk > 16), each 256-byte aligned.
 size_t moe_decode_ws_bytes(int T, int topk, int H, int I) {
     const size_t G = (size_t)T * topk;
-    return align_up(2 * G * I * 4, 256) + align_up(G * H * 4, 256);
+    return kWsHeader + align_up(2 * G * I * 4, 256) + align_up(G * H * 4, 256);
 }
 
 // (1) One grouped GEMV over 2G rows: gate and up of every pair, fp32.
@@ -365,7 +366,7 @@ ternocl_status moe_decode_run(int dtype, const void *X, const int *ids, const vo
                               const uint32_t *Bu, const void *Su, const uint32_t *Bd, const void *Sd,
                               void *O, void *ws, hipStream_t st) {
     const int G = T * topk;
-    uint8_t *b = (uint8_t *)ws;
+    uint8_t *b = (uint8_t *)ws + kWsHeader;
     float *GU = (float *)b;
     float *Y = (float *)(b + align_up((size_t)2 * G * I * 4, 256));
     ternocl_status s;

@@ -1,8 +1,9 @@
 """PyTorch custom operators over the C ABI: ``torch.ops.ternocl.*``.
 
 A serving framework calls the library through these: each operator allocates
-its outputs (and, where the C ABI takes one, its workspace) with torch on the
-inputs' device, launches on torch's current stream, and has a fake (meta)
+its outputs with torch on the inputs' device, takes its workspace (where the C
+ABI has one) from a zeroed one kept per device and stream, launches on torch's
+current stream, and has a fake (meta)
 implementation, so the operators trace under ``torch.compile`` and run inside
 captured CUDA/HIP graphs.  They add nothing to the arithmetic: every call is
 one call of the ``ternocl_amd`` function of the same name, which raises if the
@@ -34,6 +35,29 @@ __all__ = ["int2_gemm", "quant_a", "int2_int8_gemm", "bitcos_gemm", "fwht", "moe
 
 def _out_dtype(A: torch.Tensor, out_f32: bool) -> torch.dtype:
     return torch.float32 if out_f32 else A.dtype
+
+
+# One workspace per (device, stream), zeroed once when it is allocated and
+# shared by every operator on that stream: the C ABI keeps the K splits'
+# counters in the workspace header and every call leaves them at zero, and
+# calls on one stream never overlap.  A larger request allocates a larger one
+# (at least twice the size); the smaller ones are kept alive, since a captured
+# graph may still address them.
+_WS: dict = {}
+_WS_OLD: list = []
+
+
+def _workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    if nbytes == 0:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _WS_OLD.append(ws)
+        ws = torch.zeros(max(nbytes, 0 if ws is None else 2 * ws.numel()), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
 
 
 # ---- input checks ------------------------------------------------------------
@@ -95,8 +119,7 @@ def int2_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, other: Optional
     M, K = A.shape
     N = B.shape[1]
     C = torch.empty((M, N), dtype=_out_dtype(A, out_f32), device=A.device)
-    wsb = T.int2_gemm_ws_bytes(M, N, K)  # K-split sums / counters (zeroed: the counters start at 0)
-    ws = torch.zeros(wsb, dtype=torch.uint8, device=A.device) if wsb else None
+    ws = _workspace(A.device, T.int2_gemm_ws_bytes(M, N, K))  # K-split sums and counters, where it splits
     T.int2_fp16_upcvt_gemm(A, B, S, C, other, bias, M, N, K, postop, out_f32, ws=ws)
     return C
 
@@ -135,8 +158,7 @@ def int2_int8_gemm(Aq: torch.Tensor, SA: torch.Tensor, B: torch.Tensor, SB: torc
     M, K = Aq.shape
     N = B.shape[1]
     C = torch.empty((M, N), dtype=_out_dtype(SB, out_f32), device=Aq.device)
-    wsb = T.int2_int8_gemm_ws_bytes(M, N, K)  # the K split's counters and partials, where it splits
-    ws = torch.zeros(wsb, dtype=torch.uint8, device=Aq.device) if wsb else None
+    ws = _workspace(Aq.device, T.int2_int8_gemm_ws_bytes(M, N, K))  # the K split's counters and partials
     T.int2_int8_gemm(None, Aq, SA, B, SB, C, other, bias, M, N, K, postop, out_f32, ws=ws)
     return C
 
@@ -171,11 +193,10 @@ def bitcos_gemm(A: torch.Tensor, B: torch.Tensor, S: torch.Tensor, SR: Optional[
     M, K = A.shape
     C = torch.empty((M, N), dtype=_out_dtype(A, out_f32), device=A.device)
     if M >= 16:
-        ws = torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device=A.device)
+        ws = _workspace(A.device, T.bitcos_gemm_mt_ws_bytes(K, N))
         T.bitcos_fp16_upcvt_gemm_mt(A, B, S, SR, C, other, bias, M, N, K, ls, ws, postop, out_f32)
     else:
-        wsb = T.bitcos_gemv_ws_bytes(N, ls)  # the split launch's sums / counters (zeroed: counters start at 0)
-        ws = torch.zeros(wsb, dtype=torch.uint8, device=A.device) if wsb else None
+        ws = _workspace(A.device, T.bitcos_gemv_ws_bytes(N, ls))  # the split launch's sums and counters
         T.bitcos_fp16_upcvt_gemm(A, B, S, SR, C, other, bias, M, N, K, ls, postop, out_f32, ws=ws)
     return C
 
@@ -229,7 +250,7 @@ def moe_prefill(X: torch.Tensor, ids: torch.Tensor, RW: torch.Tensor, E: int, Bg
     topk = ids.shape[1]
     I = Bg.shape[2]
     O = torch.empty((Tk, H), dtype=X.dtype, device=X.device)
-    ws = torch.empty(T.int2_moe_prefill_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device=X.device)
+    ws = _workspace(X.device, T.int2_moe_prefill_ws_bytes(Tk, E, topk, H, I))
     T.int2_moe_prefill(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
     return O
 
@@ -251,7 +272,7 @@ def moe_decode(X: torch.Tensor, ids: torch.Tensor, RW: torch.Tensor, E: int, Bg:
     topk = ids.shape[1]
     I = Bg.shape[2]
     O = torch.empty((Tk, H), dtype=X.dtype, device=X.device)
-    ws = torch.empty(T.int2_moe_decode_ws_bytes(Tk, topk, H, I), dtype=torch.uint8, device=X.device)
+    ws = _workspace(X.device, T.int2_moe_decode_ws_bytes(Tk, topk, H, I))
     T.int2_moe_decode(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
     return O
 
@@ -272,7 +293,7 @@ def moe_prefill_int8(X: torch.Tensor, ids: torch.Tensor, RW: torch.Tensor, E: in
     topk = ids.shape[1]
     I = Bg.shape[2]
     O = torch.empty((Tk, H), dtype=X.dtype, device=X.device)
-    ws = torch.empty(T.int2_moe_prefill_int8_ws_bytes(Tk, E, topk, H, I), dtype=torch.uint8, device=X.device)
+    ws = _workspace(X.device, T.int2_moe_prefill_int8_ws_bytes(Tk, E, topk, H, I))
     T.int2_moe_prefill_int8(X, ids, RW, Tk, E, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, O, ws)
     return O
 

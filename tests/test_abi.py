@@ -70,21 +70,22 @@ def test_status_strings():
 
 def test_ws_bytes_query():
     import ternocl_amd as T
-    # the fp8 x fp4 GEMV's K split: 256-byte block of strip counters + slices of fp32 [M, N]
+    H = T.WS_HEADER_BYTES
+    # the fp8 x fp4 GEMV's K split: the 64 KiB workspace header (strip counters) + slices of fp32 [M, N]
     assert T.int2_gemm_ws_bytes(1, 14336, 4096) == 0  # 448 32-column strips fill the chip unsplit
-    assert T.int2_gemm_ws_bytes(1, 4096, 14336) == 1024 + 4 * 1 * 4096 * 4  # 128 strips x 4 slices
-    assert T.int2_gemm_ws_bytes(8, 4096, 14336) == 1024 + 4 * 8 * 4096 * 4  # 64 strips x 4 slices
-    assert T.int2_gemm_ws_bytes(8, 4096, 4096) == 1024 + 2 * 8 * 4096 * 4  # 128 strips x 2 slices
+    assert T.int2_gemm_ws_bytes(1, 4096, 14336) == H + 4 * 1 * 4096 * 4  # 128 strips x 4 slices
+    assert T.int2_gemm_ws_bytes(8, 4096, 14336) == H + 4 * 8 * 4096 * 4  # 64 strips x 4 slices
+    assert T.int2_gemm_ws_bytes(8, 4096, 4096) == H + 2 * 8 * 4096 * 4  # 128 strips x 2 slices
     assert T.int2_gemm_ws_bytes(4, 4096, 4096) == 0  # 32 groups: unsplit below M = 5
     assert T.int2_gemm_ws_bytes(1, 2048, 8192) == 0  # 64 groups: unsplit at M = 1
-    assert T.int2_gemm_ws_bytes(4, 2048, 8192) == 512 + 4 * 4 * 2048 * 4  # 64 groups: 4 slices at M = 4
+    assert T.int2_gemm_ws_bytes(4, 2048, 8192) == H + 4 * 4 * 2048 * 4  # 64 groups: 4 slices at M = 4
     assert T.int2_gemm_ws_bytes(5, 14336, 4096) == 0  # 448 strips
     assert T.int2_gemm_ws_bytes(8, 4096, 512) == 0  # 4 groups: too short to slice
     assert T.int2_gemm_ws_bytes(9, 4096, 14336) == 0  # the bf16/fp16 MFMA GEMV keeps no scratch
     # the prefill GEMM's split-K partials: 4 K-slices of fp32 [M, N] where the
     # 128 x 512 tiles would leave CUs idle (8 x 8 = 64 tiles here) ...
-    assert T.int2_gemm_ws_bytes(1024, 4096, 14336) == 4 * 1024 * 4096 * 4
-    assert T.int2_gemm_ws_bytes(200, 16384, 5120) == 4 * 200 * 16384 * 4
+    assert T.int2_gemm_ws_bytes(1024, 4096, 14336) == H + 4 * 1024 * 4096 * 4
+    assert T.int2_gemm_ws_bytes(200, 16384, 5120) == H + 4 * 200 * 16384 * 4
     # ... and none where they fill the chip, or K is too short to slice
     assert T.int2_gemm_ws_bytes(1024, 14336, 4096) == 0
     assert T.int2_gemm_ws_bytes(256, 1024, 1024) == 0
@@ -92,23 +93,25 @@ def test_ws_bytes_query():
 
 def test_int8_ws_bytes_query():
     """The s8 x s2 GEMM's K split: the fp16 prefill GEMM's slices and partials; the decode
-    GEMV's (M <= 4) counter block (a counter per 16-column strip, 256-byte rounded) and
-    fp32 slice sums where K is long and the strips are few."""
+    GEMV's (M <= 4) strip counters in the 64 KiB workspace header and fp32 slice sums
+    where K is long and the strips are few."""
     import ternocl_amd as T
-    assert T.int2_int8_gemm_ws_bytes(1024, 4096, 14336) == 4 * 1024 * 4096 * 4
+    H = T.WS_HEADER_BYTES
+    assert T.int2_int8_gemm_ws_bytes(1024, 4096, 14336) == H + 4 * 1024 * 4096 * 4
     assert T.int2_int8_gemm_ws_bytes(1024, 14336, 4096) == 0  # 224 wide tiles
-    assert T.int2_int8_gemm_ws_bytes(4, 4096, 14336) == 1024 + 4 * 4 * 4096 * 4  # 112 groups: 4 slices
+    assert T.int2_int8_gemm_ws_bytes(4, 4096, 14336) == H + 4 * 4 * 4096 * 4  # 112 groups: 4 slices
     assert T.int2_int8_gemm_ws_bytes(1, 4096, 4096) == 0  # 32 groups
     assert T.int2_int8_gemm_ws_bytes(1, 14336, 4096) == 0  # 448 strips of 32 columns
 
 
 def test_bitcos_ws_bytes_query():
-    """The split BITCOS launch: a counter per 64-column strip (256-byte block) and
-    fp32 sums [slices][4][N]; none where one workgroup per strip fills the chip."""
+    """The split BITCOS launch: a counter per 64-column strip in the workspace header
+    and fp32 sums [slices][4][N]; none where one workgroup per strip fills the chip."""
     import ternocl_amd as T
-    assert T.bitcos_gemv_ws_bytes(21504, 14) == 1536 + 2 * 4 * 21504 * 4  # 336 strips: 2 workgroups of 7 waves each
+    H = T.WS_HEADER_BYTES
+    assert T.bitcos_gemv_ws_bytes(21504, 14) == H + 2 * 4 * 21504 * 4  # 336 strips: 2 workgroups of 7 waves each
     assert T.bitcos_gemv_ws_bytes(16384, 14) == 0  # 256 strips of 14 waves: one per CU
-    assert T.bitcos_gemv_ws_bytes(21504, 12) == 1536 + 3 * 4 * 21504 * 4  # 3 workgroups of 4 waves
+    assert T.bitcos_gemv_ws_bytes(21504, 12) == H + 3 * 4 * 21504 * 4  # 3 workgroups of 4 waves
     assert T.bitcos_pick_ls(1, 21504, 5376) == 12
     assert T.bitcos_pick_ls(1, 16384, 5376) == 12  # a tie at one workgroup per strip: 7 chunks per slice
     assert T.bitcos_pick_ls(1, 64, 256) == 1  # too short for 6 chunks per slice
@@ -168,3 +171,33 @@ def test_operand_size_guards():
     assert "2^31" in L.ternocl_last_error().decode()
     # the decode-removed measurement kernel: B at 2^31 bytes
     assert L.ternocl_int2_gemv_stream_probe(0, p, p, p, 1, 131072, 65536, None) == 2
+
+
+def test_ws_header_everywhere():
+    """Every workspace size counts the 64 KiB header that holds the K splits' counters,
+    so one zeroed workspace can serve any sequence of entries: the MoE layers and the
+    M-tiled BITCOS re-pack place their buffers after it too."""
+    import ternocl_amd as T
+    L = T.lib()
+    H = T.WS_HEADER_BYTES
+    assert H == 64 << 10
+    assert T.bitcos_gemm_mt_ws_bytes(5376, 21504) == H + 5376 // 16 * 21504 * 4
+    for q in (L.ternocl_int2_moe_prefill_ws_bytes(64, 8, 2, 256, 256),
+              L.ternocl_int2_moe_prefill_int8_ws_bytes(64, 8, 2, 256, 256)):
+        assert q > H
+    assert L.ternocl_int2_moe_decode_ws_bytes(1, 8, 256, 256) == H + 2 * 8 * 256 * 4 + 8 * 256 * 4
+
+
+def test_noalloc_decode_rejects_oversized_scratch():
+    """The allocation-free MoE decode entry rejects, on the host, a layer whose scratch
+    exceeds its fixed 16 MiB array.  Run without a GPU on purpose: the pointers are never
+    dereferenced, and a regressed check would reach the HIP runtime and fail there (a
+    status other than 3), never launch a kernel."""
+    import ctypes
+    import ternocl_amd as T
+    L = T.lib()
+    p = ctypes.c_void_p(4096)
+    Tk, topk, H, I = 64, 8, 4096, 8192  # 2 * 512 * 8192 * 4 bytes of gate/up rows: 32 MiB > 16 MiB
+    assert L.ternocl_int2_moe_decode_ws_bytes(Tk, topk, H, I) > 16 << 20
+    assert L.ternocl_int2_moe_decode_noalloc(1, p, p, p, Tk, 8, topk, H, I, p, p, p, p, p, p, p, None) == 3
+    assert "16 MiB" in L.ternocl_last_error().decode()

@@ -259,6 +259,48 @@ def test_bitcos_hadamard_pipeline(dev, orc):
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
+@pytest.mark.parametrize("z", [0.3, 0.5, 0.7])
+def test_bitcos_c4_default_plan(dev, orc, z):
+    """The decode-step workload as bench.py dispatches it: M=1 K=5376 N=21504 fp16, sign flip
+    + FWHT (HB 512), then the BITCOS GEMV at the library's slice count
+    (ternocl_bitcos_pick_ls: 12) through the split launch (ternocl_bitcos_fp16_upcvt_gemm_ws:
+    three workgroups per strip) and unsplit; every output within 1e-3 + 1e-2 |ref| of the
+    host gold on the transformed activation, the split launch bit-identical on repeated
+    calls with its counters back at zero."""
+    import torch
+    import ternocl_amd as T
+    M, K, N, bf16, HB = 1, 5376, 21504, False, 512
+    ls = T.bitcos_pick_ls(M, N, K)
+    wsb = T.bitcos_gemv_ws_bytes(N, ls)
+    assert ls == 12 and wsb > 0
+    print(f"bitcos C4 default plan z={z} ls={ls} ws={wsb}", flush=True)
+    g = synth.rng(44 + int(10 * z))
+    x = synth.activations(g, (M, K), bf16)
+    sgn = (g.integers(0, 2, K, dtype=np.int8) * 2 - 1).astype(np.int8)
+    buf, _ = synth.bitcos_weights(g, K, N, z)
+    S = synth.scales(g, K, N, bf16)
+    dy = torch.zeros((M, K), dtype=torch.float16, device="cuda")
+    T.hadamard_fwht(dev_dt(x, bf16), dev_raw(sgn), dy, M, K, HB, True)
+    dB, dS = dev_raw(buf), dev_dt(S, bf16)
+    dSR = torch.zeros((ls - 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+    outs = []
+    for w in (ws, ws, None):
+        dC = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+        T.bitcos_fp16_upcvt_gemm(dy, dB, dS, dSR, dC, None, None, M, N, K, ls, ws=w)
+        torch.cuda.synchronize()
+        outs.append(host_u16(dC))
+    assert np.array_equal(outs[0], outs[1]), "split launch not deterministic"
+    assert not ws[:T.WS_HEADER_BYTES].any().item(), "split launch left a counter set"
+    y = orc.fwht(x, sgn, M, K, HB, True, bf16)
+    assert np.array_equal(host_u16(dy), y)
+    want = formats.dt_to_f32(orc.epilogue(orc.bitcos_gold(y, buf, S, M, K, N, bf16), None, None, 0, False, bf16), bf16)
+    for name, out in (("split", outs[0]), ("unsplit", outs[2])):
+        bad, dmax = allclose_report(formats.dt_to_f32(out, bf16), want)
+        assert bad == 0, f"{name}: {bad} bad (max |d| {dmax})"
+
+
 def test_bitcos_rejects_bad_ls(dev):
     import torch
     import ternocl_amd as T

@@ -256,8 +256,8 @@ def test_gemv_f4_k_slices(dev, orc, M, K, N, ks, cpl, bf16):
     tile = T.gemv_tile(T.F4, 0, cpl, 0, 0, ks)
     dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16), dev_dt(other, bf16)
     dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
-    cnt_bytes = ((N // 16) * 4 + 255) // 256 * 256
-    ws = torch.zeros(cnt_bytes + ks * M * N * 4, dtype=torch.uint8, device="cuda")
+    cnt_bytes = (N // 16) * 4  # the strip counters, at the front of the workspace header
+    ws = torch.zeros(T.WS_HEADER_BYTES + ks * M * N * 4, dtype=torch.uint8, device="cuda")
     for postop in (0, 5):
         outs = []
         for _ in range(3):
@@ -279,7 +279,7 @@ def test_gemv_f4_k_slices_need_the_workspace(dev):
     import ternocl_amd as T
     M, K, N = 8, 14336, 4096
     need = T.int2_gemm_ws_bytes(M, N, K)
-    assert need == 1024 + 4 * M * N * 4  # 4 slices of fp32 [M, N] after the 64 strip counters
+    assert need == T.WS_HEADER_BYTES + 4 * M * N * 4  # 4 slices of fp32 [M, N] after the counters' header
     dA = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
     dB = torch.zeros((K // 16, N), dtype=torch.int32, device="cuda")
     dS = torch.zeros((K // 128, N), dtype=torch.bfloat16, device="cuda")

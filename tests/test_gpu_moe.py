@@ -265,10 +265,45 @@ def test_moe_layer_small(dev, orc, bf16):
     assert rel < 1e-2, rel
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_moe_layer_multi_tile_experts(dev, orc, bf16):
+    """Experts spanning two to three 128-row tiles with ragged last tiles (T=512, E=8, top-4:
+    ~256 rows each) and I = 1408 = 5.5 x 256 (a half-live last column tile): every output of
+    the layer within 1e-3 + 1e-2 |ref| of the oracle's stage composition, so the tiles past
+    each expert's first (the tile search's later row offsets, their perm rows and the
+    live-block tail loops) are all compared."""
+    import torch
+    import ternocl_amd as T
+    Tk, E, topk, H, I = 512, 8, 4, 256, 1408
+    g = synth.rng(4242)
+    X = synth.activations(g, (Tk, H), bf16)
+    ids, RW = synth.moe_routing(g, Tk, E, topk, bf16)
+    counts = np.bincount(ids, minlength=E)
+    rpt = T.moe_tile_rows()
+    assert (counts > rpt).all() and (counts > 2 * rpt).any() and (counts % rpt != 0).all(), counts
+    print(f"moe multi-tile T={Tk} E={E} topk={topk} H={H} I={I} bf16={bf16} rows/expert {counts.tolist()}",
+          flush=True)
+    W = _weights(g, E, H, I, bf16)
+    got = formats.dt_to_f32(_layer(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16), bf16)
+    want = formats.dt_to_f32(_oracle_layer(orc, X, ids, RW, Tk, E, topk, H, I, W, bf16, rpt), bf16)
+    bad, dmax = allclose_report(got, want)
+    assert bad == 0, f"{bad} of {got.size} outputs outside the rule (max |d| {dmax})"
+
+
+def _c5_check_tokens(Tk, seed=2026, n_random=8):
+    """Tokens of the C5 layer the double-precision check covers: the first four (the first
+    rows of every expert's first tile), the last four (their rows land at the ends of the
+    expert segments, in the last tiles) and a seeded random sample."""
+    g = np.random.default_rng(seed)
+    rand = sorted(int(t) for t in g.choice(np.arange(4, Tk - 4), n_random, replace=False))
+    return [(0, 4), (Tk - 4, Tk)] + [(t, t + 1) for t in rand]
+
+
 def test_moe_layer_workload_shape(dev, orc):
-    """T=2048 tokens, 64 experts, top-8, H=2048, I=1408, bf16: the first tokens against
-    the double-precision reference check (int2_moe/prefill.cpp:288-319, rule rel < 1e-2),
-    and every output finite; two runs bit-identical."""
+    """T=2048 tokens, 64 experts, top-8, H=2048, I=1408, bf16: the first and last four tokens
+    and a random sample against the double-precision reference check
+    (int2_moe/prefill.cpp:288-319, rule rel < 1e-2), every output finite; two runs
+    bit-identical."""
     import torch
     import ternocl_amd as T
     Tk, E, topk, H, I, bf16 = 2048, 64, 8, 2048, 1408, True
@@ -280,9 +315,10 @@ def test_moe_layer_workload_shape(dev, orc):
     got = formats.dt_to_f32(out, bf16)
     assert np.isfinite(got).all()
     (Bg, Sg), (Bu, Su), (Bd, Sd) = W
-    ref = orc.moe_ref_tokens(X, ids, RW, 0, 4, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16)
-    rel = np.abs(got[:4] - ref).max() / np.abs(ref).max()
-    assert rel < 1e-2, rel
+    for t0, t1 in _c5_check_tokens(Tk):
+        ref = orc.moe_ref_tokens(X, ids, RW, t0, t1, topk, H, I, Bg, Sg, Bu, Su, Bd, Sd, bf16)
+        rel = np.abs(got[t0:t1] - ref).max() / np.abs(ref).max()
+        assert rel < 1e-2, (t0, t1, rel)
     again = _layer(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16)
     assert np.array_equal(out, again)
 

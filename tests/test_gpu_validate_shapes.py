@@ -4,7 +4,14 @@ drop-in caller gets).
 
 Shape lists:
 * int2 upcvt: int2_fp16_upcvt/validate.sh:8-10 (M K N; fp16 and bf16);
-* int2 x int8 (quant_a + s8 x s2): int2_via_int2_x_int8_dpas/validate.sh:9-10;
+* int2 x int8 (quant_a + s8 x s2): int2_via_int2_x_int8_dpas/validate.sh:9-10,
+  in both quantization modes (QMODE 0 upfront, QMODE 1 in the GEMM), as
+  that script runs every shape in both;
+* BITCOS: bitcos_fp16_upcvt/validate.sh:8-15 -- its GEMV lines (M <= 8, the
+  given slice count and zero density, z = 0.4 where none is given, its
+  default, bitcos_fp16_upcvt/main.cpp:47) with and without the split-launch
+  workspace, and its M-tiled lines through the M-tiled entry, both with the
+  re-pack workspace and without (the tiles decoding BITCOS);
 * the prefill workload M=1024 K=4096 N=14336 in both paths, and the decode
   workload's sweep M in {1, 2, 4, 8} x (K, N) in {(4096, 14336), (14336, 4096)}
   in bf16 with the bias + residual epilogue.
@@ -90,12 +97,14 @@ def _upcvt_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
     return _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
 
 
-def _int8_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0, split=False):
+def _int8_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0, split=False, qmode=0):
     """split: with the K-split workspace -- the same bits on a second call, and within the rule
-    of the call without it."""
+    of the call without it.  qmode 1: the DT activations are quantized inside the GEMM (SA
+    from quant_a), the reference's QMODE 1."""
     import torch
     import ternocl_amd as T
-    print(f"int8 M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32} split={split}", flush=True)
+    print(f"int8 M={M} K={K} N={N} bf16={bf16} postop={postop} f32={out_f32} split={split} qmode={qmode}",
+          flush=True)
     A, B, SB, other, bias_f = _inputs(seed + 50000 + M + K + N, M, K, N, bf16)
     dA = dev_dt(A, bf16)
     dSA = torch.zeros((K // 128, T.ldsa(M)), dtype=dA.dtype, device="cuda")
@@ -108,7 +117,10 @@ def _int8_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0, split=F
         need = T.int2_int8_gemm_ws_bytes(M, N, K)
         assert need > 0, "this shape should split"
         ws = torch.empty(need, dtype=torch.uint8, device="cuda")
-    T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
+    if qmode == 1:
+        T.int2_int8_gemm(dA, None, dSA, dB, dSB, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
+    else:
+        T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, dO, dBias, M, N, K, postop, out_f32, ws=ws)
     torch.cuda.synchronize()
     if split:
         first = dC.clone()
@@ -141,10 +153,11 @@ def test_upcvt_validate_shapes(dev, orc, M, K, N, bf16):
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
 
 
+@pytest.mark.parametrize("qmode", [0, 1])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("M,K,N", INT8_VALIDATE + [PREFILL_WORKLOAD, WIDE_RAGGED])
-def test_int8_validate_shapes(dev, orc, M, K, N, bf16):
-    bad, dmax = _int8_case(dev, orc, M, K, N, bf16)
+def test_int8_validate_shapes(dev, orc, M, K, N, bf16, qmode):
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16, qmode=qmode)
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
 
 
@@ -238,3 +251,92 @@ def test_splitk_epilogues(dev, orc, bf16, postop, out_f32):
     bad, dmax, bad_nows = _splitk_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
     assert bad_nows == 0
+
+
+# ---- BITCOS: bitcos_fp16_upcvt/validate.sh:8-15 ----------------------------------
+# (M, K, N, ls, z, postop, out_f32); ls 0 = the library's choice (the lines that give none)
+BITCOS_VALIDATE_GEMV = [(1, 4096, 4096, 4, 0.4, 0, False), (1, 4096, 4096, 1, 0.4, 0, False),
+                        (1, 4096, 6144, 8, 0.4, 0, False), (1, 12288, 4096, 8, 0.6, 0, False),
+                        (1, 17408, 5120, 4, 0.3, 0, False), (1, 16384, 32768, 1, 0.4, 0, False),
+                        (3, 4096, 2048, 2, 0.4, 0, False), (8, 1024, 512, 4, 0.1, 0, False),
+                        (1, 4096, 1024, 16, 0.95, 0, False), (1, 4096, 4096, 0, 0.4, 1, False),
+                        (1, 4096, 4096, 0, 0.4, 3, True)]
+# (M, K, N, z, postop, out_f32): the --mt-m lines
+BITCOS_VALIDATE_MT = [(64, 4096, 4096, 0.4, 0, False), (77, 4096, 2064, 0.05, 0, False),
+                      (129, 17408, 5120, 0.4, 0, False), (512, 5120, 14336, 0.4, 0, False),
+                      (9, 6144, 1024, 0.95, 0, False), (77, 4096, 2048, 0.4, 1, False),
+                      (77, 4096, 2048, 0.4, 3, True)]
+
+
+def _bitcos_inputs(seed, M, K, N, z, bf16):
+    g = synth.rng(seed)
+    A = synth.activations(g, (M, K), bf16)
+    buf, _ = synth.bitcos_weights(g, K, N, z)
+    S = synth.scales(g, K, N, bf16)
+    other = synth.activations(g, (M, N), bf16)
+    bias_f = g.standard_normal(N).astype(np.float32) * np.float32(0.1)
+    return A, buf, S, other, bias_f
+
+
+def _bitcos_device(torch, T, A, buf, S, other, bias_f, M, K, N, ls, bf16, out_f32):
+    dB = dev_raw(buf)
+    dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    dO, dBias, dC = _device_io(torch, S, other, bias_f, M, N, bf16, out_f32)
+    return dev_dt(A, bf16), dB, dev_dt(S, bf16), dSR if ls > 1 else None, dO, dBias, dC
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ls,z,postop,out_f32", BITCOS_VALIDATE_GEMV)
+def test_bitcos_validate_gemv(dev, orc, M, K, N, ls, z, postop, out_f32, bf16):
+    """Each GEMV line, unsplit and (where the shape splits) through the split-launch
+    workspace; both within the rule of the host gold, the split one bit-identical on a
+    second call with its counters back at zero."""
+    import torch
+    import ternocl_amd as T
+    ls = ls or T.bitcos_pick_ls(M, N, K)
+    wsb = T.bitcos_gemv_ws_bytes(N, ls)
+    print(f"bitcos validate gemv M={M} K={K} N={N} ls={ls} z={z} postop={postop} f32={out_f32} bf16={bf16} "
+          f"ws={wsb}", flush=True)
+    A, buf, S, other, bias_f = _bitcos_inputs(70000 + M + K + N + ls, M, K, N, z, bf16)
+    dA, dB, dS, dSR, dO, dBias, dC = _bitcos_device(torch, T, A, buf, S, other, bias_f, M, K, N, ls, bf16, out_f32)
+    T.bitcos_fp16_upcvt_gemm(dA, dB, dS, dSR, dC, dO, dBias, M, N, K, ls, postop, out_f32)
+    torch.cuda.synchronize()
+    acc = orc.bitcos_gold(A, buf, S, M, K, N, bf16)
+    rows = np.arange(M)
+    bad, dmax = _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
+    assert bad == 0, f"unsplit: {bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+    if wsb:
+        ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+        _, _, dC2 = _device_io(torch, S, other, bias_f, M, N, bf16, out_f32)
+        T.bitcos_fp16_upcvt_gemm(dA, dB, dS, dSR, dC2, dO, dBias, M, N, K, ls, postop, out_f32, ws=ws)
+        torch.cuda.synchronize()
+        first = dC2.clone()
+        T.bitcos_fp16_upcvt_gemm(dA, dB, dS, dSR, dC2, dO, dBias, M, N, K, ls, postop, out_f32, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(first, dC2), "split launch not deterministic"
+        assert not ws[:T.WS_HEADER_BYTES].any().item(), "split launch left a counter set"
+        bad, dmax = _compare(orc, dC2, acc, other, bias_f, rows, bf16, postop, out_f32)
+        assert bad == 0, f"split: {bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("in_tile", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,z,postop,out_f32", BITCOS_VALIDATE_MT)
+def test_bitcos_validate_mt(dev, orc, M, K, N, z, postop, out_f32, bf16, in_tile):
+    """Each M-tiled line through ternocl_bitcos_fp16_upcvt_gemm_mt: with the re-pack workspace
+    and without (the reference's call: the tiles decode BITCOS), row-sampled above 127 rows."""
+    import torch
+    import ternocl_amd as T
+    ls = T.bitcos_pick_ls(1, N, K)
+    print(f"bitcos validate mt M={M} K={K} N={N} ls={ls} z={z} postop={postop} f32={out_f32} bf16={bf16} "
+          f"in_tile={in_tile}", flush=True)
+    A, buf, S, other, bias_f = _bitcos_inputs(71000 + M + K + N, M, K, N, z, bf16)
+    dA, dB, dS, dSR, dO, dBias, dC = _bitcos_device(torch, T, A, buf, S, other, bias_f, M, K, N, ls, bf16, out_f32)
+    ws = None if in_tile else torch.empty(T.bitcos_gemm_mt_ws_bytes(K, N), dtype=torch.uint8, device="cuda")
+    T.bitcos_fp16_upcvt_gemm_mt(dA, dB, dS, dSR, dC, dO, dBias, M, N, K, ls, ws, postop, out_f32)
+    torch.cuda.synchronize()
+    rows = sample_rows(M)
+    acc = orc.bitcos_gold(np.ascontiguousarray(A[rows]), buf, S, rows.size, K, N, bf16)
+    bad, dmax = _compare(orc, dC, acc, other, bias_f, rows, bf16, postop, out_f32)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
