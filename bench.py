@@ -133,6 +133,12 @@ def time_graph(torch, g, s):
 
 
 REPEATS = 3  # every figure: the median of this many timed replays
+_T0 = time.perf_counter()
+
+
+def progress(msg):
+    """One progress line on stderr per finished stage (the JSON line stays alone on stdout)."""
+    print(f"[bench {time.perf_counter() - _T0:7.1f}s] {msg}", file=sys.stderr, flush=True)
 
 
 def median_replays(torch, g, s, reps=REPEATS):
@@ -277,6 +283,7 @@ def bench_ref_shapes(torch, T, synth, formats, orc):
         out[name] = e
         del W
         torch.cuda.empty_cache()
+        progress(f"ref shape {name} K={K} N={N}: GEMV {e['gemv_m1']['us']} us, prefill {e['prefill_m1024']['us']} us")
     return out
 
 
@@ -850,6 +857,7 @@ def main():
     ts = [time_graph(torch, gt, st) for _ in range(REPEATS)]
     t = float(np.median(ts))
     replay_same = all(np.array_equal(sb.output(), e) for sb, e in zip(sbs, eager))
+    progress(f"headline step timed: {t / args.steps * 1e6:.2f} us per step")
     step_bytes = sum(sb.bytes() for sb in sbs)
     value = step_bytes * args.steps / t / 1e9
 
@@ -874,6 +882,7 @@ def main():
                                                        "measured": "event pair + synchronize per launch"},
                                       "weight_sets": sb.sets, "parity_bad": bad, "max_abs_diff": dmax}
     isolated = tot_b / (tot_t * 1e-6) / 1e9
+    progress("headline shapes: per-launch, decode-removed, wait-mode and plain-read times done")
 
     extra = {}
     if not args.no_sweep:
@@ -903,20 +912,14 @@ def main():
             del sb
             torch.cuda.empty_cache()
         extra["bf16_mfma_engine_m1"] = bf
+        progress("M sweep and the other GEMV engines done")
 
     if not args.only_headline:
-        extra["prefill"] = bench_c3(torch, T, synth, formats, orc)
-        torch.cuda.empty_cache()
-        extra["c1"] = bench_c1(torch, T, synth, formats, orc)
-        torch.cuda.empty_cache()
-        extra["c4"] = bench_c4(torch, T, synth, formats, orc)
-        torch.cuda.empty_cache()
-        extra["c5"] = bench_c5(torch, T, synth, formats, orc)
-        torch.cuda.empty_cache()
-        extra["c6"] = bench_c6(torch, T, synth, formats, orc)
-        torch.cuda.empty_cache()
-        extra["int8_gemv"] = bench_c7(torch, T, synth, formats, orc)
-        torch.cuda.empty_cache()
+        for key, fn in (("prefill", bench_c3), ("c1", bench_c1), ("c4", bench_c4), ("c5", bench_c5),
+                        ("c6", bench_c6), ("int8_gemv", bench_c7)):
+            extra[key] = fn(torch, T, synth, formats, orc)
+            torch.cuda.empty_cache()
+            progress(f"{key} done")
     if not args.no_ref_shapes:
         extra["ref_shapes"] = bench_ref_shapes(torch, T, synth, formats, orc)
         torch.cuda.empty_cache()
@@ -960,6 +963,7 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_sample_s)
+        progress("cpu baseline done")
     print(json.dumps(line), flush=True)
 
 
