@@ -221,9 +221,10 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
     }
     if (ksw > 1) {
         // this workgroup's sums, then the strip's counter; the last of the ksw
-        // workgroups adds them in order (device-scope stores and loads:
-        // coherent across the XCDs' L2s without a cache write-back; the wait
-        // orders the stores before the counter)
+        // workgroups adds them in order: agent-scope stores completed
+        // (s_waitcnt) before the counter's atomic, agent-scope loads after its
+        // result is tested, no fences -- the int2 GEMV's K-split handoff and
+        // its reasoning (int2_gemv_f4.hip)
         if (n < N)
 #pragma unroll
             for (int r = 0; r < MR; ++r)
@@ -233,7 +234,6 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
         __builtin_amdgcn_s_waitcnt(0);
         const uint32_t prev = split_arrive(cnt + blockIdx.x, ksw, lane);
         if (prev != (uint32_t)(ksw - 1)) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // only the workgroup that adds the sums
         // 16 / MR workgroups' sums in flight at a time (past ksw clamped, loaded
         // and not added), added in order
         constexpr int U = 16 / MR;
