@@ -114,7 +114,8 @@ def workspace_zero(ws, stream=None) -> None:
 
 
 GemvTile = _abi.GemvTile
-VALU, MFMA, GEMM, F4 = 1, 2, 3, 4  # engines: VALU GEMV, MFMA GEMV, MFMA prefill GEMM, fp8 x fp4 GEMV
+VALU, MFMA, GEMM, F4, F4MS = 1, 2, 3, 4, 5  # engines: VALU GEMV, MFMA GEMV, MFMA prefill GEMM,
+# fp8 x fp4 GEMV, its multi-strip form (M = 1)
 
 
 def gemv_tile(engine: int = 0, waves: int = 0, cols_per_lane: int = 0, groups_per_wave: int = 0,

@@ -51,6 +51,10 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
                                 int out_f32, int waves, int cpl, int gpw, int ks, void *ws, size_t ws_bytes,
                                 hipStream_t st);
 size_t int2_gemv_f4_ws_need(int M, int N, int K);
+ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
+                                  const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                  int out_f32, int cpl, hipStream_t st);
+bool int2_gemv_f4ms_auto(int M, int N, int K);
 ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 ternocl_status stream_read_run(const void *src, size_t bytes, void *sink, hipStream_t st);  // misc.hip
 ternocl_status int2_gemv_stream_probe_run(int dtype, const uint32_t *B, const void *S, void *C, int M, int N,
@@ -194,7 +198,7 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
     ternocl_status s = check_gemm_common(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32);
     if (s != TERNOCL_OK) return s;
     const ternocl_gemv_tile t = tile ? *tile : ternocl_gemv_tile{0, 0, 0, 0, 0, 0};
-    if (t.engine < 0 || t.engine > 4) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..4");
+    if (t.engine < 0 || t.engine > 5) FAIL(TERNOCL_ERR_INVALID_ARG, "tile engine must be 0..5");
     if (t.k_slices < 0 || t.k_slices > 16) FAIL(TERNOCL_ERR_INVALID_ARG, "k_slices must be 0..16");
     if (t.engine == 3 || (M > 16 && t.engine == 0)) {
         if (t.k_slices > 1) FAIL(TERNOCL_ERR_INVALID_ARG, "k_slices > 1: the fp8 x fp4 GEMV (engine 4) only");
@@ -205,7 +209,19 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
                                   (hipStream_t)stream, ws, ws_bytes);
     }
     if (M <= 16) {
-        // automatic: the fp8 x fp4 engine where it applies, else the bf16/fp16 MFMA GEMV
+        // automatic: the fp8 x fp4 engine where it applies (its multi-strip
+        // kernel for M = 1 on many strips), else the bf16/fp16 MFMA GEMV
+        const bool auto_tile = t.engine == 0 && t.waves == 0 && t.cols_per_lane == 0 && t.groups_per_wave == 0 &&
+                               t.k_slices == 0;
+        if (t.engine == 5 || (auto_tile && int2_gemv_f4_supports(M, N, A) && int2_gemv_f4ms_auto(M, N, K))) {
+            if (t.waves || t.groups_per_wave || t.k_slices > 1)
+                FAIL(TERNOCL_ERR_INVALID_ARG, "the multi-strip GEMV (engine 5) takes cols_per_lane only "
+                                              "(its waves follow from K)");
+            if (!int2_gemv_f4_supports(M, N, A))
+                FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the multi-strip GEMV takes M = 1 and A 16-byte aligned");
+            return int2_gemv_f4ms_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.cols_per_lane,
+                                      (hipStream_t)stream);
+        }
         if (t.engine == 4 || (t.engine == 0 && int2_gemv_f4_supports(M, N, A)))
             return int2_gemv_f4_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,
                                     t.cols_per_lane, t.groups_per_wave, t.k_slices, ws, ws_bytes,

@@ -59,6 +59,7 @@
 // the result does not depend on the order the workgroups run in.
 #include "common.hpp"
 
+#include <algorithm>
 #include <climits>
 
 namespace tcl {
@@ -405,7 +406,7 @@ struct F4Group {
 // ksn > 1 (the plain GEMV, DT or int8, grid.y = ksn): K slice blockIdx.y; part fp32
 // [ksn][M][N] slice sums, cnt one zero-initialised counter per strip (left at
 // zero again).
-template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0, bool DS = false>
+template <int MR, int CPL, int GPW, bool BF16, bool GRP = false, int QM = 0, bool DS = false, bool MW = false>
 __global__ void __launch_bounds__(64 * f4_max_waves(MR, CPL))
 k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                const uint16_t *__restrict__ S, void *__restrict__ C,
@@ -495,15 +496,17 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 #pragma unroll
             for (int i = 0; i < ROWS; ++i) acc[t][j][i] = 0.0f;
 
-    for (int win = 0; win < windows; ++win) {
+    // One window: its MFMAs and group FMAs; PRE: first the next window's loads,
+    // unconditional -- loads under a branch are waited for at the branch's
+    // end, which would serialise them with this window's work.
+    auto window = [&](int win, auto PRE_, F4Slab<CPL, GPW> &cu, F4Slab<CPL, GPW> &nx) __attribute__((always_inline)) {
+        constexpr bool PRE = decltype(PRE_)::value;
         asm volatile("" ::: "memory");  // staging writes precede the reads (in-order LDS per wave)
         const uint8_t *buf = wlds + (size_t)(win & 1) * WB;
-        const bool more = win + 1 < windows;
-        F4Slab<CPL, GPW> nxt;
-        if (more) {
+        if constexpr (PRE) {
             if constexpr (!NODEC) st.load(A, M, K, groups, (win + 1) * gw + g0w, lane, SA, ldsa);
             after = f4_loads_after_barrier();
-            nxt.load(B + after, S + after, N, groups, (win + 1) * gw + g0w, q, n0);
+            nx.load(B + after, S + after, N, groups, (win + 1) * gw + g0w, q, n0);
         }
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
@@ -512,7 +515,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             if constexpr (NODEC) {
 #pragma unroll
                 for (int j = 0; j < CPL; ++j)
-                    acc[0][j][0] += (float)(cur.w[gi][0].v[j] ^ cur.w[gi][1].v[j]) * dt2f<BF16>(cur.scale(gi, j));
+                    acc[0][j][0] += (float)(cu.w[gi][0].v[j] ^ cu.w[gi][1].v[j]) * dt2f<BF16>(cu.scale(gi, j));
                 continue;
             }
             v8i_t av[RSETS];
@@ -532,14 +535,14 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             for (int j = 0; j < CPL; ++j) {
                 uint32_t d0, d1, e0, e1;
                 if constexpr (I8) {
-                    f4_decode_s2(cur.w[gi][0].v[j], d0, d1);
-                    f4_decode_s2(cur.w[gi][1].v[j], e0, e1);
+                    f4_decode_s2(cu.w[gi][0].v[j], d0, d1);
+                    f4_decode_s2(cu.w[gi][1].v[j], e0, e1);
                 } else {
-                    f4_decode(cur.w[gi][0].v[j], d0, d1);
-                    f4_decode(cur.w[gi][1].v[j], e0, e1);
+                    f4_decode(cu.w[gi][0].v[j], d0, d1);
+                    f4_decode(cu.w[gi][1].v[j], e0, e1);
                 }
                 const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
-                const float s = dt2f<BF16>(cur.scale(gi, j));
+                const float s = dt2f<BF16>(cu.scale(gi, j));
 #pragma unroll
                 for (int t = 0; t < RSETS; ++t) {
                     const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
@@ -554,11 +557,40 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 }
             }
         }
-        if (more) {
+        if constexpr (PRE) {
             asm volatile("" ::: "memory");
             uint8_t *nb = wlds + (size_t)((win + 1) & 1) * WB;
             if constexpr (!NODEC) st.store(nb, lane);
-            cur = nxt;
+        }
+    };
+    if constexpr (!MW) {
+        // one window (the host's choice for one), or the group modes: a next
+        // window loaded under a branch and copied into place
+        for (int win = 0; win < windows; ++win) {
+            F4Slab<CPL, GPW> nxt;
+            if (win + 1 < windows) {
+                window(win, std::true_type{}, cur, nxt);
+                cur = nxt;
+            } else {
+                window(win, std::false_type{}, cur, nxt);
+            }
+        }
+    } else {
+        F4Slab<CPL, GPW> cur2;
+        // two register sets used in turn (ping-pong): a copy of the next
+        // window's registers into the current ones would wait for their
+        // loads; the last window loads nothing (uniform tests, no loads inside)
+        for (int win = 0;; win += 2) {
+            window(win, std::true_type{}, cur, cur2);
+            if (win + 2 == windows) {
+                window(win + 1, std::false_type{}, cur2, cur);
+                break;
+            }
+            window(win + 1, std::true_type{}, cur2, cur);
+            if (win + 3 == windows) {
+                window(win + 2, std::false_type{}, cur, cur2);
+                break;
+            }
         }
     }
 
@@ -697,15 +729,158 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     });
 }
 
+// ---- multi-strip decode GEMV (engine 5: M = 1, all of K in one window) ----
+// The kernel above stages the activation pieces in every workgroup, i.e. once
+// per 16- or 32-column strip: at N = 151680 that is 4740 times the same
+// vector, and the staging's VALU work, not HBM, bounds the launch.  Here a
+// workgroup stages them once and keeps each wave's A fragments (its GPW
+// groups, all of K across the W waves) in registers, then walks the strips
+// s = blockIdx.x, + gridDim.x, ... of 16 columns: the next strip's weight
+// words, scales and epilogue operands are loaded while the current strip's
+// MFMAs run, the wave partials meet in LDS (two buffers, one barrier per
+// strip) and wave it % W adds them in wave order and stores the strip.  The
+// per-column arithmetic (pieces, MFMA, per-group FMA in group order, wave
+// order) is the kernel above's with the same waves and groups per wave: the
+// same bits.
+template <int GPW, int CPL, bool BF16>
+__global__ void __launch_bounds__(64 * 16)
+k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
+                 const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
+                 const void *__restrict__ Bias, int N, int K, int postop, int out_f32) {
+    constexpr int RR = kF4RowStride, P = f4_pieces(BF16);
+    constexpr int WB = f4_window_bytes(RR, GPW);
+    extern __shared__ uint8_t lds8[];
+    const int W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int c = lane & 15, q = lane >> 4;
+    const int groups = K / kGS, g0w = wave * GPW;  // (the host keeps groups <= W GPW)
+    const int strips = N / (16 * CPL);
+    int s = blockIdx.x;
+    if (s >= strips) return;  // (whole workgroup)
+    uint8_t *wlds = lds8 + (size_t)wave * WB;
+    float *red = (float *)(lds8 + (size_t)W * WB);  // [2][W][CPL][16]
+
+    F4Stage<1, GPW, BF16, 0> st;
+    st.load(A, 1, K, groups, g0w, lane);
+    int after = f4_loads_after_barrier();
+    F4Slab<CPL, GPW> cur;
+    cur.load(B + after, S + after, N, groups, g0w, q, s * 16 * CPL + CPL * c);
+    F4EpiIn<1, CPL, BF16> ein;
+    ein.load(Other, Bias, postop, out_f32, 1, N, q, s * 16 * CPL + CPL * c, wave == 0);
+    st.store(wlds, lane);
+    asm volatile("" ::: "memory");  // this wave's staging writes precede its reads (in-order LDS per wave)
+    const int rho = c & (RR - 1);
+    v8i_t av[GPW];
+    int sa[GPW];
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) {
+        const int pr = gi * RR + rho;
+        const uint8_t *row = wlds + pr * 128 + 32 * q;
+        const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
+        sa[gi] = wlds[GPW * RR * 128 + pr * 4 + q];
+        av[gi] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+    }
+    // Strips in pairs with two register sets (ping-pong): a copy of the next
+    // strip's registers into the current ones would wait for their loads.
+    F4Slab<CPL, GPW> cur2;
+    F4EpiIn<1, CPL, BF16> ein2;
+    int it = 0;
+    // PRE: the next strip's loads first, unconditional (loads under a branch
+    // are waited for at the branch's end, which would serialise them with this
+    // strip's work); the last strip of the workgroup loads nothing.
+    auto strip = [&](F4Slab<CPL, GPW> &cu, F4EpiIn<1, CPL, BF16> &ec, F4Slab<CPL, GPW> &nx,
+                     F4EpiIn<1, CPL, BF16> &en, auto PRE_) __attribute__((always_inline)) {
+        const int sn = s + (int)gridDim.x;
+        if constexpr (decltype(PRE_)::value) {
+            nx.load(B, S, N, groups, g0w, q, sn * 16 * CPL + CPL * c);
+            en.load(Other, Bias, postop, out_f32, 1, N, q, sn * 16 * CPL + CPL * c, wave == (it + 1) % W);
+        }
+        float acc[CPL][P];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < P; ++i) acc[j][i] = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            if (g0w + gi >= groups) break;  // uniform across the wave
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                uint32_t d0, d1, e0, e1;
+                f4_decode(cu.w[gi][0].v[j], d0, d1);
+                f4_decode(cu.w[gi][1].v[j], e0, e1);
+                const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
+                const float sc = dt2f<BF16>(cu.scale(gi, j));
+                const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    av[gi], bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa[gi], 0, 127);
+#pragma unroll
+                for (int i = 0; i < P; ++i) acc[j][i] = d[i] * sc + acc[j][i];
+            }
+        }
+        float *rb = red + (size_t)(it & 1) * W * CPL * 16;
+        if (q == 0) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                float out = acc[j][0];
+#pragma unroll
+                for (int i = 1; i < P; ++i) out += acc[j][i];
+                rb[(wave * CPL + j) * 16 + c] = out * 0.5f;  // the fp4 operand held 2v
+            }
+        }
+        __syncthreads();
+        if (wave == it % W && q == 0) {  // (wave-uniform) this strip's reducer
+            float sum[CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) sum[j] = rb[j * 16 + c];
+            for (int w2 = 1; w2 < W; ++w2)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) sum[j] += rb[(w2 * CPL + j) * 16 + c];
+            const int n0 = s * 16 * CPL + CPL * c;
+            epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+                constexpr int PO = decltype(P_)::value;
+                constexpr bool F32 = decltype(F_)::value;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const float r = epi_apply_c<PO>(sum[j], ec.other(0, j), ec.bias(j, F32));
+                    if constexpr (F32) ((float *)C)[n0 + j] = r;
+                    else ((uint16_t *)C)[n0 + j] = (uint16_t)f2dt<BF16>(r);
+                }
+            });
+        }
+        ++it;
+        s = sn;
+    };
+    const int G = (int)gridDim.x;
+    for (;;) {  // (uniform tests)
+        if (s + G >= strips) {
+            strip(cur, ein, cur2, ein2, std::false_type{});
+            break;
+        }
+        strip(cur, ein, cur2, ein2, std::true_type{});
+        if (s + G >= strips) {
+            strip(cur2, ein2, cur, ein, std::false_type{});
+            break;
+        }
+        strip(cur2, ein2, cur, ein, std::true_type{});
+    }
+}
+
 struct F4Plan {
     int cpl, waves, gpw, mr;
     size_t lds;
+    int windows = 1;           // LDS windows per workgroup (its K slice / (waves x gpw))
     int ks = 1;                // K slices (workgroups per strip)
     float *part = nullptr;     // ks > 1: slice sums fp32 [ks][M][N] ...
     uint32_t *cnt = nullptr;   // ... and a counter per strip (workspace)
 };
 
 constexpr size_t kF4MaxLds = 96 * 1024;
+// The automatic plan of an M = 1 GEMV takes the multi-strip kernel from this
+// many 32-column strips on (graph-timed against the one-strip kernel over the
+// reference's benchmark shapes: K = N = 4096, 128 strips, 4.28 against 4.17 us;
+// K = 6144 N = 5120, 160 strips, 5.16 against 6.85 us; K = 4096 N = 14336
+// 6.37 against 6.82 us; K = 5120 N = 248320 72.0 against 100.8 us).
+constexpr int kF4msMinStrips = 160;
+constexpr int kF4msCpl = 2;  // its columns per lane (4: too many registers, measured slower)
 
 int f4_mr(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -749,6 +924,7 @@ F4Plan f4_plan(bool bf16, int M, int N, int K, int waves, int cpl, int gpw, int 
     p.waves = bw;
     p.gpw = bg;
     p.lds = f4_lds(MR, bw, bg, p.cpl, groups);
+    p.windows = (groups + bw * bg - 1) / (bw * bg);
     return p;
 }
 
@@ -761,9 +937,17 @@ hipError_t f4_launch_t(const F4Plan &p, const void *A, const uint32_t *B, const 
     } else {
         const int strips = N / (16 * CPL);
         const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
-        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QMODE>), dim3(strips, p.ks), dim3(64 * p.waves),
-                           p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other,
-                           Bias, M, N, K, postop, out_f32, swz, F4Group{}, nullptr, 0, p.ks, p.part, p.cnt);
+        // (several windows: the form that keeps the next window's loads in flight)
+        if (p.windows > 1)
+            hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QMODE, false, true>), dim3(strips, p.ks),
+                               dim3(64 * p.waves), p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C,
+                               (const uint16_t *)Other, Bias, M, N, K, postop, out_f32, swz, F4Group{}, nullptr, 0,
+                               p.ks, p.part, p.cnt);
+        else
+            hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QMODE>), dim3(strips, p.ks),
+                               dim3(64 * p.waves), p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C,
+                               (const uint16_t *)Other, Bias, M, N, K, postop, out_f32, swz, F4Group{}, nullptr, 0,
+                               p.ks, p.part, p.cnt);
         return hipGetLastError();
     }
 }
@@ -845,9 +1029,15 @@ hipError_t f4q_launch_t(const F4Plan &p, const void *A, const void *SA, int ldsa
                         int postop, int out_f32, hipStream_t st) {
     const int strips = N / (16 * CPL);
     const int swz = (CPL == 1 && strips % 16 == 0) ? 1 : 0;
-    hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QM>), dim3(strips, p.ks), dim3(64 * p.waves),
-                       p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M,
-                       N, K, postop, out_f32, swz, F4Group{}, (const uint16_t *)SA, ldsa, p.ks, p.part, p.cnt);
+    if (p.windows > 1)
+        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QM, false, true>), dim3(strips, p.ks),
+                           dim3(64 * p.waves), p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C,
+                           (const uint16_t *)Other, Bias, M, N, K, postop, out_f32, swz, F4Group{}, (const uint16_t *)SA,
+                           ldsa, p.ks, p.part, p.cnt);
+    else
+        hipLaunchKernelGGL((k_int2_gemv_f4<MR, CPL, GPW, BF16, false, QM>), dim3(strips, p.ks), dim3(64 * p.waves),
+                           p.lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M,
+                           N, K, postop, out_f32, swz, F4Group{}, (const uint16_t *)SA, ldsa, p.ks, p.part, p.cnt);
     return hipGetLastError();
 }
 
@@ -943,6 +1133,63 @@ void f4_auto_split(int M, int N, int K, int cpl_req, int &cpl, int &ks) {
     while (k < 16 && (double)groups / 28.0 > k * 1.4142) k *= 2;
     cpl = c;
     ks = f4_slices(groups, k);
+}
+
+// The multi-strip GEMV's plan for K: groups per wave (1, 2 or 4) and waves
+// (<= 16) holding all of K in one window; 0 waves: K too long (> 64 groups).
+void f4ms_plan(int K, int &gpw, int &waves) {
+    const int groups = K / kGS;
+    gpw = groups >= 32 ? 4 : groups >= 16 ? 2 : 1;
+    waves = (groups + gpw - 1) / gpw;
+    if (waves > 16) waves = 0;
+}
+size_t f4ms_lds(int gpw, int waves, int cpl) {
+    return (size_t)waves * f4_window_bytes(kF4RowStride, gpw) + (size_t)2 * waves * cpl * 16 * 4;
+}
+
+// cpl: columns per lane (1, 2 or 4; 0 = automatic), strips of 16 cpl columns;
+// 512 workgroups (two per CU), at most one per strip.
+ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
+                                  const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                  int out_f32, int cpl, hipStream_t st) {
+    constexpr int wgs = 512;
+    int gpw, waves;
+    f4ms_plan(K, gpw, waves);
+    if (cpl == 0) cpl = N % (16 * kF4msCpl) == 0 ? kF4msCpl : N % 32 == 0 ? 2 : 1;
+    if (M != 1 || waves == 0 || (cpl != 1 && cpl != 2 && cpl != 4) || N % (16 * cpl)) {
+        set_error("the multi-strip GEMV (engine 5) takes M = 1, K <= 8192, cols_per_lane 1, 2 or 4 and "
+                  "N % (16 * cols_per_lane) == 0");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    const int strips = N / (16 * cpl);
+    const dim3 grid(std::min(strips, wgs)), block(64 * waves);
+    const size_t lds = f4ms_lds(gpw, waves, cpl);
+    const uint16_t *a = (const uint16_t *)A, *s = (const uint16_t *)S, *o = (const uint16_t *)Other;
+#define TCL_F4MS(G, CP, BF)                                                                                    \
+    hipLaunchKernelGGL((k_int2_gemv_f4ms<G, CP, BF>), grid, block, lds, st, a, B, s, C, o, Bias, N, K, postop, \
+                       out_f32)
+#define TCL_F4MS_C(G, BF)            \
+    do {                             \
+        if (cpl == 4) TCL_F4MS(G, 4, BF); \
+        else if (cpl == 2) TCL_F4MS(G, 2, BF); \
+        else TCL_F4MS(G, 1, BF);     \
+    } while (0)
+    const bool bf16 = dtype == TERNOCL_BF16;
+    if (gpw == 4) { if (bf16) TCL_F4MS_C(4, true); else TCL_F4MS_C(4, false); }
+    else if (gpw == 2) { if (bf16) TCL_F4MS_C(2, true); else TCL_F4MS_C(2, false); }
+    else { if (bf16) TCL_F4MS_C(1, true); else TCL_F4MS_C(1, false); }
+#undef TCL_F4MS_C
+#undef TCL_F4MS
+    return launch_status(hipGetLastError());
+}
+
+// Whether the automatic choice for an M = 1 GEMV is the multi-strip kernel:
+// many strips per CU (the staging it saves grows with them) and all of K in
+// one window.
+bool int2_gemv_f4ms_auto(int M, int N, int K) {
+    int gpw, waves;
+    f4ms_plan(K, gpw, waves);
+    return M == 1 && waves > 0 && N % (16 * kF4msCpl) == 0 && N / (16 * kF4msCpl) >= kF4msMinStrips;
 }
 
 // Workspace bytes of the automatic plan (0: no K split).

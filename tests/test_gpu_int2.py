@@ -365,3 +365,91 @@ def test_gemv_f4_wide_dynamic_range(dev, orc, bf16):
     _, acc = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 0, True)
     bad, dmax = allclose_report(host_f32(dC), acc)
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+# ---- the multi-strip GEMV (engine 5, M = 1) ----------------------------------------
+# (K, N): one window of waves x groups per wave covering K (1, 2 and 4 groups per
+# wave, up to 16 waves), fewer strips than workgroups, many strips per workgroup,
+# the two reference LM heads (int2_fp16_upcvt/bench.sh:12) and a 129-strip N
+MULTISTRIP = [(128, 16), (256, 48), (1024, 2064), (2048, 40960), (4096, 14336), (5120, 34816),
+              (8192, 4096), (4096, 151680), (5120, 248320)]
+
+
+def _ms_plan(K):
+    groups = K // 128
+    gpw = 4 if groups >= 32 else 2 if groups >= 16 else 1
+    return gpw, (groups + gpw - 1) // gpw
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("K,N", MULTISTRIP)
+def test_gemv_multistrip_parity(dev, orc, K, N, bf16):
+    """Engine 5 gives engine 4's bits when engine 4 runs the same waves and groups per
+    wave on 16-column strips (the same per-column arithmetic in the same order), with
+    and without the bias + residual epilogue, and every output within 1e-3 + 1e-2 |ref|
+    of the host gold."""
+    import ternocl_amd as T
+    M = 1
+    gpw, waves = _ms_plan(K)
+    print(f"gemv multi-strip K={K} N={N} bf16={bf16} (waves {waves} x {gpw} groups)", flush=True)
+    A, B, S, other, bias_f = _inputs(77 + K + N, M, K, N, bf16)
+    for postop, cpl in ((0, 0), (5, 1), (5, 2), (5, 4)):
+        if N % (16 * max(cpl, 1)):
+            continue
+        ms, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
+                     tile=T.gemv_tile(T.F4MS, 0, cpl))
+        f4, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
+                     tile=T.gemv_tile(T.F4, waves, 1, gpw, 0, 1))
+        assert np.array_equal(host_u16(ms), host_u16(f4)), f"postop {postop}: engine 5 differs from engine 4"
+        want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, False)
+        bad, dmax = allclose_report(formats.dt_to_f32(host_u16(ms), bf16), formats.dt_to_f32(want, bf16))
+        assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("postop,out_f32", [(1, False), (2, True), (3, True), (4, False)])
+def test_gemv_multistrip_epilogues(dev, orc, postop, out_f32):
+    import torch
+    import ternocl_amd as T
+    M, K, N, bf16 = 1, 4096, 40960, True
+    A, B, S, other, bias_f = _inputs(91 + postop, M, K, N, bf16)
+    dC, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32, tile=T.gemv_tile(T.F4MS))
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, out_f32)
+    if out_f32:
+        bad, dmax = allclose_report(host_f32(dC), want)
+    else:
+        bad, dmax = allclose_report(formats.dt_to_f32(host_u16(dC), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+def test_gemv_multistrip_automatic_and_rejects(dev):
+    """The automatic plan takes engine 5 at M = 1 from 160 strips of 32 columns (the same
+    bits as the explicit engine); engine 5 rejects M > 1, K past one window (64 groups)
+    and tile fields other than cols_per_lane."""
+    import torch
+    import ternocl_amd as T
+    K, N = 4096, 5120
+    A = torch.randn((1, K), device="cuda").to(torch.bfloat16)
+    B = torch.randint(-2**31, 2**31 - 1, (K // 16, N), dtype=torch.int32, device="cuda")
+    S = (torch.rand((K // 128, N), device="cuda") * 0.01).to(torch.bfloat16)
+    c0 = torch.zeros((1, N), dtype=torch.bfloat16, device="cuda")
+    c1 = torch.ones((1, N), dtype=torch.bfloat16, device="cuda")
+    T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K)
+    T.int2_fp16_upcvt_gemm(A, B, S, c1, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS))
+    torch.cuda.synchronize()
+    assert torch.equal(c0, c1)
+    A2 = torch.zeros((2, K), dtype=torch.bfloat16, device="cuda")
+    C2 = torch.zeros((2, N), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(A2, B, S, C2, None, None, 2, N, K, tile=T.gemv_tile(T.F4MS))
+    assert e.value.status == 2
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS, 8))
+    assert e.value.status == 1
+    K2 = 8320
+    A3 = torch.zeros((1, K2), dtype=torch.bfloat16, device="cuda")
+    B3 = torch.zeros((K2 // 16, 64), dtype=torch.int32, device="cuda")
+    S3 = torch.zeros((K2 // 128, 64), dtype=torch.bfloat16, device="cuda")
+    C3 = torch.zeros((1, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(A3, B3, S3, C3, None, None, 1, 64, K2, tile=T.gemv_tile(T.F4MS))
+    assert e.value.status == 2
