@@ -498,7 +498,8 @@ def bench_c3(torch, T, synth, formats, orc):
 def bench_c4(torch, T, synth, formats, orc):
     """FWHT (HB 512) + BITCOS GEMV M=1 K=5376 N=21504 fp16 at z = .3 / .5 / .7."""
     M, K, N, HB, bf16 = 1, 5376, 21504, 512, False
-    out = {"workload": "sign flip + FWHT HB=512, then BITCOS GEMV M=1 K=5376 N=21504 fp16"}
+    out = {"workload": "sign flip + FWHT HB=512, then BITCOS GEMV M=1 K=5376 N=21504 fp16; us = the transform "
+                       "fused into the GEMV launch, two_launch_us = FWHT and GEMV as two launches"}
     for z in (0.3, 0.5, 0.7):
         g = synth.rng(44 + int(10 * z))
         x = synth.activations(g, (M, K), bf16)
@@ -525,9 +526,14 @@ def bench_c4(torch, T, synth, formats, orc):
             it[0] += 1
             T.bitcos_fp16_upcvt_gemm(dy, b, sc, sr, dC, None, None, M, N, K, ls, ws=ws)
 
-        def call():
+        def call():  # the two launches, as the reference runs them
             fwht()
             gemv()
+
+        def fused():  # the transform inside the GEMV (ternocl_bitcos_fwht_gemm_ws)
+            b, sc, sr = W[it[0] % sets]
+            it[0] += 1
+            T.bitcos_fwht_gemm(dx, ds, HB, b, sc, sr, dC, None, None, M, N, K, ls, ws=dws)
         call()
         torch.cuda.synchronize()
         y = orc.fwht(x, sgn, M, K, HB, True, bf16)
@@ -536,12 +542,19 @@ def bench_c4(torch, T, synth, formats, orc):
                                               bf16), bf16)
         got = formats.dt_to_f32(dC.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
         bad = int((np.abs(got - want) > 1e-3 + 1e-2 * np.abs(want)).sum())
-        us = graph_time_us(torch, call, 200)
+        two = dC.clone()
+        it[0] = 0
+        fused()
+        torch.cuda.synchronize()
+        fused_same = bool(torch.equal(dC, two))
+        us2 = graph_time_us(torch, call, 200)
+        us = graph_time_us(torch, fused, 200)
         g_us = graph_time_us(torch, gemv, 200)
         g1_us = graph_time_us(torch, lambda: gemv(None), 200)  # one workgroup per strip
         f_us = graph_time_us(torch, fwht, 200)
         nbytes = M * K * 2 + buf.nbytes + S.nbytes + M * N * 2  # bitcos_fp16_upcvt/main.cpp:289-291
-        out[f"z{z}"] = {"us": round(us, 2), "gemv_us": round(g_us, 2), "gemv_unsplit_us": round(g1_us, 2),
+        out[f"z{z}"] = {"us": round(us, 2), "two_launch_us": round(us2, 2), "fused_bits_equal_two_launch": fused_same,
+                        "gemv_us": round(g_us, 2), "gemv_unsplit_us": round(g1_us, 2),
                         "fwht_us": round(f_us, 2),
                         "gemv_GB/s": round(nbytes / g_us / 1e3, 1),
                         "gemv_hbm_frac": round(nbytes / g_us / 1e3 / HBM_PEAK_GBS, 4),

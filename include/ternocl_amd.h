@@ -250,6 +250,21 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_ws(int dtype, const void *A, const
                                                  const void *Other, const void *Bias, int M, int N,
                                                  int K, int postop, int out_f32, void *ws, size_t ws_bytes,
                                                  void *stream);
+/* The decode step's sign flip + Hadamard transform and BITCOS GEMV in one
+ * launch (no reference counterpart: the reference runs hadamard_fwht,
+ * hadamard/hadamard_fwht.cl:62-115, then bitcos_fp16_upcvt_gemv): the same C,
+ * bit for bit, as ternocl_hadamard_fwht(x, signs, y, M, K, HB, use_signs)
+ * followed by ternocl_bitcos_fp16_upcvt_gemm_ws(y, ...), without writing y.
+ * Each workgroup transforms the HB-blocks its K range reads, one wave per
+ * block, in the transform's own operation order.  x: DT [M, K], 16-byte
+ * aligned; signs: int8 [K], 8-byte aligned, read when use_signs; HB 256 or
+ * 512 with K % HB 0 or a power of two >= 8 (that tail transformed as one
+ * block, as ternocl_hadamard_fwht does).  B, S, SR, ls, ws and the rest as
+ * ternocl_bitcos_fp16_upcvt_gemm_ws. */
+ternocl_status ternocl_bitcos_fwht_gemm_ws(int dtype, const void *x, const int8_t *signs, int HB, int use_signs,
+                                          const uint32_t *B, const void *S, const uint32_t *SR, int ls, void *C,
+                                          const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                          int out_f32, void *ws, size_t ws_bytes, void *stream);
 /* ---- BITCOS M-tiled prefill ---------------------------------------------
  * Replaces bitcos_fp16_upcvt_gemm_mt (bitcos_fp16_upcvt/bitcos_fp16_upcvt.cl:303-305):
  * the same C as ternocl_bitcos_fp16_upcvt_gemm (within the float tolerance) for

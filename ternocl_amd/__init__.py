@@ -25,7 +25,7 @@ __all__ = [
     "int2_gemv_decode", "int2_gemv_stream_probe", "stream_read_probe", "gemv_tile", "GemvTile", "VALU", "MFMA", "GEMM",
     "int2_pack", "int2_unpack", "bitcos_pack", "bitcos_unpack", "bitcos_slice_ranks_host",
     "ldsa", "quant_a", "int2_int8_gemm", "int2_int8_gemm_ws_bytes", "int2_s8_decode",
-    "bitcos_fp16_upcvt_gemm", "bitcos_gemv_ws_bytes", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
+    "bitcos_fp16_upcvt_gemm", "bitcos_fwht_gemm", "bitcos_gemv_ws_bytes", "bitcos_slice_ranks", "bitcos_pick_ls", "bitcos_dequant",
     "hadamard_fwht",
     "moe_tile_rows", "int2_moe_route", "int2_moe_gather", "int2_moe_gemm", "int2_moe_combine",
     "int2_moe_prefill_ws_bytes", "int2_moe_prefill", "int2_moe_prefill_int8_ws_bytes", "int2_moe_prefill_int8",
@@ -287,6 +287,16 @@ def bitcos_fp16_upcvt_gemm(A, B, S, SR, C, Other, Bias, M: int, N: int, K: int, 
                                                        _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
                                                        int(bool(out_f32)), _ptr(ws), _nbytes(ws),
                                                        _stream(stream)))
+
+
+def bitcos_fwht_gemm(x, signs, HB: int, B, S, SR, C, Other, Bias, M: int, N: int, K: int, ls: int = 1,
+                     postop: int = 0, out_f32: bool = False, ws=None, use_signs: bool = True, stream=None) -> None:
+    """The decode step's sign flip + FWHT (hadamard_fwht.cl:62) and BITCOS GEMV (bitcos_fp16_upcvt.cl:179)
+    in one launch: the C of hadamard_fwht(x, signs, y) then bitcos_fp16_upcvt_gemm(y, ...), bit for bit,
+    without y.  ``ws``: as bitcos_fp16_upcvt_gemm (bitcos_gemv_ws_bytes, zeroed once)."""
+    _check(lib().ternocl_bitcos_fwht_gemm_ws(_dtype_of(x), _ptr(x), _ptr(signs), HB, int(bool(use_signs)), _ptr(B),
+                                             _ptr(S), _ptr(SR), ls, _ptr(C), _ptr(Other), _ptr(Bias), M, N, K, postop,
+                                             int(bool(out_f32)), _ptr(ws), _nbytes(ws), _stream(stream)))
 
 
 def bitcos_gemm_mt_ws_bytes(K: int, N: int) -> int:

@@ -31,6 +31,7 @@ SYMBOLS: dict[str, tuple] = {
     "ternocl_int2_dequant": (I, [I, P, P, P, I, I, P]),
     "ternocl_int2_gemv_decode": (I, [I, I, P, P, I, I, P]),
     "ternocl_int2_gemv_stream_probe": (I, [I, P, P, P, I, I, I, P]),
+    "ternocl_bitcos_fwht_gemm_ws": (I, [I, P, P, I, I, P, P, P, I, P, P, P, I, I, I, I, I, P, Z, P]),
     "ternocl_stream_read_probe": (I, [P, Z, P, P]),
     "ternocl_ldsa": (I, [I]),
     "ternocl_quant_a": (I, [I, P, P, P, I, I, P]),

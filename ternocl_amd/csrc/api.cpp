@@ -94,6 +94,11 @@ ternocl_status bitcos_to_int2_run(const uint32_t *Bc, const uint32_t *SR, int ls
 // kernels (hadamard.hip)
 ternocl_status fwht_run(int dtype, const void *x, const int8_t *signs, void *y, int rows, int K,
                         int HB, int use_signs, float scale_full, float scale_tail, hipStream_t st);
+ternocl_status bitcos_fwht_gemv_run(int dtype, const void *x, const int8_t *signs, int HB, int use_signs,
+                                    float scale_full, float scale_tail, const uint32_t *Bc, const void *S,
+                                    const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias, int M,
+                                    int N, int K, int postop, int out_f32, hipStream_t st, void *ws,
+                                    size_t ws_bytes);  // bitcos.hip
 // kernels (moe.hip, int2_gemm_mfma.hip)
 int moe_tile_rows();
 ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st);
@@ -343,6 +348,29 @@ ternocl_status ternocl_bitcos_fp16_upcvt_gemm_ws(int dtype, const void *A, const
     if (ls > 1 && !SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR (slice ranks for ls slices) must be non-null when ls > 1");
     return bitcos_gemv_run(dtype, A, B, S, SR, ls, C, Other, Bias, M, N, K, postop, out_f32,
                            (hipStream_t)stream, ws, ws_bytes);
+}
+
+ternocl_status ternocl_bitcos_fwht_gemm_ws(int dtype, const void *x, const int8_t *signs, int HB, int use_signs,
+                                          const uint32_t *B, const void *S, const uint32_t *SR, int ls, void *C,
+                                          const void *Other, const void *Bias, int M, int N, int K, int postop,
+                                          int out_f32, void *ws, size_t ws_bytes, void *stream) {
+    ternocl_status s = check_gemm_common(dtype, x, B, S, C, Other, Bias, M, N, K, postop, out_f32);
+    if (s != TERNOCL_OK) return s;
+    if (ls < 1 || ls > bitcos_max_ls()) FAIL(TERNOCL_ERR_INVALID_ARG, "ls must be 1..16");
+    if (K % (64 * ls)) FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "BITCOS needs K % (64 * ls) == 0");
+    if (ls > 1 && !SR) FAIL(TERNOCL_ERR_INVALID_ARG, "SR (slice ranks for ls slices) must be non-null when ls > 1");
+    if (use_signs && !signs) FAIL(TERNOCL_ERR_INVALID_ARG, "use_signs needs a signs vector");
+    if (HB < 256 || HB > 512 || (HB & (HB - 1)))
+        FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the fused transform takes HB 256 or 512 (one wave per block)");
+    const int tail = K % HB;
+    if ((tail & (tail - 1)) || (tail && tail < 8))
+        FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the fused transform takes K % HB of 0 or a power of two >= 8");
+    if (((uintptr_t)x & 15) || (use_signs && ((uintptr_t)signs & 7)))
+        FAIL(TERNOCL_ERR_INVALID_ARG, "the fused transform reads x 16-byte and signs 8-byte aligned");
+    const float full = (float)(1.0 / std::sqrt((double)HB));
+    const float part = tail ? (float)(1.0 / std::sqrt((double)tail)) : full;
+    return bitcos_fwht_gemv_run(dtype, x, signs, HB, use_signs ? 1 : 0, full, part, B, S, SR, ls, C, Other, Bias,
+                                M, N, K, postop, out_f32, (hipStream_t)stream, ws, ws_bytes);
 }
 
 ternocl_status ternocl_bitcos_fp16_upcvt_gemm(int dtype, const void *A, const uint32_t *B,

@@ -32,6 +32,8 @@
 // gold (bitcos_fp16_upcvt/main.cpp:64-86).
 #include "common.hpp"
 
+#include <algorithm>
+
 
 namespace tcl {
 namespace {
@@ -83,18 +85,79 @@ __device__ __forceinline__ void bc_decode_word(const uint2 *lut, uint32_t bm, ui
     }
 }
 
+// The sign flip and Hadamard transform fused in front of the GEMV (the decode
+// step's hadamard_fwht + bitcos_fp16_upcvt_gemv, hadamard_fwht.cl:62-115):
+// each workgroup transforms the HB-blocks (HB <= 512: one wave per block) that
+// cover its K range, for its rows, into LDS as DT values -- y = DT(SCALE *
+// H(s .* x)) with k_fwht_r's operations in its order (hadamard.hip), so the
+// GEMV reads the bits a separate transform would have written.
+struct BcFwht {
+    const int8_t *signs;  // int8 [K] (+1 / -1), read when use_signs
+    int HB, use_signs;
+    float scale_full, scale_tail;
+};
+
+// One block of n elements (a power of two, 8 <= n <= 512) of row x in one
+// wave: lane l holds elements 8 l .. 8 l + 7 (lanes past n / 8 idle), strides 1,
+// 2, 4 in registers and 8 .. n / 2 across lanes, as k_fwht_r; the DT results
+// go to d[8 l .. 8 l + 7].
+template <bool BF16>
+__device__ __forceinline__ void bc_fwht_block(const uint16_t *__restrict__ x, const int8_t *__restrict__ sg,
+                                              int n, int use_signs, float sc, uint16_t *d, int lane) {
+    const int e0 = 8 * lane;
+    const bool live = e0 < n;
+    const int ec = live ? e0 : 0;
+    float v[8];
+    const uint4 raw = *(const uint4 *)(x + ec);
+    const uint2 sv = use_signs ? *(const uint2 *)(sg + ec) : make_uint2(0u, 0u);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float f = dt2f<BF16>((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+        if (use_signs) f *= (float)(int8_t)(((i < 4 ? sv.x : sv.y) >> (8 * (i & 3))) & 0xffu);
+        v[i] = f;
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if ((j & h) == 0) {
+                const float a = v[j], c = v[j + h];
+                v[j] = a + c;
+                v[j + h] = a - c;
+            }
+    for (int h = 8; h < n; h <<= 1) {  // partner lane ^ h / 8 holds elements i ^ h
+        const int m = h >> 3;
+        const bool up = (lane & m) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = __shfl_xor(v[j], m);
+            v[j] = up ? p - v[j] : v[j] + p;  // (a + c, a - c) with a the lower element
+        }
+    }
+    if (!live) return;
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)f2dt<BF16>(v[2 * i] * sc) | ((uint32_t)f2dt<BF16>(v[2 * i + 1] * sc) << 16);
+    *(uint4 *)(d + e0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // ksw > 1: workgroup (strip, blockIdx.y) runs slices blockIdx.y * wps ..
 // + wps - 1 (wps = waves per workgroup); wsum fp32 [ksw][MR][N] sums, cnt one
 // zero-initialised counter per strip (left at zero again).
-template <int MR, bool BF16, int BC>
+// FW: A holds the untransformed activations x; the workgroup transforms its
+// K range of rows m0 .. m0 + MR - 1 first (fw), into the dynamic LDS xs.
+template <int MR, bool BF16, int BC, bool FW = false>
 __global__ void __launch_bounds__(64 * kBcMaxLs)
 k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
               const uint16_t *__restrict__ S, const uint32_t *__restrict__ SR, void *__restrict__ C,
               const uint16_t *__restrict__ Other, const void *__restrict__ Bias, int M, int m0, int N,
-              int K, int ls, int postop, int out_f32, int ksw = 1, float *wsum = nullptr, uint32_t *cnt = nullptr) {
+              int K, int ls, int postop, int out_f32, int ksw = 1, float *wsum = nullptr, uint32_t *cnt = nullptr,
+              BcFwht fw = BcFwht{}) {
     __shared__ uint2 lut[256];
     __shared__ float red[kBcMaxLs - 1][MR][64];
-    bc_build_lut<BF16>(lut);
+    extern __shared__ __attribute__((aligned(16))) uint32_t xs[];  // FW: [MR][xlen] DT pairs of the blocks
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -113,7 +176,6 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
     const uint32_t *__restrict__ ar[MR];
 #pragma unroll
     for (int r = 0; r < MR; ++r) ar[r] = (const uint32_t *)(A + (size_t)min(m0 + r, M - 1) * K);
-
     // Blocks of BC 64-row chunks.  A block's bitmap words are loaded one block
     // ahead (the first block's with the slice rank and the stream offset);
     // the block's ranks then follow from them at once, and all of its sign
@@ -141,9 +203,32 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
 #pragma unroll
     for (int r = 0; r < MR; ++r) acc[r] = part[r] = 0.0f;
 
-    uint32_t bm[BC][2];
+    uint32_t bm[BC][2];  // (issued before the transform below: they do not depend on it)
 #pragma unroll
     for (int i = 0; i < BC; ++i) bm_load(i, bm[i]);
+    // FW: the blocks b_lo .. b_hi cover this workgroup's rows [kw0, kw0 + wps slice)
+    // of K; row r's transformed block b sits at xs + r xlen + (b - b_lo) HB / 2
+    int xofs = 0, xlen = 0;
+    if constexpr (FW) {
+        const int kw0 = ks * wps * slice, b_lo = kw0 / fw.HB, b_hi = (kw0 + wps * slice - 1) / fw.HB;
+        xlen = (b_hi - b_lo + 1) * fw.HB / 2;
+        xofs = b_lo * fw.HB / 2;
+        for (int b = b_lo + wave; b <= b_hi; b += wps) {  // (uniform per wave)
+            const int kb = b * fw.HB, nb = min(fw.HB, K - kb);
+            const float sc = nb == fw.HB ? fw.scale_full : fw.scale_tail;
+#pragma unroll
+            for (int r = 0; r < MR; ++r)
+                bc_fwht_block<BF16>(A + (size_t)min(m0 + r, M - 1) * K + kb, fw.signs + kb, nb, fw.use_signs, sc,
+                                    (uint16_t *)(xs + r * xlen) + (kb - b_lo * fw.HB), lane);
+        }
+    }
+    bc_build_lut<BF16>(lut);  // (its barrier also publishes the transformed blocks)
+    // activation pair idx of row r (FW: from the LDS blocks, a broadcast read)
+    auto act = [&](int r, int idx) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (FW) return xs[r * xlen + idx - xofs];
+        else return ar[r][idx];
+    };
+
     for (int b0 = 0; b0 < chunks; b0 += BC) {
         uint32_t rs[BC], q[BC][3], sc[BC], nb[BC][2];
 #pragma unroll
@@ -185,8 +270,8 @@ k_bitcos_gemv(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc,
                     float pr = part[r];
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
-                        pr = dot2<BF16>(e[i].x, ar[r][kd + 2 * i], pr);
-                        pr = dot2<BF16>(e[i].y, ar[r][kd + 2 * i + 1], pr);
+                        pr = dot2<BF16>(e[i].x, act(r, kd + 2 * i), pr);
+                        pr = dot2<BF16>(e[i].y, act(r, kd + 2 * i + 1), pr);
                     }
                     part[r] = pr;
                 }
@@ -385,21 +470,33 @@ int bc_block(int chunks) {
     return chunks % 6 == 0 ? 6 : 8;
 }
 
+// LDS of the fused transform: MR rows of the blocks a workgroup's K range
+// (ls / ksw slices) can touch.
+size_t bc_fw_lds(int MR, int K, int ls, int ksw, int HB) {
+    const int range = K / ls * (ls / ksw);
+    return (size_t)MR * ((range + HB - 1) / HB + 1) * HB * 2;
+}
+
 template <int MR, bool BF16, int BC>
 void bc_launch_b(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                  const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
-                 int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
-    hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16, BC>), dim3((N + 63) / 64, ksw), dim3(64 * (ls / ksw)), 0, st,
-                       (const uint16_t *)A, Bc, (const uint16_t *)S, SR, C, (const uint16_t *)Other, Bias,
-                       M, m0, N, K, ls, postop, out_f32, ksw, part, cnt);
+                 int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st, const BcFwht *fw) {
+    if (fw)
+        hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16, BC, true>), dim3((N + 63) / 64, ksw), dim3(64 * (ls / ksw)),
+                           bc_fw_lds(MR, K, ls, ksw, fw->HB), st, (const uint16_t *)A, Bc, (const uint16_t *)S, SR,
+                           C, (const uint16_t *)Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, *fw);
+    else
+        hipLaunchKernelGGL((k_bitcos_gemv<MR, BF16, BC>), dim3((N + 63) / 64, ksw), dim3(64 * (ls / ksw)), 0, st,
+                           (const uint16_t *)A, Bc, (const uint16_t *)S, SR, C, (const uint16_t *)Other, Bias,
+                           M, m0, N, K, ls, postop, out_f32, ksw, part, cnt);
 }
 
 template <int MR, bool BF16>
 void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                const void *Other, const void *Bias, int M, int m0, int N, int K, int ls, int postop,
-               int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
+               int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st, const BcFwht *fw) {
 #define TCL_BC_B(BC) \
-    bc_launch_b<MR, BF16, BC>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st)
+    bc_launch_b<MR, BF16, BC>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st, fw)
     switch (bc_block(K / ls / 64)) {
     case 2: TCL_BC_B(2); break;
     case 4: TCL_BC_B(4); break;
@@ -412,15 +509,17 @@ void bc_launch(const void *A, const uint32_t *Bc, const void *S, const uint32_t 
 #undef TCL_BC_B
 }
 
+// Launches of up to maxr (1, 2 or 4) rows each.
 template <bool BF16>
 void bc_launch_rows(const void *A, const uint32_t *Bc, const void *S, const uint32_t *SR, void *C,
                     const void *Other, const void *Bias, int M, int N, int K, int ls, int postop,
-                    int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st) {
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        const int rows = M - m0;
-        if (rows == 1) bc_launch<1, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st);
-        else if (rows == 2) bc_launch<2, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st);
-        else bc_launch<4, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st);
+                    int out_f32, int ksw, float *part, uint32_t *cnt, hipStream_t st, const BcFwht *fw = nullptr,
+                    int maxr = 4) {
+    for (int m0 = 0; m0 < M; m0 += maxr) {
+        const int rows = std::min(M - m0, maxr);
+        if (rows == 1) bc_launch<1, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st, fw);
+        else if (rows == 2) bc_launch<2, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st, fw);
+        else bc_launch<4, BF16>(A, Bc, S, SR, C, Other, Bias, M, m0, N, K, ls, postop, out_f32, ksw, part, cnt, st, fw);
     }
 }
 
@@ -497,6 +596,34 @@ ternocl_status bitcos_gemv_run(int dtype, const void *A, const uint32_t *Bc, con
         bc_launch_rows<true>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st);
     else
         bc_launch_rows<false>(A, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st);
+    return check_launch();
+}
+
+// The sign flip + FWHT (HB <= 512; blocks of K: each a power of two >= 8,
+// x 16-byte and signs 8-byte aligned: the host checks) fused into the GEMV;
+// the same workspace rule as bitcos_gemv_run.
+ternocl_status bitcos_fwht_gemv_run(int dtype, const void *x, const int8_t *signs, int HB, int use_signs,
+                                    float scale_full, float scale_tail, const uint32_t *Bc, const void *S,
+                                    const uint32_t *SR, int ls, void *C, const void *Other, const void *Bias, int M,
+                                    int N, int K, int postop, int out_f32, hipStream_t st, void *ws, size_t ws_bytes) {
+    int ksw = bc_pick_ksw(N, ls);
+    if (ksw > 1 && !(ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= bc_split_ws(N, ksw) && bc_cnt_fit(N))) ksw = 1;
+    // rows per launch: the most (4, 2, 1) whose blocks fit the workgroup's LDS
+    // beside the table and the slice sums
+    int maxr = 4;
+    auto lds_of = [&](int r) { return bc_fw_lds(r, K, ls, ksw, HB) + 256 * 8 + (size_t)(kBcMaxLs - 1) * r * 64 * 4; };
+    while (maxr > 1 && lds_of(maxr) > 64 * 1024) maxr >>= 1;
+    if (lds_of(maxr) > 64 * 1024) {
+        set_error("the fused transform's blocks take more than 64 KiB of LDS at this K / ls");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    uint32_t *cnt = ksw > 1 ? (uint32_t *)ws : nullptr;
+    float *part = ksw > 1 ? (float *)((uint8_t *)ws + kWsHeader) : nullptr;
+    const BcFwht fw{signs, HB, use_signs, scale_full, scale_tail};
+    if (dtype == TERNOCL_BF16)
+        bc_launch_rows<true>(x, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st, &fw, maxr);
+    else
+        bc_launch_rows<false>(x, Bc, S, SR, C, Other, Bias, M, N, K, ls, postop, out_f32, ksw, part, cnt, st, &fw, maxr);
     return check_launch();
 }
 

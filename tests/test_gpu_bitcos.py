@@ -443,3 +443,75 @@ def test_bitcos_gemm_mt_rejects_small_workspace(dev):
     T.bitcos_fp16_upcvt_gemm_mt(A, B, S, None, C, None, None, M, N, K, 1, None)
     torch.cuda.synchronize()
     assert not C.any().item()
+
+
+# ---- the transform fused into the GEMV (ternocl_bitcos_fwht_gemm_ws) ----------------
+# (M, K, N, ls, HB, z): C4 at its default plan, a 256-element tail block, HB 256,
+# several rows (one and two launches of 4 rows), slices that straddle blocks
+FUSED = [(1, 5376, 21504, 0, 512, 0.5), (1, 5376, 21504, 0, 512, 0.3), (1, 5376, 21504, 0, 512, 0.7),
+         (2, 4096, 1040, 8, 512, 0.5), (3, 2048, 528, 4, 256, 0.4), (4, 5376, 2048, 7, 512, 0.5),
+         (5, 1536, 336, 6, 512, 0.6), (1, 2304, 4096, 6, 256, 0.5)]
+
+
+@pytest.mark.parametrize("use_signs", [True, False])
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ls,HB,z", FUSED)
+def test_bitcos_fwht_fused_bit_exact(dev, orc, M, K, N, ls, HB, z, bf16, use_signs):
+    """The fused launch gives, bit for bit, what the transform followed by the GEMV gives
+    (split launch and one workgroup per strip), and the GEMV's result within the rule of
+    the host gold on the oracle's transform."""
+    import torch
+    import ternocl_amd as T
+    ls = ls or T.bitcos_pick_ls(M, N, K)
+    wsb = T.bitcos_gemv_ws_bytes(N, ls)
+    print(f"bitcos fused fwht M={M} K={K} N={N} ls={ls} HB={HB} z={z} bf16={bf16} signs={use_signs} ws={wsb}",
+          flush=True)
+    g = synth.rng(8000 + M + K + N + HB)
+    x = synth.activations(g, (M, K), bf16)
+    sgn = (g.integers(0, 2, K, dtype=np.int8) * 2 - 1).astype(np.int8)
+    buf, _ = synth.bitcos_weights(g, K, N, z)
+    S = synth.scales(g, K, N, bf16)
+    other = synth.activations(g, (M, N), bf16)
+    bias = formats.f32_to_dt(g.standard_normal(N).astype(np.float32) * np.float32(0.1), bf16)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    dx, ds = dev_dt(x, bf16), dev_raw(sgn)
+    dB, dS, dO, dBias = dev_raw(buf), dev_dt(S, bf16), dev_dt(other, bf16), dev_dt(bias, bf16)
+    dSR = torch.zeros(max(ls - 1, 1) * N, dtype=torch.int32, device="cuda")
+    T.bitcos_slice_ranks(dB, dSR, K, N, ls)
+    SR = dSR if ls > 1 else None
+    dy = torch.zeros((M, K), dtype=dt, device="cuda")
+    T.hadamard_fwht(dx, ds, dy, M, K, HB, use_signs)
+    for w in ([torch.zeros(wsb, dtype=torch.uint8, device="cuda")] if wsb else []) + [None]:
+        ref = torch.zeros((M, N), dtype=dt, device="cuda")
+        T.bitcos_fp16_upcvt_gemm(dy, dB, dS, SR, ref, dO, dBias, M, N, K, ls, 5, False, ws=w)
+        got = torch.full((M, N), 7.0, dtype=dt, device="cuda")
+        T.bitcos_fwht_gemm(dx, ds, HB, dB, dS, SR, got, dO, dBias, M, N, K, ls, 5, False, ws=w, use_signs=use_signs)
+        torch.cuda.synchronize()
+        assert np.array_equal(host_u16(got), host_u16(ref)), f"fused differs (ws={w is not None})"
+    y = orc.fwht(x, sgn, M, K, HB, use_signs, bf16)
+    assert np.array_equal(host_u16(dy), y)
+    want = orc.epilogue(orc.bitcos_gold(y, buf, S, M, K, N, bf16), other, bias, 5, False, bf16)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(got), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
+def test_bitcos_fwht_fused_rejects(dev):
+    """Host checks of the fused entry: HB past one wave (1024), a tail that is not a power
+    of two, x not 16-byte aligned."""
+    import torch
+    import ternocl_amd as T
+    K, N = 4096, 64
+    x = torch.zeros((1, K + 8), dtype=torch.float16, device="cuda")
+    s = torch.ones(K, dtype=torch.int8, device="cuda")
+    B = torch.zeros(K // 32 * N + N + 4, dtype=torch.int32, device="cuda")
+    S = torch.zeros((K // 128, N), dtype=torch.float16, device="cuda")
+    C = torch.zeros((1, N), dtype=torch.float16, device="cuda")
+    with pytest.raises(T.TernoclError) as e:
+        T.bitcos_fwht_gemm(x, s, 1024, B, S, None, C, None, None, 1, N, K, 1)
+    assert e.value.status == 2
+    with pytest.raises(T.TernoclError) as e:
+        T.bitcos_fwht_gemm(x, s, 512, B, S, None, C, None, None, 1, N, 4096 + 384, 1)
+    assert e.value.status == 2
+    with pytest.raises(T.TernoclError) as e:
+        T.bitcos_fwht_gemm(x[:, 1:], s, 512, B, S, None, C, None, None, 1, N, K, 1)
+    assert e.value.status == 1
