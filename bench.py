@@ -775,7 +775,8 @@ def main():
                     help="counter-collection mode for rocprofv3 --pmc: N eager launches per GEMV shape, "
                          "a 64 MiB device copy (the calibration kernel of known size), N calls each of the "
                          "int8 prefill (quant_a + s8 x s2 GEMM) and the fp16 upcvt prefill GEMM (M=1024 "
-                         "K=4096 N=14336), of the BITCOS GEMV (K=5376 N=21504, z = .5) and of one MoE "
+                         "K=4096 N=14336), of the BITCOS GEMV (K=5376 N=21504, z = .5; alone and with the "
+                         "FWHT fused in), of the LM head GEMV (M=1 K=4096 N=151680) and of one MoE "
                          "prefill layer (T=2048 E=64 top-8 H=2048 I=1408); prints one line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -828,7 +829,19 @@ def main():
         dws = torch.zeros(max(wsb, 16), dtype=torch.uint8, device="cuda")
         for _ in range(args.probe):
             T.bitcos_fp16_upcvt_gemm(x, dBc, dSc, dSR, dCb, None, None, 1, Nb, Kb, ls, ws=dws)
-        del x, dBc, dSc, dSR, dCb, dws
+        sgn = torch.ones(Kb, dtype=torch.int8, device="cuda")
+        for _ in range(args.probe):  # the same GEMV with the sign flip + FWHT (HB 512) fused in
+            T.bitcos_fwht_gemm(x, sgn, 512, dBc, dSc, dSR, dCb, None, None, 1, Nb, Kb, ls, ws=dws)
+        del x, dBc, dSc, dSR, dCb, dws, sgn
+        # the reference's 8B LM head GEMV, M=1 K=4096 N=151680 fp16 (the multi-strip kernel)
+        Kl, Nl = 4096, 151680
+        g = synth.rng(901)
+        xl = dev16(torch, synth.activations(g, (1, Kl), False), False)
+        dBl, dSl = dev32(torch, synth.int2_weights(g, Kl, Nl)), dev16(torch, synth.scales(g, Kl, Nl, False), False)
+        dCl = torch.empty((1, Nl), dtype=torch.float16, device="cuda")
+        for _ in range(args.probe):
+            T.int2_fp16_upcvt_gemm(xl, dBl, dSl, dCl, None, None, 1, Nl, Kl)
+        del xl, dBl, dSl, dCl
         # one int2 MoE prefill layer, T=2048 E=64 top-8 H=2048 I=1408 bf16
         Tk, E, topk, H, I = 2048, 64, 8, 2048, 1408
         g = synth.rng(55)
