@@ -663,13 +663,33 @@ def bench_c5(torch, T, synth, formats, orc):
     got8 = formats.dt_to_f32(dO.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
     rel8 = check(got8)
     us8 = graph_time_us(torch, call8, 10)
+    # the route alone at this layer's G and at a long prefill's (T = 32768 tokens, G = 262144,
+    # where each route workgroup ranks its chunk in four passes), checked against the oracle
+    route = {}
+    for gT in (Tk, 32768):
+        G = gT * topk
+        rid = ids if gT == Tk else np.random.default_rng(506).integers(0, E, G, dtype=np.int32)
+        drid = torch.from_numpy(rid).cuda()
+        meta = torch.zeros(2 * E + 2, dtype=torch.int32, device="cuda")
+        perm = torch.empty(G, dtype=torch.int32, device="cuda")
+        inv = torch.empty(G, dtype=torch.int32, device="cuda")
+
+        def rcall():
+            T.int2_moe_route(drid, meta, perm, inv, G, E)
+        rcall()
+        torch.cuda.synchronize()
+        m, pm, iv = orc.moe_route(rid, E, T.moe_tile_rows())
+        exact = bool(np.array_equal(meta.cpu().numpy(), m) and np.array_equal(perm.cpu().numpy(), pm)
+                     and np.array_equal(inv.cpu().numpy(), iv))
+        route[f"G{G}"] = {"us": round(graph_time_us(torch, rcall, 20), 2), "exact": exact}
     return {"workload": "int2 MoE prefill layer T=2048 E=64 top-8 H=2048 I=1408 bf16 (route, up, gate, down, combine)",
             "value": round(tf, 1), "unit": "TFLOPS", "us": round(us, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
             "peak": BF16_PEAK_TFLOPS, "layers_rotated": sets, "layer_weight_bytes": int(layer_bytes),
             "check_tokens": [list(t[:2]) for t in refs], "check_rel_err": rel, "check_pass": rel < 1e-2,
             "int8": {"us": round(us8, 2), "TOPS": round(flops / us8 / 1e6, 1),
                      "mfma_frac": round(flops / us8 / 1e6 / I8_PEAK_TOPS, 4), "peak": I8_PEAK_TOPS,
-                     "check_rel_err": rel8, "check_pass": rel8 < 5e-2}}
+                     "check_rel_err": rel8, "check_pass": rel8 < 5e-2},
+            "route": route}
 
 
 def bench_c6(torch, T, synth, formats, orc):

@@ -61,6 +61,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cmath>
 
 namespace tcl {
 namespace {
@@ -1133,6 +1134,26 @@ void f4_auto_split(int M, int N, int K, int cpl_req, int &cpl, int &ks) {
     while (k < 16 && (double)groups / 28.0 > k * 1.4142) k *= 2;
     cpl = c;
     ks = f4_slices(groups, k);
+    // Slices that do not split into waves of whole groups (K = 17408: 136
+    // groups / 4 = 34 = 2 x 17, planned as one group on each of 2 waves for 17
+    // windows, one 16-byte load per lane in flight) take instead the slice
+    // count, from 2 to 16, whose plan needs the fewest windows, the nearest to
+    // k on a tie (K = 17408: 5 slices of 28 groups, 7 waves x 4 groups).
+    const F4Plan p0 = f4_plan(false, M, N, K, 0, c, 0, ks);
+    if (p0.waves * p0.gpw < 4) {
+        int best_w = p0.windows;
+        double best_d = 0.0;
+        for (int kk = 2; kk <= 16; ++kk) {
+            const int s = f4_slices(groups, kk);
+            const F4Plan p = f4_plan(false, M, N, K, 0, c, 0, s);
+            const double d = std::fabs(std::log((double)s / k));
+            if (p.windows < best_w || (p.windows == best_w && d < best_d)) {
+                best_w = p.windows;
+                best_d = d;
+                ks = s;
+            }
+        }
+    }
 }
 
 // The multi-strip GEMV's plan for K: groups per wave (1, 2 or 4) and waves

@@ -40,7 +40,11 @@ namespace {
 
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
 constexpr int kRoutePieces = 1;                                // 64-id pieces per wave of a chunk
-constexpr int kRouteChunk = kRouteWaves * kRoutePieces * 64;   // ids placed per workgroup (1024)
+constexpr int kRouteChunk = kRouteWaves * kRoutePieces * 64;   // ids ranked per pass of a workgroup (1024)
+// Every workgroup counts all G ids, so the workgroups are capped: past
+// 64 x 1024 ids a workgroup's chunk grows (whole passes of 1024) and the
+// total work stays linear in G (at most 64 G counts and G ranks).
+constexpr int kRouteMaxBlocks = 64;
 
 // Lanes of a wave holding the same valid expert id as this lane (log2(E)
 // ballots); invalid lanes get an empty set.
@@ -54,28 +58,29 @@ __device__ __forceinline__ unsigned long long route_group(bool valid, int e, int
     return valid ? same : 0ull;
 }
 
-// Stable counting sort over ceil(G / kRouteChunk) workgroups, no
-// communication between them: workgroup b places the ids of its chunk
-// [b C, (b + 1) C).  It counts all ids (the histogram, hence each expert's
-// first row) and those before its chunk (the expert's rows that precede the
-// chunk) with LDS atomics (integer counts: order-free); then it ranks its
-// chunk in order (waves in order, pieces in order, lanes in order, lanes of
-// one expert found with log2(E) ballots) and writes perm and inv.  Workgroup
-// 0 writes meta.  Ids outside [0, E) are dropped (inv = -1), and perm past
-// the kept rows is -1.
+// Stable counting sort over ceil(G / chunk) workgroups, no communication
+// between them: workgroup b places the ids of its chunk [b chunk, (b + 1)
+// chunk), chunk a multiple of kRouteChunk.  It counts all ids (the histogram,
+// hence each expert's first row) and those before its chunk (the expert's
+// rows that precede the chunk) with LDS atomics (integer counts: order-free);
+// then it ranks its chunk in passes of kRouteChunk ids, in order (passes in
+// order, waves in order, pieces in order, lanes in order, lanes of one expert
+// found with log2(E) ballots) and writes perm and inv.  Workgroup 0 writes
+// meta.  Ids outside [0, E) are dropped (inv = -1), and perm past the kept
+// rows is -1.
 __global__ void __launch_bounds__(kRouteThreads)
 k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict__ perm,
-            int *__restrict__ inv, int G, int E, int rpt) {
+            int *__restrict__ inv, int G, int E, int rpt, int chunk) {
     extern __shared__ int sh[];
     // counts of all ids tot [E] (first those from the chunk on) and of the
     // ids before the chunk bef [E], the
-    // chunk's per-wave counts / wave bases wc [W][E], each expert's first row
-    // for this chunk base [E]
+    // pass's per-wave counts / wave bases wc [W][E], each expert's first row
+    // for this pass base [E]
     int *tot = sh, *bef = sh + E, *wc = sh + 2 * E, *base = sh + (2 + kRouteWaves) * E;
     __shared__ int s_rows;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const unsigned long long below = (1ull << lane) - 1ull;
-    const int c0 = blockIdx.x * kRouteChunk;
+    const int c0 = blockIdx.x * chunk, c1 = (int)min((long long)c0 + chunk, (long long)G);
     for (int i = tid; i < (2 + kRouteWaves) * E; i += kRouteThreads) sh[i] = 0;
     __syncthreads();
 
@@ -126,48 +131,57 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
         }
     }
 
-    // rank this chunk: wave w's ids c0 + (w P + c) 64 + lane, pieces c in order
-    int eid[kRoutePieces], loc[kRoutePieces];
-    const int seg = c0 + wave * kRoutePieces * 64;
+    // rank the chunk, a pass of kRouteChunk ids at a time: wave w's ids
+    // s0 + (w P + c) 64 + lane, pieces c in order
     int *mine = wc + wave * E;
+    for (int s0 = c0; s0 < c1; s0 += kRouteChunk) {
+        int eid[kRoutePieces], loc[kRoutePieces];
+        const int seg = s0 + wave * kRoutePieces * 64;
 #pragma unroll
-    for (int c = 0; c < kRoutePieces; ++c) {
-        const int g = seg + c * 64 + lane;
-        eid[c] = g < G ? ids[g] : -1;
-    }
-#pragma unroll
-    for (int c = 0; c < kRoutePieces; ++c) {
-        const bool valid = eid[c] >= 0 && eid[c] < E;
-        const int e = valid ? eid[c] : 0;
-        const unsigned long long same = route_group(valid, e, E);
-        const int before = valid ? mine[e] : 0;  // every lane reads before the leader writes
-        loc[c] = before + __popcll(same & below);
-        if (valid && (same & below) == 0ull) mine[e] = before + __popcll(same);
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += kRouteThreads) {  // wave counts -> wave bases, in wave order
-        int r = base[e];
-        for (int w = 0; w < kRouteWaves; ++w) {
-            const int n = wc[w * E + e];
-            wc[w * E + e] = r;
-            r += n;
+        for (int c = 0; c < kRoutePieces; ++c) {
+            const int g = seg + c * 64 + lane;
+            eid[c] = g < c1 ? ids[g] : -1;
         }
-    }
-    __syncthreads();
 #pragma unroll
-    for (int c = 0; c < kRoutePieces; ++c) {
-        const int g = seg + c * 64 + lane;
-        if (eid[c] >= 0 && eid[c] < E) {
-            const int p = mine[eid[c]] + loc[c];
-            perm[p] = g;
-            inv[g] = p;
-        } else if (g < G) {
-            inv[g] = -1;
+        for (int c = 0; c < kRoutePieces; ++c) {
+            const bool valid = eid[c] >= 0 && eid[c] < E;
+            const int e = valid ? eid[c] : 0;
+            const unsigned long long same = route_group(valid, e, E);
+            const int before = valid ? mine[e] : 0;  // every lane reads before the leader writes
+            loc[c] = before + __popcll(same & below);
+            if (valid && (same & below) == 0ull) mine[e] = before + __popcll(same);
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += kRouteThreads) {  // wave counts -> wave bases, in wave order
+            int r = base[e];
+            for (int w = 0; w < kRouteWaves; ++w) {
+                const int n = wc[w * E + e];
+                wc[w * E + e] = r;
+                r += n;
+            }
+            base[e] = r;  // the next pass's first row of expert e
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < kRoutePieces; ++c) {
+            const int g = seg + c * 64 + lane;
+            if (eid[c] >= 0 && eid[c] < E) {
+                const int p = mine[eid[c]] + loc[c];
+                perm[p] = g;
+                inv[g] = p;
+            } else if (g < c1) {
+                inv[g] = -1;
+            }
+        }
+        if (s0 + kRouteChunk < c1) {  // a next pass: its wave counts start from zero
+            __syncthreads();
+            for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wc[i] = 0;
+            __syncthreads();
         }
     }
     // perm past the kept rows: this workgroup's share of [rows, G)
     const int rows = s_rows;
-    for (int i = c0 + tid; i < min(c0 + kRouteChunk, G); i += kRouteThreads)
+    for (int i = c0 + tid; i < c1; i += kRouteThreads)
         if (i >= rows) perm[i] = -1;
 }
 
@@ -225,9 +239,12 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
 size_t moe_route_lds(int E) { return (size_t)(3 + kRouteWaves) * E * sizeof(int); }
 
 ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st) {
-    const unsigned blocks = (unsigned)((G + kRouteChunk - 1) / kRouteChunk);
+    const int passes = (G + kRouteChunk - 1) / kRouteChunk;
+    const int per = (passes + kRouteMaxBlocks - 1) / kRouteMaxBlocks;  // passes per workgroup
+    const int chunk = per * kRouteChunk;
+    const unsigned blocks = (unsigned)((G + chunk - 1) / chunk);
     hipLaunchKernelGGL(k_moe_route, dim3(blocks), dim3(kRouteThreads), moe_route_lds(E), st, ids, meta, perm, inv,
-                       G, E, moe_tile_rows());
+                       G, E, moe_tile_rows(), chunk);
     return check_launch();
 }
 

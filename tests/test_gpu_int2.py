@@ -272,6 +272,41 @@ def test_gemv_f4_k_slices(dev, orc, M, K, N, ks, cpl, bf16):
         assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
 
 
+# (M, K, N, slices of the automatic plan): K whose power-of-two split gives slices
+# that do not divide into waves of whole groups (K = 17408: 136 groups, 4 slices
+# of 34 = 2 x 17) take the slice count whose plan has the fewest windows
+AUTO_UNEVEN = [(1, 17408, 5120, 5), (2, 13312, 1024, 9), (3, 23552, 256, 12), (1, 34816, 256, 10)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ks", AUTO_UNEVEN)
+def test_gemv_f4_auto_split_uneven_slices(dev, orc, M, K, N, ks, bf16):
+    """The automatic K split on slice counts chosen for whole waves of groups: the
+    workspace the entry asks for holds that many slices, the result is within the
+    rule of the gold, bit-identical over repeated calls, and the counters are left
+    at zero."""
+    import torch
+    import ternocl_amd as T
+    print(f"gemv f4 auto split M={M} K={K} N={N} ks={ks} bf16={bf16}", flush=True)
+    need = T.int2_gemm_ws_bytes(M, N, K)
+    assert need == T.WS_HEADER_BYTES + ks * M * N * 4
+    A, B, S, other, bias_f = _inputs(77 + M + K // 1024, M, K, N, bf16)
+    dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16), dev_dt(other, bf16)
+    dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(3):
+        dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+        T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, 5, False, ws=ws)
+        torch.cuda.synchronize()
+        outs.append(host_u16(dC))
+    assert all(np.array_equal(outs[0], o) for o in outs[1:]), "non-deterministic"
+    assert not ws[:(N // 16) * 4].any().item(), "strip counters not left at zero"
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 5, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(outs[0], bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
 def test_gemv_f4_k_slices_need_the_workspace(dev):
     """An explicit split without a large enough workspace is an error; the
     automatic plan without one runs unsplit."""

@@ -35,8 +35,11 @@ def _route(T, ids, G, E):
     return meta, perm, inv
 
 
+# past 64 x 1024 ids a route workgroup ranks its chunk in several passes
 @pytest.mark.parametrize("G,E,skew", [(1, 1, False), (100, 7, False), (16384, 64, False), (16384, 64, True),
-                                      (20000, 128, True), (3000, 512, False), (5000, 33, True), (40000, 64, False)])
+                                      (20000, 128, True), (3000, 512, False), (5000, 33, True), (40000, 64, False),
+                                      (65537, 64, False), (100000, 64, True), (262144, 128, True),
+                                      (300001, 512, False)])
 def test_moe_route_matches_stable_sort(dev, orc, G, E, skew):
     import ternocl_amd as T
     g = synth.rng(G + E)
@@ -53,9 +56,10 @@ def test_moe_route_matches_stable_sort(dev, orc, G, E, skew):
     assert np.array_equal(inv.cpu().numpy(), iv)
 
 
-def test_moe_route_drops_out_of_range_ids(dev, orc):
+@pytest.mark.parametrize("G", [3000, 150000])
+def test_moe_route_drops_out_of_range_ids(dev, orc, G):
     import ternocl_amd as T
-    G, E = 3000, 16
+    E = 16
     g = synth.rng(5)
     ids = g.integers(0, E, G, dtype=np.int32)
     bad = g.random(G) < 0.1
