@@ -1168,12 +1168,23 @@ size_t f4ms_lds(int gpw, int waves, int cpl) {
     return (size_t)waves * f4_window_bytes(kF4RowStride, gpw) + (size_t)2 * waves * cpl * 16 * 4;
 }
 
-// cpl: columns per lane (1, 2 or 4; 0 = automatic), strips of 16 cpl columns;
-// 512 workgroups (two per CU), at most one per strip.
+// cpl: columns per lane (1, 2 or 4; 0 = automatic), strips of 16 cpl columns.
+// Grid, from graph-timed sweeps (fp16, >2 GiB rotated): workgroups of up to 8
+// waves (K <= 4096) run two per CU, min(strips, 512) of them; larger ones one
+// per CU, the strips spread evenly (every workgroup ceil or floor of the
+// mean): against 512 of them, K = 5120 N = 248320 70.9 -> 64.5 us, K = 7168
+// N = 28672 16.5 -> 14.7, K = 8192 N = 14336 11.4 -> 9.9, K = 3072 N = 32768
+// 10.0 -> 8.9; 8-wave workgroups lose that way (K = 4096 N = 151680 33.9 ->
+// 36.3, K = 2048 N = 65536 10.5 -> 12.8).
+int f4ms_grid(int strips, int waves) {
+    if (waves <= 8) return std::min(strips, 512);
+    const int per = (strips + 255) / 256;
+    return (strips + per - 1) / per;
+}
+
 ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K, int postop,
                                   int out_f32, int cpl, hipStream_t st) {
-    constexpr int wgs = 512;
     int gpw, waves;
     f4ms_plan(K, gpw, waves);
     if (cpl == 0) cpl = N % (16 * kF4msCpl) == 0 ? kF4msCpl : N % 32 == 0 ? 2 : 1;
@@ -1183,7 +1194,7 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
     const int strips = N / (16 * cpl);
-    const dim3 grid(std::min(strips, wgs)), block(64 * waves);
+    const dim3 grid(f4ms_grid(strips, waves)), block(64 * waves);
     const size_t lds = f4ms_lds(gpw, waves, cpl);
     const uint16_t *a = (const uint16_t *)A, *s = (const uint16_t *)S, *o = (const uint16_t *)Other;
 #define TCL_F4MS(G, CP, BF)                                                                                    \
