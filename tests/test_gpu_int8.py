@@ -277,6 +277,55 @@ def test_int8_gemm_in_gemm_quantization(dev, orc, M, K, N, bf16):
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
+# ---- A off the int8 grid (validate.sh with OFFGRID=F) ---------------------------------
+
+def _offgrid_a(orc, g, M, K, bf16, F):
+    """The reference driver's A with --offgrid F (int2_via_int2_x_int8_dpas/main.cpp:250-272):
+    A ~ U[-5, 5] fake-quantized per (row, 128-group) as v = sat_int8(rint(A SA)), then moved
+    F LSB away from zero, A = DT((v +- F) / SA), so the rounding of A * SA is exercised near
+    the int8 grid's midpoints (F = .5: ties before the DT rounding of A)."""
+    A = formats.f32_to_dt(g.uniform(-5, 5, (M, K)).astype(np.float32), bf16)
+    SA = orc.scale_a(A, M, K, bf16)
+    sa = formats.dt_to_f32(SA[:, :M], bf16).T.repeat(128, axis=1)  # [M, K]
+    v = np.clip(np.rint(formats.dt_to_f32(A, bf16) * sa), -128, 127).astype(np.float32)
+    off = np.where(v >= 0, np.float32(F), np.float32(-F))
+    return formats.f32_to_dt(((v + off) * (np.float32(1.0) / sa)).astype(np.float32), bf16)
+
+
+OFFGRID_SHAPES = [(77, 128, 48), (129, 256, 272), (4, 6144, 5120), (1, 17408, 5120), (100, 5120, 1024),
+                  (1024, 1024, 512)]
+
+
+@pytest.mark.parametrize("F", [0.5, 0.6])
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", OFFGRID_SHAPES)
+def test_int8_offgrid_activations(dev, orc, M, K, N, bf16, F):
+    """validate.sh's OFFGRID runs: SA and Aq bit-exact with the oracle's quantization on A
+    placed F LSB off the int8 grid; C of QMODE 1 (A quantized in the GEMM / GEMV) equal to
+    QMODE 0's bit for bit, and within the rule of the oracle's gold."""
+    import torch
+    import ternocl_amd as T
+    print(f"int8 offgrid F={F} M={M} K={K} N={N} bf16={bf16}", flush=True)
+    g = synth.rng(int(7000 + 10 * F + M + K + N))
+    A = _offgrid_a(orc, g, M, K, bf16, F)
+    B = synth.int2_weights(g, K, N)
+    SB = synth.scales(g, K, N, bf16)
+    dA, dSA, dAq = _quant(T, torch, A, M, K, bf16)
+    SA = orc.scale_a(A, M, K, bf16)
+    assert np.array_equal(host_u16(dSA)[:, :M], SA[:, :M]), "SA differs from the oracle"
+    assert np.array_equal(dAq.cpu().numpy(), orc.quant_a(A, SA, M, K, bf16)), "Aq differs from the oracle"
+    dB, dSB = dev_raw(B), dev_dt(SB, bf16)
+    up = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+    ig = torch.zeros((M, N), dtype=dSB.dtype, device="cuda")
+    T.int2_int8_gemm(None, dAq, dSA, dB, dSB, up, None, None, M, N, K, 0, False)
+    T.int2_int8_gemm(dA, None, dSA, dB, dSB, ig, None, None, M, N, K, 0, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(up), host_u16(ig)), "QMODE 1 differs from QMODE 0"
+    want = orc.epilogue(orc.int8_gold(A, B, SA, SB, M, K, N, bf16), None, None, 0, False, bf16)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(up), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
 # ---- M <= 4: the s8 x s2 decode GEMV (int2_int8_dpas.cl:213-215) ------------------
 
 DECODE_SHAPES = [(1, 128, 16), (1, 4096, 14336), (2, 14336, 4096), (3, 2048, 1040), (4, 4096, 4096),
