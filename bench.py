@@ -682,6 +682,22 @@ def bench_c5(torch, T, synth, formats, orc):
         exact = bool(np.array_equal(meta.cpu().numpy(), m) and np.array_equal(perm.cpu().numpy(), pm)
                      and np.array_equal(inv.cpu().numpy(), iv))
         route[f"G{G}"] = {"us": round(graph_time_us(torch, rcall, 20), 2), "exact": exact}
+        if gT == Tk:
+            # the combine alone on this layer's inv (Y: fp32 [G][H] as the down GEMM writes it)
+            dY = torch.randn((G, H), dtype=torch.float32, device="cuda")
+
+            def ccall():
+                T.int2_moe_combine(dY, inv, dRW, dO, Tk, topk, H)
+            combine_us = graph_time_us(torch, ccall, 20)
+            del dY
+    route_us = route[f"G{Tk * topk}"]["us"]
+    # the reference reports each phase (int2_moe/prefill.cpp:323-350); here the layer is one
+    # call, so its grouped GEMMs are the layer minus its route and combine, each timed alone
+    phases = {"route_us": route_us, "combine_us": round(combine_us, 2),
+              "gemm_us": round(us - route_us - combine_us, 2),
+              "gemm_TFLOPS": round(flops / (us - route_us - combine_us) / 1e6, 1),
+              "measured": "route and combine graph-timed alone; gemm_us = us - route_us - combine_us "
+                          "(gate/up in one launch, then down)"}
     return {"workload": "int2 MoE prefill layer T=2048 E=64 top-8 H=2048 I=1408 bf16 (route, up, gate, down, combine)",
             "value": round(tf, 1), "unit": "TFLOPS", "us": round(us, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
             "peak": BF16_PEAK_TFLOPS, "layers_rotated": sets, "layer_weight_bytes": int(layer_bytes),
@@ -689,7 +705,7 @@ def bench_c5(torch, T, synth, formats, orc):
             "int8": {"us": round(us8, 2), "TOPS": round(flops / us8 / 1e6, 1),
                      "mfma_frac": round(flops / us8 / 1e6 / I8_PEAK_TOPS, 4), "peak": I8_PEAK_TOPS,
                      "check_rel_err": rel8, "check_pass": rel8 < 5e-2},
-            "route": route}
+            "phases": phases, "route": route}
 
 
 def bench_c6(torch, T, synth, formats, orc):
