@@ -21,8 +21,10 @@ __global__ void k_fill_zero_bytes(uint8_t *__restrict__ p, size_t n) {
 // coalesced 16-byte loads per lane, all issued before any is used, and XORs
 // the words.  The sum is stored only if it equals an arbitrary constant, so
 // the loads stay live and the kernel writes (almost) nothing: its duration is
-// the read alone.
+// the read alone.  Non-temporal loads, as the GEMVs stream their weights
+// (faster than plain loads here: 15.7 MB in 3.95 against 4.26 us).
 constexpr int kReadU = 4, kReadThreads = 256;
+typedef uint32_t rd_u32x4 __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(kReadThreads) k_stream_read(const uint4 *__restrict__ src, size_t n16,
                                                               uint32_t *__restrict__ sink) {
     const size_t base = (size_t)blockIdx.x * (kReadU * kReadThreads) + threadIdx.x;
@@ -30,7 +32,8 @@ __global__ void __launch_bounds__(kReadThreads) k_stream_read(const uint4 *__res
 #pragma unroll
     for (int u = 0; u < kReadU; ++u) {
         const size_t i = base + (size_t)u * kReadThreads;
-        v[u] = i < n16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+        const rd_u32x4 t = i < n16 ? __builtin_nontemporal_load((const rd_u32x4 *)(src + i)) : rd_u32x4{0u, 0u, 0u, 0u};
+        v[u] = make_uint4(t.x, t.y, t.z, t.w);
     }
     uint32_t x = 0;
 #pragma unroll
