@@ -118,8 +118,14 @@ template <int P> __device__ __forceinline__ float epi_apply_c(float v, float oth
     else if constexpr (P == 5) return (v + bias) + other;
     else return v;
 }
-// Epilogue + store of 4 consecutive outputs (m, n..n+3), n % 4 == 0.
-template <bool BF16, int P, bool F32>
+// Epilogue + store of 4 consecutive outputs (m, n..n+3), n % 4 == 0.  NT: a
+// non-temporal store, for outputs no kernel of the same call re-reads (the
+// dense prefill GEMMs' C, 28 MB at M = 1024 N = 14336: written through, it
+// would evict the weight and activation tiles other workgroups still read;
+// same box, two runs each: C3's quant_a + int8 GEMM 98.8-99.1 -> 97.1-97.4
+// us, the fp16 GEMM 106.6-106.7 -> 105.7-106.3 us; the MoE layer's outputs,
+// re-read by its next GEMM, measured slower so: 383-391 -> 391-398 us).
+template <bool BF16, int P, bool F32, bool NT = false>
 __device__ __forceinline__ void epi_store4_c(void *C, const uint16_t *Other, const void *Bias, int N, int m, int n,
                                              const float v[4]) {
     const size_t i = (size_t)m * N + n;
@@ -142,13 +148,16 @@ __device__ __forceinline__ void epi_store4_c(void *C, const uint16_t *Other, con
     float r[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) r[c] = epi_apply_c<P>(v[c], o[c], b[c]);
+    typedef float epi_f32x4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t epi_u32x2 __attribute__((ext_vector_type(2)));
     if constexpr (F32) {
-        *(float4 *)((float *)C + i) = make_float4(r[0], r[1], r[2], r[3]);
+        const epi_f32x4 t = {r[0], r[1], r[2], r[3]};
+        if constexpr (NT) __builtin_nontemporal_store(t, (epi_f32x4 *)((float *)C + i));
+        else *(epi_f32x4 *)((float *)C + i) = t;
     } else {
-        uint2 t;
-        t.x = f2dt<BF16>(r[0]) | (f2dt<BF16>(r[1]) << 16);
-        t.y = f2dt<BF16>(r[2]) | (f2dt<BF16>(r[3]) << 16);
-        *(uint2 *)((uint16_t *)C + i) = t;
+        const epi_u32x2 t = {f2dt<BF16>(r[0]) | (f2dt<BF16>(r[1]) << 16), f2dt<BF16>(r[2]) | (f2dt<BF16>(r[3]) << 16)};
+        if constexpr (NT) __builtin_nontemporal_store(t, (epi_u32x2 *)((uint16_t *)C + i));
+        else *(epi_u32x2 *)((uint16_t *)C + i) = t;
     }
 }
 

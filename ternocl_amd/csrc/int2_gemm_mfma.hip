@@ -546,7 +546,7 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
                             *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
                                 make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
                         } else {
-                            epi_store4_c<BF16, P, F32>(C, Other, Bias, N, crow0 + r, n, v4);
+                            epi_store4_c<BF16, P, F32, !SHORT>(C, Other, Bias, N, crow0 + r, n, v4);  // (SHORT: MoE)
                         }
                     }
                 }
@@ -609,7 +609,7 @@ k_splitk_reduce(const float *__restrict__ part, int splits, void *__restrict__ C
     const float v[4] = {t.x, t.y, t.z, t.w};
     const int m = (int)(4 * i / N), n = (int)(4 * i - (size_t)m * N);
     epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
-        epi_store4_c<BF16, decltype(P_)::value, decltype(F_)::value>(C, Other, Bias, N, m, n, v);
+        epi_store4_c<BF16, decltype(P_)::value, decltype(F_)::value, true>(C, Other, Bias, N, m, n, v);
     });
 }
 

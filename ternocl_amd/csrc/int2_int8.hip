@@ -395,7 +395,7 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
                 const int r = wm + 16 * pass + (lane >> 2);
                 const float4 t = *(const float4 *)(ct + (16 * pass + (lane >> 2)) * EP + 4 * (lane & 3));
                 const float v4[4] = {t.x, t.y, t.z, t.w};
-                if (r < mrows && n < N) epi_store4_c<BF16, P, F32>(C, Other, Bias, N, m0 + r, n, v4);
+                if (r < mrows && n < N) epi_store4_c<BF16, P, F32, true>(C, Other, Bias, N, m0 + r, n, v4);
             }
             __builtin_amdgcn_wave_barrier();  // reads of this block done before the next block's writes
         }
@@ -725,7 +725,7 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
                     const int r = 32 * (br >> 4) + 16 * hf + (br & 15);
                     const float4 t = *(const float4 *)(ct + br * EP + 4 * (lane & 7));
                     const float v4[4] = {t.x, t.y, t.z, t.w};
-                    if (r < mrows && n < N) epi_store4_c<BF16, P, F32>(C, Other, Bias, N, m0 + r, n, v4);
+                    if (r < mrows && n < N) epi_store4_c<BF16, P, F32, !GRP>(C, Other, Bias, N, m0 + r, n, v4);
                 }
                 __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes
             }
