@@ -275,31 +275,38 @@ template <int MR, int GPW, bool BF16, int QM = 0> struct F4Stage {
     }
 };
 
-// Weight words and scales are read once per launch: non-temporal loads, so
-// that the weight stream does not evict from L2 what the launch and the next
-// one re-read (activations, epilogue operands, slice sums).  Measured against
-// plain loads (graph-timed, >2 GiB rotated): the C2 step 2214-2252 -> 2281-
-// 2323 GB/s, K = 4096 N = 151680 33.1-34.4 -> 32.4-32.6 us, K = 5120 N = 34816
-// 13.7 -> 12.8 us; the same bits.
+// Weight words and scales are read once per launch: non-temporal loads (NT),
+// so that the weight stream does not evict from L2 what the launch and the
+// next one re-read (activations, epilogue operands, slice sums).  Measured
+// against plain loads (graph-timed, >2 GiB rotated): the C2 step 2214-2252 ->
+// 2281-2323 GB/s, K = 4096 N = 151680 33.1-34.4 -> 32.4-32.6 us, K = 5120 N =
+// 34816 13.7 -> 12.8 us; the same bits.  The grouped (MoE decode) GEMVs, a few
+// MB per launch and latency-bound, keep plain loads: the decode layer took
+// 12.15 us with them non-temporal against 11.65 us (same box, three runs).
 typedef uint32_t f4_u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t f4_u32x4 __attribute__((ext_vector_type(4)));
 
-template <int CPL> struct F4Words;
-template <> struct F4Words<1> {
+template <bool NT, class T> __device__ __forceinline__ T f4_ld(const T *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+template <int CPL, bool NT> struct F4Words;
+template <bool NT> struct F4Words<1, NT> {
     uint32_t v[1];
-    __device__ void load(const uint32_t *p) { v[0] = __builtin_nontemporal_load(p); }
+    __device__ void load(const uint32_t *p) { v[0] = f4_ld<NT>(p); }
 };
-template <> struct F4Words<2> {
+template <bool NT> struct F4Words<2, NT> {
     uint32_t v[2];
     __device__ void load(const uint32_t *p) {
-        const f4_u32x2 t = __builtin_nontemporal_load((const f4_u32x2 *)p);
+        const f4_u32x2 t = f4_ld<NT>((const f4_u32x2 *)p);
         v[0] = t.x; v[1] = t.y;
     }
 };
-template <> struct F4Words<4> {
+template <bool NT> struct F4Words<4, NT> {
     uint32_t v[4];
     __device__ void load(const uint32_t *p) {
-        const f4_u32x4 t = __builtin_nontemporal_load((const f4_u32x4 *)p);
+        const f4_u32x4 t = f4_ld<NT>((const f4_u32x4 *)p);
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
     }
 };
@@ -307,8 +314,8 @@ template <> struct F4Words<4> {
 // This wave's weight words (words 2q and 2q + 1 of each group) and raw scale
 // bits of one window; loads unconditional (group clamped; groups past K are
 // never consumed).
-template <int CPL, int GPW> struct F4Slab {
-    F4Words<CPL> w[GPW][2];
+template <int CPL, int GPW, bool NT = true> struct F4Slab {
+    F4Words<CPL, NT> w[GPW][2];
     uint32_t sc[GPW][(CPL + 1) / 2];
     __device__ __forceinline__ void load(const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                          int N, int groups, int g0w, int q, int n0) {
@@ -319,13 +326,13 @@ template <int CPL, int GPW> struct F4Slab {
 #pragma unroll
             for (int t = 0; t < 2; ++t) w[gi][t].load(B + ((size_t)g * 8 + 2 * q + t) * N + n0);
             if constexpr (CPL == 4) {
-                const f4_u32x2 t = __builtin_nontemporal_load((const f4_u32x2 *)(S + (size_t)g * N + n0));
+                const f4_u32x2 t = f4_ld<NT>((const f4_u32x2 *)(S + (size_t)g * N + n0));
                 sc[gi][0] = t.x;
                 sc[gi][1] = t.y;
             } else if constexpr (CPL == 2) {
-                sc[gi][0] = __builtin_nontemporal_load((const uint32_t *)(S + (size_t)g * N + n0));
+                sc[gi][0] = f4_ld<NT>((const uint32_t *)(S + (size_t)g * N + n0));
             } else {
-                sc[gi][0] = __builtin_nontemporal_load(S + (size_t)g * N + n0);
+                sc[gi][0] = f4_ld<NT>(S + (size_t)g * N + n0);
             }
         }
     }
@@ -491,7 +498,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     F4Stage<MR, GPW, BF16, QM> st;
     if constexpr (!NODEC) st.load(A, M, K, groups, g0w, lane, SA, ldsa);
     int after = f4_loads_after_barrier();
-    F4Slab<CPL, GPW> cur;
+    F4Slab<CPL, GPW, !GRP> cur;
     cur.load(B + after, S + after, N, groups, g0w, q, n0);
     F4EpiIn<MR, CPL, BF16> ein;  // behind the weights: waited for only at the epilogue
     ein.load(Other, Bias, postop, out_f32, M, N, q, n0, wave == 0);
@@ -509,7 +516,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     // One window: its MFMAs and group FMAs; PRE: first the next window's loads,
     // unconditional -- loads under a branch are waited for at the branch's
     // end, which would serialise them with this window's work.
-    auto window = [&](int win, auto PRE_, F4Slab<CPL, GPW> &cu, F4Slab<CPL, GPW> &nx) __attribute__((always_inline)) {
+    auto window = [&](int win, auto PRE_, F4Slab<CPL, GPW, !GRP> &cu, F4Slab<CPL, GPW, !GRP> &nx) __attribute__((always_inline)) {
         constexpr bool PRE = decltype(PRE_)::value;
         asm volatile("" ::: "memory");  // staging writes precede the reads (in-order LDS per wave)
         const uint8_t *buf = wlds + (size_t)(win & 1) * WB;
@@ -577,7 +584,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         // one window (the host's choice for one), or the group modes: a next
         // window loaded under a branch and copied into place
         for (int win = 0; win < windows; ++win) {
-            F4Slab<CPL, GPW> nxt;
+            F4Slab<CPL, GPW, !GRP> nxt;
             if (win + 1 < windows) {
                 window(win, std::true_type{}, cur, nxt);
                 cur = nxt;
@@ -586,7 +593,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             }
         }
     } else {
-        F4Slab<CPL, GPW> cur2;
+        F4Slab<CPL, GPW, !GRP> cur2;
         // two register sets used in turn (ping-pong): a copy of the next
         // window's registers into the current ones would wait for their
         // loads; the last window loads nothing (uniform tests, no loads inside)
