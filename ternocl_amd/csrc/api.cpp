@@ -215,7 +215,7 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
     }
     if (M <= 16) {
         // automatic: the fp8 x fp4 engine where it applies (its multi-strip
-        // kernel for M = 1 on many strips), else the bf16/fp16 MFMA GEMV
+        // kernel on many strips), else the bf16/fp16 MFMA GEMV
         const bool auto_tile = t.engine == 0 && t.waves == 0 && t.cols_per_lane == 0 && t.groups_per_wave == 0 &&
                                t.k_slices == 0;
         if (t.engine == 5 || (auto_tile && int2_gemv_f4_supports(M, N, A) && int2_gemv_f4ms_auto(M, N, K))) {
@@ -223,7 +223,7 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
                 FAIL(TERNOCL_ERR_INVALID_ARG, "the multi-strip GEMV (engine 5) takes cols_per_lane only "
                                               "(its waves follow from K)");
             if (!int2_gemv_f4_supports(M, N, A))
-                FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the multi-strip GEMV takes M = 1 and A 16-byte aligned");
+                FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the multi-strip GEMV takes M <= 4 and A 16-byte aligned");
             return int2_gemv_f4ms_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.cols_per_lane,
                                       (hipStream_t)stream);
         }

@@ -746,7 +746,7 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     });
 }
 
-// ---- multi-strip decode GEMV (engine 5: M = 1, all of K in one window) ----
+// ---- multi-strip decode GEMV (engine 5: M <= 4, all of K in one window) ----
 // The kernel above stages the activation pieces in every workgroup, i.e. once
 // per 16- or 32-column strip: at N = 151680 that is 4740 times the same
 // vector, and the staging's VALU work, not HBM, bounds the launch.  Here a
@@ -758,13 +758,16 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // strip) and wave it % W adds them in wave order and stores the strip.  The
 // per-column arithmetic (pieces, MFMA, per-group FMA in group order, wave
 // order) is the kernel above's with the same waves and groups per wave: the
-// same bits.
-template <int GPW, int CPL, bool BF16>
+// same bits.  MR rows (1, 2 or 4 >= M): piece rows 4m .. 4m + 3 of the MFMA,
+// lane q < MR carries output row q (rows from M on are computed on the last
+// row's data and not stored).
+template <int MR, int GPW, int CPL, bool BF16>
 __global__ void __launch_bounds__(64 * 16)
 k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                  const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
-                 const void *__restrict__ Bias, int N, int K, int postop, int out_f32) {
-    constexpr int RR = kF4RowStride, P = f4_pieces(BF16);
+                 const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
+    static_assert(MR == 1 || MR == 2 || MR == 4, "one MFMA row set");
+    constexpr int RR = kF4RowStride * MR, P = f4_pieces(BF16);
     constexpr int WB = f4_window_bytes(RR, GPW);
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
@@ -775,15 +778,15 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     int s = blockIdx.x;
     if (s >= strips) return;  // (whole workgroup)
     uint8_t *wlds = lds8 + (size_t)wave * WB;
-    float *red = (float *)(lds8 + (size_t)W * WB);  // [2][W][CPL][16]
+    float *red = (float *)(lds8 + (size_t)W * WB);  // [2][W][CPL][MR][16]
 
-    F4Stage<1, GPW, BF16, 0> st;
-    st.load(A, 1, K, groups, g0w, lane);
+    F4Stage<MR, GPW, BF16, 0> st;
+    st.load(A, M, K, groups, g0w, lane);
     int after = f4_loads_after_barrier();
     F4Slab<CPL, GPW> cur;
     cur.load(B + after, S + after, N, groups, g0w, q, s * 16 * CPL + CPL * c);
-    F4EpiIn<1, CPL, BF16> ein;
-    ein.load(Other, Bias, postop, out_f32, 1, N, q, s * 16 * CPL + CPL * c, wave == 0);
+    F4EpiIn<MR, CPL, BF16> ein;
+    ein.load(Other, Bias, postop, out_f32, M, N, q, s * 16 * CPL + CPL * c, wave == 0);
     st.store(wlds, lane);
     asm volatile("" ::: "memory");  // this wave's staging writes precede its reads (in-order LDS per wave)
     const int rho = c & (RR - 1);
@@ -800,17 +803,17 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     // Strips in pairs with two register sets (ping-pong): a copy of the next
     // strip's registers into the current ones would wait for their loads.
     F4Slab<CPL, GPW> cur2;
-    F4EpiIn<1, CPL, BF16> ein2;
+    F4EpiIn<MR, CPL, BF16> ein2;
     int it = 0;
     // PRE: the next strip's loads first, unconditional (loads under a branch
     // are waited for at the branch's end, which would serialise them with this
     // strip's work); the last strip of the workgroup loads nothing.
-    auto strip = [&](F4Slab<CPL, GPW> &cu, F4EpiIn<1, CPL, BF16> &ec, F4Slab<CPL, GPW> &nx,
-                     F4EpiIn<1, CPL, BF16> &en, auto PRE_) __attribute__((always_inline)) {
+    auto strip = [&](F4Slab<CPL, GPW> &cu, F4EpiIn<MR, CPL, BF16> &ec, F4Slab<CPL, GPW> &nx,
+                     F4EpiIn<MR, CPL, BF16> &en, auto PRE_) __attribute__((always_inline)) {
         const int sn = s + (int)gridDim.x;
         if constexpr (decltype(PRE_)::value) {
             nx.load(B, S, N, groups, g0w, q, sn * 16 * CPL + CPL * c);
-            en.load(Other, Bias, postop, out_f32, 1, N, q, sn * 16 * CPL + CPL * c, wave == (it + 1) % W);
+            en.load(Other, Bias, postop, out_f32, M, N, q, sn * 16 * CPL + CPL * c, wave == (it + 1) % W);
         }
         float acc[CPL][P];
 #pragma unroll
@@ -833,33 +836,33 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 for (int i = 0; i < P; ++i) acc[j][i] = d[i] * sc + acc[j][i];
             }
         }
-        float *rb = red + (size_t)(it & 1) * W * CPL * 16;
-        if (q == 0) {
+        float *rb = red + (size_t)(it & 1) * W * CPL * MR * 16;
+        if (q < MR) {  // lane q: the pieces of row q
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 float out = acc[j][0];
 #pragma unroll
                 for (int i = 1; i < P; ++i) out += acc[j][i];
-                rb[(wave * CPL + j) * 16 + c] = out * 0.5f;  // the fp4 operand held 2v
+                rb[((wave * CPL + j) * MR + q) * 16 + c] = out * 0.5f;  // the fp4 operand held 2v
             }
         }
         __syncthreads();
-        if (wave == it % W && q == 0) {  // (wave-uniform) this strip's reducer
+        if (wave == it % W && q < M) {  // (wave-uniform) this strip's reducer, lane q row q
             float sum[CPL];
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) sum[j] = rb[j * 16 + c];
+            for (int j = 0; j < CPL; ++j) sum[j] = rb[(j * MR + q) * 16 + c];
             for (int w2 = 1; w2 < W; ++w2)
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) sum[j] += rb[(w2 * CPL + j) * 16 + c];
-            const int n0 = s * 16 * CPL + CPL * c;
+                for (int j = 0; j < CPL; ++j) sum[j] += rb[((w2 * CPL + j) * MR + q) * 16 + c];
+            const size_t o0 = (size_t)q * N + s * 16 * CPL + CPL * c;
             epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
                 constexpr int PO = decltype(P_)::value;
                 constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
                     const float r = epi_apply_c<PO>(sum[j], ec.other(0, j), ec.bias(j, F32));
-                    if constexpr (F32) ((float *)C)[n0 + j] = r;
-                    else ((uint16_t *)C)[n0 + j] = (uint16_t)f2dt<BF16>(r);
+                    if constexpr (F32) ((float *)C)[o0 + j] = r;
+                    else ((uint16_t *)C)[o0 + j] = (uint16_t)f2dt<BF16>(r);
                 }
             });
         }
@@ -898,6 +901,7 @@ constexpr size_t kF4MaxLds = 96 * 1024;
 // 6.37 against 6.82 us; K = 5120 N = 248320 72.0 against 100.8 us).
 constexpr int kF4msMinStrips = 160;
 constexpr int kF4msCpl = 2;  // its columns per lane (4: too many registers, measured slower)
+constexpr size_t kF4msMaxLds = 160 * 1024;  // a workgroup's LDS on gfx950
 
 int f4_mr(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -1180,8 +1184,8 @@ void f4ms_plan(int K, int &gpw, int &waves) {
     waves = (groups + gpw - 1) / gpw;
     if (waves > 16) waves = 0;
 }
-size_t f4ms_lds(int gpw, int waves, int cpl) {
-    return (size_t)waves * f4_window_bytes(kF4RowStride, gpw) + (size_t)2 * waves * cpl * 16 * 4;
+size_t f4ms_lds(int mr, int gpw, int waves, int cpl) {
+    return (size_t)waves * f4_window_bytes(kF4RowStride * mr, gpw) + (size_t)2 * waves * cpl * mr * 16 * 4;
 }
 
 // cpl: columns per lane (1, 2 or 4; 0 = automatic), strips of 16 cpl columns.
@@ -1204,45 +1208,70 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
     int gpw, waves;
     f4ms_plan(K, gpw, waves);
     if (cpl == 0) cpl = N % (16 * kF4msCpl) == 0 ? kF4msCpl : N % 32 == 0 ? 2 : 1;
-    if (M != 1 || waves == 0 || (cpl != 1 && cpl != 2 && cpl != 4) || N % (16 * cpl)) {
-        set_error("the multi-strip GEMV (engine 5) takes M = 1, K <= 8192, cols_per_lane 1, 2 or 4 and "
-                  "N % (16 * cols_per_lane) == 0");
+    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+    if (M < 1 || M > 4 || waves == 0 || (cpl != 1 && cpl != 2 && cpl != 4) || (cpl == 4 && mr > 1) ||
+        N % (16 * cpl) || f4ms_lds(mr, gpw, waves, cpl) > kF4msMaxLds) {
+        set_error("the multi-strip GEMV (engine 5) takes M <= 4, K <= 8192, cols_per_lane 1 or 2 (4 at M = 1) "
+                  "and N % (16 * cols_per_lane) == 0");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
     const int strips = N / (16 * cpl);
     const dim3 grid(f4ms_grid(strips, waves)), block(64 * waves);
-    const size_t lds = f4ms_lds(gpw, waves, cpl);
+    const size_t lds = f4ms_lds(mr, gpw, waves, cpl);
     const uint16_t *a = (const uint16_t *)A, *s = (const uint16_t *)S, *o = (const uint16_t *)Other;
-#define TCL_F4MS(G, CP, BF)                                                                                    \
-    hipLaunchKernelGGL((k_int2_gemv_f4ms<G, CP, BF>), grid, block, lds, st, a, B, s, C, o, Bias, N, K, postop, \
-                       out_f32)
-#define TCL_F4MS_C(G, BF)            \
-    do {                             \
-        if (cpl == 4) TCL_F4MS(G, 4, BF); \
-        else if (cpl == 2) TCL_F4MS(G, 2, BF); \
-        else TCL_F4MS(G, 1, BF);     \
+#define TCL_F4MS(R, G, CP, BF)                                                                                 \
+    hipLaunchKernelGGL((k_int2_gemv_f4ms<R, G, CP, BF>), grid, block, lds, st, a, B, s, C, o, Bias, M, N, K,  \
+                       postop, out_f32)
+#define TCL_F4MS_G(R, CP, BF)                \
+    do {                                     \
+        if (gpw == 4) TCL_F4MS(R, 4, CP, BF);     \
+        else if (gpw == 2) TCL_F4MS(R, 2, CP, BF); \
+        else TCL_F4MS(R, 1, CP, BF);         \
     } while (0)
-    const bool bf16 = dtype == TERNOCL_BF16;
-    if (gpw == 4) { if (bf16) TCL_F4MS_C(4, true); else TCL_F4MS_C(4, false); }
-    else if (gpw == 2) { if (bf16) TCL_F4MS_C(2, true); else TCL_F4MS_C(2, false); }
-    else { if (bf16) TCL_F4MS_C(1, true); else TCL_F4MS_C(1, false); }
-#undef TCL_F4MS_C
+#define TCL_F4MS_R(BF)                                                    \
+    do {                                                                  \
+        if (mr == 1) {                                                    \
+            if (cpl == 4) TCL_F4MS_G(1, 4, BF);                           \
+            else if (cpl == 2) TCL_F4MS_G(1, 2, BF);                      \
+            else TCL_F4MS_G(1, 1, BF);                                    \
+        } else if (mr == 2) {                                             \
+            if (cpl == 2) TCL_F4MS_G(2, 2, BF);                           \
+            else TCL_F4MS_G(2, 1, BF);                                    \
+        } else {                                                          \
+            if (cpl == 2) TCL_F4MS_G(4, 2, BF);                           \
+            else TCL_F4MS_G(4, 1, BF);                                    \
+        }                                                                 \
+    } while (0)
+    if (dtype == TERNOCL_BF16) TCL_F4MS_R(true);
+    else TCL_F4MS_R(false);
+#undef TCL_F4MS_R
+#undef TCL_F4MS_G
 #undef TCL_F4MS
     return launch_status(hipGetLastError());
 }
 
-// Whether the automatic choice for an M = 1 GEMV is the multi-strip kernel:
-// many strips per CU (the staging it saves grows with them) and all of K in
-// one window.
+// Whether the automatic choice for a GEMV of M <= 4 rows is the multi-strip
+// kernel: many strips per CU (the staging it saves grows with them) and all
+// of K in one window.  Graph-timed against the per-strip engine's automatic
+// plan (fp16, >2 GiB rotated), M = 2 / 4: K = 4096 N = 151680 47.0 / 57.2 ->
+// 32.3 / 32.4 us, K = 5120 N = 248320 110.7 / 226.2 -> 65.5 / 65.1, K = 5120
+// N = 34816 19.3 / 37.3 -> 13.2 / 14.7, K = 4096 N = 14336 (bf16, bias +
+// residual) 6.82 / 8.14 -> 6.46 / 7.63, K = 4096 N = 6144 6.19 / 8.16 -> 4.96 /
+// 5.98; below 160 strips the per-strip engine's K split wins (K = 8192 N =
+// 4096: 6.33 / 7.18 against 6.69 / 8.42).
 bool int2_gemv_f4ms_auto(int M, int N, int K) {
     int gpw, waves;
     f4ms_plan(K, gpw, waves);
-    return M == 1 && waves > 0 && N % (16 * kF4msCpl) == 0 && N / (16 * kF4msCpl) >= kF4msMinStrips;
+    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+    return M >= 1 && M <= 4 && waves > 0 && N % (16 * kF4msCpl) == 0 && N / (16 * kF4msCpl) >= kF4msMinStrips &&
+           f4ms_lds(mr, gpw, waves, kF4msCpl) <= kF4msMaxLds;
 }
 
-// Workspace bytes of the automatic plan (0: no K split).
+// Workspace bytes of the automatic plan (0: no K split; the multi-strip
+// kernel takes none).
 size_t int2_gemv_f4_ws_need(int M, int N, int K) {
     if (M < 1 || M > kF4MaxM || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    if (int2_gemv_f4ms_auto(M, N, K)) return 0;
     int cpl, ks;
     f4_auto_split(M, N, K, 0, cpl, ks);
     return f4_split_ws(M, N, ks);

@@ -402,7 +402,7 @@ def test_gemv_f4_wide_dynamic_range(dev, orc, bf16):
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
-# ---- the multi-strip GEMV (engine 5, M = 1) ----------------------------------------
+# ---- the multi-strip GEMV (engine 5, M <= 4) ---------------------------------------
 # (K, N): one window of waves x groups per wave covering K (1, 2 and 4 groups per
 # wave, up to 16 waves), fewer strips than workgroups, many strips per workgroup,
 # the two reference LM heads (int2_fp16_upcvt/bench.sh:12) and a 129-strip N
@@ -416,26 +416,30 @@ def _ms_plan(K):
     return gpw, (groups + gpw - 1) // gpw
 
 
+MULTISTRIP_M = [(M, K, N) for K, N in MULTISTRIP for M in (1, 2, 3, 4) if M == 1 or N <= 40960]
+
+
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("K,N", MULTISTRIP)
-def test_gemv_multistrip_parity(dev, orc, K, N, bf16):
+@pytest.mark.parametrize("M,K,N", MULTISTRIP_M)
+def test_gemv_multistrip_parity(dev, orc, M, K, N, bf16):
     """Engine 5 gives engine 4's bits when engine 4 runs the same waves and groups per
-    wave on 16-column strips (the same per-column arithmetic in the same order), with
-    and without the bias + residual epilogue, and every output within 1e-3 + 1e-2 |ref|
-    of the host gold."""
+    wave on 16-column strips (the same per-column arithmetic in the same order; engine 4
+    takes at most 8 waves above one row), with and without the bias + residual epilogue,
+    and every output within 1e-3 + 1e-2 |ref| of the host gold; rows M = 1..4 (3: the
+    4-row kernel with its last row not stored)."""
     import ternocl_amd as T
-    M = 1
     gpw, waves = _ms_plan(K)
-    print(f"gemv multi-strip K={K} N={N} bf16={bf16} (waves {waves} x {gpw} groups)", flush=True)
-    A, B, S, other, bias_f = _inputs(77 + K + N, M, K, N, bf16)
+    print(f"gemv multi-strip M={M} K={K} N={N} bf16={bf16} (waves {waves} x {gpw} groups)", flush=True)
+    A, B, S, other, bias_f = _inputs(77 + K + N + M, M, K, N, bf16)
     for postop, cpl in ((0, 0), (5, 1), (5, 2), (5, 4)):
-        if N % (16 * max(cpl, 1)):
+        if N % (16 * max(cpl, 1)) or (cpl == 4 and M > 1):
             continue
         ms, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
                      tile=T.gemv_tile(T.F4MS, 0, cpl))
-        f4, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
-                     tile=T.gemv_tile(T.F4, waves, 1, gpw, 0, 1))
-        assert np.array_equal(host_u16(ms), host_u16(f4)), f"postop {postop}: engine 5 differs from engine 4"
+        if M == 1 or waves <= 8:
+            f4, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
+                         tile=T.gemv_tile(T.F4, waves, 1, gpw, 0, 1))
+            assert np.array_equal(host_u16(ms), host_u16(f4)), f"postop {postop}: engine 5 differs from engine 4"
         want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, False)
         bad, dmax = allclose_report(formats.dt_to_f32(host_u16(ms), bf16), formats.dt_to_f32(want, bf16))
         assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
@@ -458,8 +462,8 @@ def test_gemv_multistrip_epilogues(dev, orc, postop, out_f32):
 
 def test_gemv_multistrip_automatic_and_rejects(dev):
     """The automatic plan takes engine 5 at M = 1 from 160 strips of 32 columns (the same
-    bits as the explicit engine); engine 5 rejects M > 1, K past one window (64 groups)
-    and tile fields other than cols_per_lane."""
+    bits as the explicit engine); engine 5 rejects M > 4, cols_per_lane 4 above one row, K
+    past one window (64 groups) and tile fields other than cols_per_lane."""
     import torch
     import ternocl_amd as T
     K, N = 4096, 5120
@@ -472,10 +476,13 @@ def test_gemv_multistrip_automatic_and_rejects(dev):
     T.int2_fp16_upcvt_gemm(A, B, S, c1, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS))
     torch.cuda.synchronize()
     assert torch.equal(c0, c1)
-    A2 = torch.zeros((2, K), dtype=torch.bfloat16, device="cuda")
-    C2 = torch.zeros((2, N), dtype=torch.bfloat16, device="cuda")
+    A5 = torch.zeros((5, K), dtype=torch.bfloat16, device="cuda")
+    C5 = torch.zeros((5, N), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(T.TernoclError) as e:
-        T.int2_fp16_upcvt_gemm(A2, B, S, C2, None, None, 2, N, K, tile=T.gemv_tile(T.F4MS))
+        T.int2_fp16_upcvt_gemm(A5, B, S, C5, None, None, 5, N, K, tile=T.gemv_tile(T.F4MS))
+    assert e.value.status == 2
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(A5, B, S, C5, None, None, 2, N, K, tile=T.gemv_tile(T.F4MS, 0, 4))
     assert e.value.status == 2
     with pytest.raises(T.TernoclError) as e:
         T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS, 8))
