@@ -760,14 +760,19 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // order) is the kernel above's with the same waves and groups per wave: the
 // same bits.  MR rows (1, 2 or 4 >= M): piece rows 4m .. 4m + 3 of the MFMA,
 // lane q < MR carries output row q (rows from M on are computed on the last
-// row's data and not stored).
-template <int MR, int GPW, int CPL, bool BF16>
+// row's data and not stored).  QM 1 / 2: the s8 x s2 GEMV's int8 modes (the
+// kernel above's QM 1 / 2: A int8, or DT quantized while staged; SA [K/128]
+// [ldsa]), each group's 1 / SA[g, q] held in registers beside its fragments.
+template <int MR, int GPW, int CPL, bool BF16, int QM = 0>
 __global__ void __launch_bounds__(64 * 16)
 k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                  const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
-                 const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32) {
+                 const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32,
+                 const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
     static_assert(MR == 1 || MR == 2 || MR == 4, "one MFMA row set");
-    constexpr int RR = kF4RowStride * MR, P = f4_pieces(BF16);
+    static_assert(QM == 0 || QM == 1 || QM == 2, "DT or int8 activations");
+    constexpr bool I8 = QM != 0;
+    constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
     constexpr int WB = f4_window_bytes(RR, GPW);
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
@@ -780,8 +785,8 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     uint8_t *wlds = lds8 + (size_t)wave * WB;
     float *red = (float *)(lds8 + (size_t)W * WB);  // [2][W][CPL][MR][16]
 
-    F4Stage<MR, GPW, BF16, 0> st;
-    st.load(A, M, K, groups, g0w, lane);
+    F4Stage<MR, GPW, BF16, QM> st;
+    st.load(A, M, K, groups, g0w, lane, SA, ldsa);
     int after = f4_loads_after_barrier();
     F4Slab<CPL, GPW> cur;
     cur.load(B + after, S + after, N, groups, g0w, q, s * 16 * CPL + CPL * c);
@@ -792,12 +797,15 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int rho = c & (RR - 1);
     v8i_t av[GPW];
     int sa[GPW];
+    float inv[GPW];  // int8 modes: 1 / SA[g, m] of row m = q (clamped into the rows staged)
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
         const int pr = gi * RR + rho;
         const uint8_t *row = wlds + pr * 128 + 32 * q;
         const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
         sa[gi] = wlds[GPW * RR * 128 + pr * 4 + q];
+        inv[gi] = I8 ? *(const float *)(wlds + GPW * RR * 128 + (gi * RR + RS * (q < MR ? q : MR - 1) + 2) * 4)
+                     : 0.0f;
         av[gi] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
     }
     // Strips in pairs with two register sets (ping-pong): a copy of the next
@@ -826,14 +834,24 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 uint32_t d0, d1, e0, e1;
-                f4_decode(cu.w[gi][0].v[j], d0, d1);
-                f4_decode(cu.w[gi][1].v[j], e0, e1);
+                if constexpr (I8) {
+                    f4_decode_s2(cu.w[gi][0].v[j], d0, d1);
+                    f4_decode_s2(cu.w[gi][1].v[j], e0, e1);
+                } else {
+                    f4_decode(cu.w[gi][0].v[j], d0, d1);
+                    f4_decode(cu.w[gi][1].v[j], e0, e1);
+                }
                 const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
                 const float sc = dt2f<BF16>(cu.scale(gi, j));
                 const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                     av[gi], bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa[gi], 0, 127);
+                if constexpr (I8) {
+                    const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
+                    acc[j][0] += dot * (sc * inv[gi]);
+                } else {
 #pragma unroll
-                for (int i = 0; i < P; ++i) acc[j][i] = d[i] * sc + acc[j][i];
+                    for (int i = 0; i < P; ++i) acc[j][i] = d[i] * sc + acc[j][i];
+                }
             }
         }
         float *rb = red + (size_t)(it & 1) * W * CPL * MR * 16;
@@ -841,9 +859,12 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 float out = acc[j][0];
+                if constexpr (!I8) {
 #pragma unroll
-                for (int i = 1; i < P; ++i) out += acc[j][i];
-                rb[((wave * CPL + j) * MR + q) * 16 + c] = out * 0.5f;  // the fp4 operand held 2v
+                    for (int i = 1; i < P; ++i) out += acc[j][i];
+                    out *= 0.5f;  // the fp4 operand held 2v
+                }
+                rb[((wave * CPL + j) * MR + q) * 16 + c] = out;
             }
         }
         __syncthreads();
@@ -1398,12 +1419,41 @@ static int f4q_auto_split(int M, int N, int K, int &cpl) {
 
 size_t int2_int8_gemv_ws_need(int M, int N, int K) {
     if (M < 1 || M > kF4MaxMI8 || N < 16 || N % 16 || K < kGS || K % kGS) return 0;
+    if (int2_gemv_f4ms_auto(M, N, K)) return 0;  // the multi-strip kernel takes none
     int cpl;
     return f4_split_ws(M, N, f4q_auto_split(M, N, K, cpl));
 }
 
 // ws (16-byte aligned, int2_int8_gemv_ws_need bytes, zeroed once before its
 // first use): the automatic K split; NULL or short: one slice.
+// The multi-strip kernel in an int8 mode (QM 1: A = Aq int8, 2: A = DT
+// quantized while staged), 32-column strips; the host has checked
+// int2_gemv_f4ms_auto(M, N, K).
+template <int QM, bool BF16>
+static hipError_t f4ms_q_launch(const void *A, const void *SA, int ldsa, const uint32_t *B, const void *S, void *C,
+                                const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
+                                hipStream_t st) {
+    int gpw, waves;
+    f4ms_plan(K, gpw, waves);
+    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : 4, strips = N / 32;
+    const dim3 grid(f4ms_grid(strips, waves)), block(64 * waves);
+    const size_t lds = f4ms_lds(mr, gpw, waves, 2);
+    auto go = [&](auto R_, auto G_) {
+        hipLaunchKernelGGL((k_int2_gemv_f4ms<decltype(R_)::value, decltype(G_)::value, 2, BF16, QM>), grid, block,
+                           lds, st, (const uint16_t *)A, B, (const uint16_t *)S, C, (const uint16_t *)Other, Bias, M,
+                           N, K, postop, out_f32, (const uint16_t *)SA, ldsa);
+    };
+    auto rows = [&](auto G_) {
+        if (mr == 1) go(std::integral_constant<int, 1>{}, G_);
+        else if (mr == 2) go(std::integral_constant<int, 2>{}, G_);
+        else go(std::integral_constant<int, 4>{}, G_);
+    };
+    if (gpw == 4) rows(std::integral_constant<int, 4>{});
+    else if (gpw == 2) rows(std::integral_constant<int, 2>{});
+    else rows(std::integral_constant<int, 1>{});
+    return hipGetLastError();
+}
+
 ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
@@ -1411,6 +1461,18 @@ ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, co
     if (!int2_int8_gemv_supports(M, N, K, A, Aq)) {
         set_error("the s8 x s2 GEMV takes M <= 4, N % 16 == 0 and aligned activations");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
+    if (int2_gemv_f4ms_auto(M, N, K)) {  // many strips: the multi-strip kernel, as the int2 GEMV
+        const int ldsa = (M + 31) & ~31;
+        const bool bf = dtype == TERNOCL_BF16;
+        hipError_t e;
+        if (Aq)
+            e = bf ? f4ms_q_launch<1, true>(Aq, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+                   : f4ms_q_launch<1, false>(Aq, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
+        else
+            e = bf ? f4ms_q_launch<2, true>(A, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+                   : f4ms_q_launch<2, false>(A, SA, ldsa, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
+        return launch_status(e);
     }
     int cpl = 0, ks = f4q_auto_split(M, N, K, cpl);
     if (ks > 1 && !(ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= f4_split_ws(M, N, ks))) {
