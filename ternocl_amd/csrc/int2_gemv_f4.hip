@@ -758,21 +758,26 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // strip) and wave it % W adds them in wave order and stores the strip.  The
 // per-column arithmetic (pieces, MFMA, per-group FMA in group order, wave
 // order) is the kernel above's with the same waves and groups per wave: the
-// same bits.  MR rows (1, 2 or 4 >= M): piece rows 4m .. 4m + 3 of the MFMA,
-// lane q < MR carries output row q (rows from M on are computed on the last
-// row's data and not stored).  QM 1 / 2: the s8 x s2 GEMV's int8 modes (the
-// kernel above's QM 1 / 2: A int8, or DT quantized while staged; SA [K/128]
-// [ldsa]), each group's 1 / SA[g, q] held in registers beside its fragments.
+// same bits.  MR rows (1, 2, 4 or 8 >= M): piece rows 4m .. 4m + 3 of the
+// MFMA; up to 4 rows one MFMA per group and 16 columns, 8 rows two (row sets t
+// = 0, 1: rows m = 4t + q); lane q carries output rows q + 4t (rows from M on
+// are computed on the last row's data and not stored).  MR 8: at most 8 waves
+// (the registers of two row sets), and the wave partials reuse the staging
+// windows once the fragments are in registers.  QM 1 / 2 (MR <= 4): the s8 x
+// s2 GEMV's int8 modes (the kernel above's QM 1 / 2: A int8, or DT quantized
+// while staged; SA [K/128][ldsa]), each group's 1 / SA[g, q] held in
+// registers beside its fragments.
 template <int MR, int GPW, int CPL, bool BF16, int QM = 0>
-__global__ void __launch_bounds__(64 * 16)
+__global__ void __launch_bounds__(MR > 4 ? 64 * 8 : 64 * 16)
 k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                  const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
                  const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32,
                  const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
-    static_assert(MR == 1 || MR == 2 || MR == 4, "one MFMA row set");
-    static_assert(QM == 0 || QM == 1 || QM == 2, "DT or int8 activations");
+    static_assert(MR == 1 || MR == 2 || MR == 4 || MR == 8, "1, 2, 4 or 8 rows");
+    static_assert(QM == 0 || ((QM == 1 || QM == 2) && MR <= 4), "DT, or int8 activations up to 4 rows");
     constexpr bool I8 = QM != 0;
     constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
+    constexpr int RSETS = f4_rsets(MR), RR1 = RR < 16 ? RR : 16, QV = MR < 4 ? MR : 4;
     constexpr int WB = f4_window_bytes(RR, GPW);
     extern __shared__ uint8_t lds8[];
     const int W = blockDim.x >> 6;
@@ -783,7 +788,7 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     int s = blockIdx.x;
     if (s >= strips) return;  // (whole workgroup)
     uint8_t *wlds = lds8 + (size_t)wave * WB;
-    float *red = (float *)(lds8 + (size_t)W * WB);  // [2][W][CPL][MR][16]
+    float *red = (float *)(lds8 + (MR > 4 ? (size_t)0 : (size_t)W * WB));  // [2][W][CPL][MR][16]
 
     F4Stage<MR, GPW, BF16, QM> st;
     st.load(A, M, K, groups, g0w, lane, SA, ldsa);
@@ -794,20 +799,24 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     ein.load(Other, Bias, postop, out_f32, M, N, q, s * 16 * CPL + CPL * c, wave == 0);
     st.store(wlds, lane);
     asm volatile("" ::: "memory");  // this wave's staging writes precede its reads (in-order LDS per wave)
-    const int rho = c & (RR - 1);
-    v8i_t av[GPW];
-    int sa[GPW];
+    const int rho = c & (RR1 - 1);
+    v8i_t av[RSETS][GPW];
+    int sa[RSETS][GPW];
     float inv[GPW];  // int8 modes: 1 / SA[g, m] of row m = q (clamped into the rows staged)
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
-        const int pr = gi * RR + rho;
-        const uint8_t *row = wlds + pr * 128 + 32 * q;
-        const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
-        sa[gi] = wlds[GPW * RR * 128 + pr * 4 + q];
+#pragma unroll
+        for (int t = 0; t < RSETS; ++t) {
+            const int pr = gi * RR + 16 * t + rho;
+            const uint8_t *row = wlds + pr * 128 + 32 * q;
+            const uint4 a0 = *(const uint4 *)row, a1 = *(const uint4 *)(row + 16);
+            sa[t][gi] = wlds[GPW * RR * 128 + pr * 4 + q];
+            av[t][gi] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        }
         inv[gi] = I8 ? *(const float *)(wlds + GPW * RR * 128 + (gi * RR + RS * (q < MR ? q : MR - 1) + 2) * 4)
                      : 0.0f;
-        av[gi] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
     }
+    if constexpr (MR > 4) __syncthreads();  // every wave's fragments read: the windows become the partials
     // Strips in pairs with two register sets (ping-pong): a copy of the next
     // strip's registers into the current ones would wait for their loads.
     F4Slab<CPL, GPW> cur2;
@@ -823,11 +832,13 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
             nx.load(B, S, N, groups, g0w, q, sn * 16 * CPL + CPL * c);
             en.load(Other, Bias, postop, out_f32, M, N, q, sn * 16 * CPL + CPL * c, wave == (it + 1) % W);
         }
-        float acc[CPL][P];
+        float acc[RSETS][CPL][P];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j)
+        for (int t = 0; t < RSETS; ++t)
 #pragma unroll
-            for (int i = 0; i < P; ++i) acc[j][i] = 0.0f;
+            for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int i = 0; i < P; ++i) acc[t][j][i] = 0.0f;
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
             if (g0w + gi >= groups) break;  // uniform across the wave
@@ -843,49 +854,59 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 }
                 const v8i_t bv = {(int)d0, (int)d1, (int)e0, (int)e1, 0, 0, 0, 0};
                 const float sc = dt2f<BF16>(cu.scale(gi, j));
-                const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    av[gi], bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa[gi], 0, 127);
-                if constexpr (I8) {
-                    const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
-                    acc[j][0] += dot * (sc * inv[gi]);
-                } else {
 #pragma unroll
-                    for (int i = 0; i < P; ++i) acc[j][i] = d[i] * sc + acc[j][i];
+                for (int t = 0; t < RSETS; ++t) {
+                    const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        av[t][gi], bv, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sa[t][gi], 0, 127);
+                    if constexpr (I8) {
+                        const float dot = (d[0] + d[1]) * 0.5f;  // the group's int32 dot product
+                        acc[t][j][0] += dot * (sc * inv[gi]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < P; ++i) acc[t][j][i] = d[i] * sc + acc[t][j][i];
+                    }
                 }
             }
         }
         float *rb = red + (size_t)(it & 1) * W * CPL * MR * 16;
-        if (q < MR) {  // lane q: the pieces of row q
+        if (q < QV) {  // lane q: the pieces of rows q + 4t
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                float out = acc[j][0];
-                if constexpr (!I8) {
-#pragma unroll
-                    for (int i = 1; i < P; ++i) out += acc[j][i];
-                    out *= 0.5f;  // the fp4 operand held 2v
-                }
-                rb[((wave * CPL + j) * MR + q) * 16 + c] = out;
-            }
-        }
-        __syncthreads();
-        if (wave == it % W && q < M) {  // (wave-uniform) this strip's reducer, lane q row q
-            float sum[CPL];
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) sum[j] = rb[(j * MR + q) * 16 + c];
-            for (int w2 = 1; w2 < W; ++w2)
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) sum[j] += rb[((w2 * CPL + j) * MR + q) * 16 + c];
-            const size_t o0 = (size_t)q * N + s * 16 * CPL + CPL * c;
-            epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
-                constexpr int PO = decltype(P_)::value;
-                constexpr bool F32 = decltype(F_)::value;
+            for (int t = 0; t < RSETS; ++t)
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
-                    const float r = epi_apply_c<PO>(sum[j], ec.other(0, j), ec.bias(j, F32));
-                    if constexpr (F32) ((float *)C)[o0 + j] = r;
-                    else ((uint16_t *)C)[o0 + j] = (uint16_t)f2dt<BF16>(r);
+                    float out = acc[t][j][0];
+                    if constexpr (!I8) {
+#pragma unroll
+                        for (int i = 1; i < P; ++i) out += acc[t][j][i];
+                        out *= 0.5f;  // the fp4 operand held 2v
+                    }
+                    rb[((wave * CPL + j) * MR + q + 4 * t) * 16 + c] = out;
                 }
-            });
+        }
+        __syncthreads();
+        if (wave == it % W && q < QV) {  // (wave-uniform) this strip's reducer, lane q rows q + 4t
+#pragma unroll
+            for (int t = 0; t < RSETS; ++t) {
+                const int m = q + 4 * t;
+                float sum[CPL];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) sum[j] = rb[(j * MR + m) * 16 + c];
+                for (int w2 = 1; w2 < W; ++w2)
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) sum[j] += rb[((w2 * CPL + j) * MR + m) * 16 + c];
+                const size_t o0 = (size_t)m * N + s * 16 * CPL + CPL * c;
+                if (m < M)
+                    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+                        constexpr int PO = decltype(P_)::value;
+                        constexpr bool F32 = decltype(F_)::value;
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j) {
+                            const float r = epi_apply_c<PO>(sum[j], ec.other(t, j), ec.bias(j, F32));
+                            if constexpr (F32) ((float *)C)[o0 + j] = r;
+                            else ((uint16_t *)C)[o0 + j] = (uint16_t)f2dt<BF16>(r);
+                        }
+                    });
+            }
         }
         ++it;
         s = sn;
@@ -1197,16 +1218,22 @@ void f4_auto_split(int M, int N, int K, int cpl_req, int &cpl, int &ks) {
     }
 }
 
-// The multi-strip GEMV's plan for K: groups per wave (1, 2 or 4) and waves
-// (<= 16) holding all of K in one window; 0 waves: K too long (> 64 groups).
-void f4ms_plan(int K, int &gpw, int &waves) {
+// The multi-strip GEMV's plan for K and mr rows: groups per wave (1, 2 or 4)
+// and waves (<= 16; 8 rows: <= 8) holding all of K in one window; 0 waves: K
+// too long (> 64 groups; 8 rows: > 32).
+void f4ms_plan(int K, int &gpw, int &waves, int mr = 1) {
     const int groups = K / kGS;
-    gpw = groups >= 32 ? 4 : groups >= 16 ? 2 : 1;
+    if (mr > 4) gpw = groups > 16 ? 4 : groups > 8 ? 2 : 1;
+    else gpw = groups >= 32 ? 4 : groups >= 16 ? 2 : 1;
     waves = (groups + gpw - 1) / gpw;
-    if (waves > 16) waves = 0;
+    if (waves > (mr > 4 ? 8 : 16)) waves = 0;
 }
+// Staging windows, then the double-buffered wave partials (8 rows: the
+// partials in the windows' place).
 size_t f4ms_lds(int mr, int gpw, int waves, int cpl) {
-    return (size_t)waves * f4_window_bytes(kF4RowStride * mr, gpw) + (size_t)2 * waves * cpl * mr * 16 * 4;
+    const size_t win = (size_t)waves * f4_window_bytes(kF4RowStride * mr, gpw);
+    const size_t red = (size_t)2 * waves * cpl * mr * 16 * 4;
+    return mr > 4 ? std::max(win, red) : win + red;
 }
 
 // cpl: columns per lane (1, 2 or 4; 0 = automatic), strips of 16 cpl columns.
@@ -1216,9 +1243,10 @@ size_t f4ms_lds(int mr, int gpw, int waves, int cpl) {
 // mean): against 512 of them, K = 5120 N = 248320 70.9 -> 64.5 us, K = 7168
 // N = 28672 16.5 -> 14.7, K = 8192 N = 14336 11.4 -> 9.9, K = 3072 N = 32768
 // 10.0 -> 8.9; 8-wave workgroups lose that way (K = 4096 N = 151680 33.9 ->
-// 36.3, K = 2048 N = 65536 10.5 -> 12.8).
-int f4ms_grid(int strips, int waves) {
-    if (waves <= 8) return std::min(strips, 512);
+// 36.3, K = 2048 N = 65536 10.5 -> 12.8).  8 rows: one per CU too (their
+// staging windows take most of a CU's LDS).
+int f4ms_grid(int strips, int waves, int mr = 1) {
+    if (waves <= 8 && mr <= 4) return std::min(strips, 512);
     const int per = (strips + 255) / 256;
     return (strips + per - 1) / per;
 }
@@ -1226,18 +1254,18 @@ int f4ms_grid(int strips, int waves) {
 ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K, int postop,
                                   int out_f32, int cpl, hipStream_t st) {
+    const int mr = f4_mr(M);
     int gpw, waves;
-    f4ms_plan(K, gpw, waves);
+    f4ms_plan(K, gpw, waves, mr);
     if (cpl == 0) cpl = N % (16 * kF4msCpl) == 0 ? kF4msCpl : N % 32 == 0 ? 2 : 1;
-    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : 4;
-    if (M < 1 || M > 4 || waves == 0 || (cpl != 1 && cpl != 2 && cpl != 4) || (cpl == 4 && mr > 1) ||
+    if (M < 1 || M > 8 || waves == 0 || (cpl != 1 && cpl != 2 && cpl != 4) || (cpl == 4 && mr > 1) ||
         N % (16 * cpl) || f4ms_lds(mr, gpw, waves, cpl) > kF4msMaxLds) {
-        set_error("the multi-strip GEMV (engine 5) takes M <= 4, K <= 8192, cols_per_lane 1 or 2 (4 at M = 1) "
-                  "and N % (16 * cols_per_lane) == 0");
+        set_error("the multi-strip GEMV (engine 5) takes M <= 8, K <= 8192 (M > 4: K <= 4096), cols_per_lane "
+                  "1 or 2 (4 at M = 1) and N % (16 * cols_per_lane) == 0");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
     const int strips = N / (16 * cpl);
-    const dim3 grid(f4ms_grid(strips, waves)), block(64 * waves);
+    const dim3 grid(f4ms_grid(strips, waves, mr)), block(64 * waves);
     const size_t lds = f4ms_lds(mr, gpw, waves, cpl);
     const uint16_t *a = (const uint16_t *)A, *s = (const uint16_t *)S, *o = (const uint16_t *)Other;
 #define TCL_F4MS(R, G, CP, BF)                                                                                 \
@@ -1258,9 +1286,12 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
         } else if (mr == 2) {                                             \
             if (cpl == 2) TCL_F4MS_G(2, 2, BF);                           \
             else TCL_F4MS_G(2, 1, BF);                                    \
-        } else {                                                          \
+        } else if (mr == 4) {                                             \
             if (cpl == 2) TCL_F4MS_G(4, 2, BF);                           \
             else TCL_F4MS_G(4, 1, BF);                                    \
+        } else {                                                          \
+            if (cpl == 2) TCL_F4MS_G(8, 2, BF);                           \
+            else TCL_F4MS_G(8, 1, BF);                                    \
         }                                                                 \
     } while (0)
     if (dtype == TERNOCL_BF16) TCL_F4MS_R(true);
@@ -1279,12 +1310,17 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
 // N = 34816 19.3 / 37.3 -> 13.2 / 14.7, K = 4096 N = 14336 (bf16, bias +
 // residual) 6.82 / 8.14 -> 6.46 / 7.63, K = 4096 N = 6144 6.19 / 8.16 -> 4.96 /
 // 5.98; below 160 strips the per-strip engine's K split wins (K = 8192 N =
-// 4096: 6.33 / 7.18 against 6.69 / 8.42).
+// 4096: 6.33 / 7.18 against 6.69 / 8.42).  5..8 rows (K <= 4096, one
+// workgroup per CU), the same rule; M = 5 / 8 against the per-strip engine:
+// K = 4096 N = 151680 101.6 -> 49.7 us (M = 8), N = 24576 19.3 / 18.9 -> 14.5 /
+// 14.6, N = 14336 11.2 / 11.4 -> 11.1 / 11.1, N = 6144 11.6 -> 9.5, K = 3072
+// N = 32768 19.7 / 19.1 -> 15.3 / 15.4; N = 4096 (128 strips) 7.2 against 9.3.
 bool int2_gemv_f4ms_auto(int M, int N, int K) {
+    const int mr = f4_mr(M);
     int gpw, waves;
-    f4ms_plan(K, gpw, waves);
-    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : 4;
-    return M >= 1 && M <= 4 && waves > 0 && N % (16 * kF4msCpl) == 0 && N / (16 * kF4msCpl) >= kF4msMinStrips &&
+    f4ms_plan(K, gpw, waves, mr);
+    const int strips = N % (16 * kF4msCpl) == 0 ? N / (16 * kF4msCpl) : 0;
+    return M >= 1 && M <= 8 && waves > 0 && strips >= kF4msMinStrips &&
            f4ms_lds(mr, gpw, waves, kF4msCpl) <= kF4msMaxLds;
 }
 

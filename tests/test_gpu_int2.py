@@ -416,7 +416,8 @@ def _ms_plan(K):
     return gpw, (groups + gpw - 1) // gpw
 
 
-MULTISTRIP_M = [(M, K, N) for K, N in MULTISTRIP for M in (1, 2, 3, 4) if M == 1 or N <= 40960]
+MULTISTRIP_M = [(M, K, N) for K, N in MULTISTRIP for M in (1, 2, 3, 4, 5, 8)
+                if M == 1 or (N <= 40960 and (M <= 4 or K <= 4096))]
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -424,9 +425,10 @@ MULTISTRIP_M = [(M, K, N) for K, N in MULTISTRIP for M in (1, 2, 3, 4) if M == 1
 def test_gemv_multistrip_parity(dev, orc, M, K, N, bf16):
     """Engine 5 gives engine 4's bits when engine 4 runs the same waves and groups per
     wave on 16-column strips (the same per-column arithmetic in the same order; engine 4
-    takes at most 8 waves above one row), with and without the bias + residual epilogue,
-    and every output within 1e-3 + 1e-2 |ref| of the host gold; rows M = 1..4 (3: the
-    4-row kernel with its last row not stored)."""
+    takes at most 8 waves above one row, and at most 2 groups per wave at 8 rows, so those
+    shapes are checked against the gold only), with and without the bias + residual
+    epilogue, and every output within 1e-3 + 1e-2 |ref| of the host gold; rows M = 1..8
+    (3, 5: the 4- and 8-row kernels with their last rows not stored)."""
     import ternocl_amd as T
     gpw, waves = _ms_plan(K)
     print(f"gemv multi-strip M={M} K={K} N={N} bf16={bf16} (waves {waves} x {gpw} groups)", flush=True)
@@ -436,13 +438,31 @@ def test_gemv_multistrip_parity(dev, orc, M, K, N, bf16):
             continue
         ms, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
                      tile=T.gemv_tile(T.F4MS, 0, cpl))
-        if M == 1 or waves <= 8:
+        if M == 1 or (waves <= 8 and M <= 4):
             f4, _ = _run(T, __import__("torch"), A, B, S, other, bias_f, M, K, N, bf16, postop, False,
                          tile=T.gemv_tile(T.F4, waves, 1, gpw, 0, 1))
             assert np.array_equal(host_u16(ms), host_u16(f4)), f"postop {postop}: engine 5 differs from engine 4"
         want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, False)
         bad, dmax = allclose_report(formats.dt_to_f32(host_u16(ms), bf16), formats.dt_to_f32(want, bf16))
         assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("M,K,N", [(6, 1024, 65536), (8, 2048, 65536), (3, 4096, 5120), (5, 4096, 6144)])
+def test_gemv_multistrip_automatic_rows(dev, orc, M, K, N):
+    """The automatic plan at 3..8 rows where it takes the multi-strip kernel (from 160
+    strips of 32 columns; K <= 4096 above 4 rows): the same bits as the explicit engine and
+    the gold within the rule, with the bias + residual epilogue."""
+    import torch
+    import ternocl_amd as T
+    bf16 = True
+    print(f"gemv multi-strip automatic M={M} K={K} N={N}", flush=True)
+    A, B, S, other, bias_f = _inputs(313 + M, M, K, N, bf16)
+    auto, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 5, False)
+    ms, _ = _run(T, torch, A, B, S, other, bias_f, M, K, N, bf16, 5, False, tile=T.gemv_tile(T.F4MS))
+    assert np.array_equal(host_u16(auto), host_u16(ms))
+    want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, 5, False)
+    bad, dmax = allclose_report(formats.dt_to_f32(host_u16(auto), bf16), formats.dt_to_f32(want, bf16))
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
 @pytest.mark.parametrize("postop,out_f32", [(1, False), (2, True), (3, True), (4, False)])
@@ -462,8 +482,9 @@ def test_gemv_multistrip_epilogues(dev, orc, postop, out_f32):
 
 def test_gemv_multistrip_automatic_and_rejects(dev):
     """The automatic plan takes engine 5 at M = 1 from 160 strips of 32 columns (the same
-    bits as the explicit engine); engine 5 rejects M > 4, cols_per_lane 4 above one row, K
-    past one window (64 groups) and tile fields other than cols_per_lane."""
+    bits as the explicit engine); engine 5 rejects M > 8, K > 4096 above 4 rows,
+    cols_per_lane 4 above one row, K past one window (64 groups) and tile fields other than
+    cols_per_lane."""
     import torch
     import ternocl_amd as T
     K, N = 4096, 5120
@@ -476,13 +497,20 @@ def test_gemv_multistrip_automatic_and_rejects(dev):
     T.int2_fp16_upcvt_gemm(A, B, S, c1, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS))
     torch.cuda.synchronize()
     assert torch.equal(c0, c1)
-    A5 = torch.zeros((5, K), dtype=torch.bfloat16, device="cuda")
-    C5 = torch.zeros((5, N), dtype=torch.bfloat16, device="cuda")
+    A9 = torch.zeros((9, K), dtype=torch.bfloat16, device="cuda")
+    C9 = torch.zeros((9, N), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(T.TernoclError) as e:
-        T.int2_fp16_upcvt_gemm(A5, B, S, C5, None, None, 5, N, K, tile=T.gemv_tile(T.F4MS))
+        T.int2_fp16_upcvt_gemm(A9, B, S, C9, None, None, 9, N, K, tile=T.gemv_tile(T.F4MS))
     assert e.value.status == 2
     with pytest.raises(T.TernoclError) as e:
-        T.int2_fp16_upcvt_gemm(A5, B, S, C5, None, None, 2, N, K, tile=T.gemv_tile(T.F4MS, 0, 4))
+        T.int2_fp16_upcvt_gemm(A9, B, S, C9, None, None, 2, N, K, tile=T.gemv_tile(T.F4MS, 0, 4))
+    assert e.value.status == 2
+    K6 = 5120
+    A6 = torch.zeros((5, K6), dtype=torch.bfloat16, device="cuda")
+    B6 = torch.zeros((K6 // 16, N), dtype=torch.int32, device="cuda")
+    S6 = torch.zeros((K6 // 128, N), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(T.TernoclError) as e:
+        T.int2_fp16_upcvt_gemm(A6, B6, S6, C9, None, None, 5, N, K6, tile=T.gemv_tile(T.F4MS))
     assert e.value.status == 2
     with pytest.raises(T.TernoclError) as e:
         T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS, 8))
