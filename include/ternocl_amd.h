@@ -106,7 +106,7 @@ typedef struct {
                                A 16-byte aligned): a workgroup stages the activations once and
                                walks many column strips, loading the next strip's weights during
                                the current one's MFMAs (the automatic choice for N a multiple of
-                               32 from 5120 on); takes
+                               32 above 4096); takes
                                cols_per_lane only (1 or 2; 4 at M = 1) */
     int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
     int cols_per_lane;   /* MFMA: adjacent columns per lane, 1, 2 or 4 (16-, 32- or 64-column strips) */

@@ -936,12 +936,15 @@ struct F4Plan {
 };
 
 constexpr size_t kF4MaxLds = 96 * 1024;
-// The automatic plan of an M = 1 GEMV takes the multi-strip kernel from this
-// many 32-column strips on (graph-timed against the one-strip kernel over the
-// reference's benchmark shapes: K = N = 4096, 128 strips, 4.28 against 4.17 us;
-// K = 6144 N = 5120, 160 strips, 5.16 against 6.85 us; K = 4096 N = 14336
-// 6.37 against 6.82 us; K = 5120 N = 248320 72.0 against 100.8 us).
-constexpr int kF4msMinStrips = 160;
+// The automatic plan of a GEMV takes the multi-strip kernel from this many
+// 32-column strips on, i.e. past the 128 that put one per-strip workgroup of
+// 16 columns on each CU (graph-timed against the one-strip kernel, fp16: K = N
+// = 4096, 128 strips, 4.12 against 3.97 us; N = 4224 (132 strips): K = 4096
+// M = 1 / 4 / 8 4.17 / 5.87 / 9.45 against 5.46 / 8.40 / 11.54 us, K = 8192
+// 5.64 / 8.50 against 8.19 / 12.03, K = 2048 3.62 / 4.25 against 4.46 /
+// 4.99; K = 6144 N = 5120 5.16 against 6.85 us; K = 5120 N = 248320 72.0
+// against 100.8 us).
+constexpr int kF4msMinStrips = 129;
 constexpr int kF4msCpl = 2;  // its columns per lane (4: too many registers, measured slower)
 constexpr size_t kF4msMaxLds = 160 * 1024;  // a workgroup's LDS on gfx950
 

@@ -447,9 +447,10 @@ def test_gemv_multistrip_parity(dev, orc, M, K, N, bf16):
         assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
 
 
-@pytest.mark.parametrize("M,K,N", [(6, 1024, 65536), (8, 2048, 65536), (3, 4096, 5120), (5, 4096, 6144)])
+@pytest.mark.parametrize("M,K,N", [(6, 1024, 65536), (8, 2048, 65536), (3, 4096, 5120), (5, 4096, 6144),
+                                   (1, 8192, 4224), (4, 2048, 4128)])
 def test_gemv_multistrip_automatic_rows(dev, orc, M, K, N):
-    """The automatic plan at 3..8 rows where it takes the multi-strip kernel (from 160
+    """The automatic plan at 1..8 rows where it takes the multi-strip kernel (past 128
     strips of 32 columns; K <= 4096 above 4 rows): the same bits as the explicit engine and
     the gold within the rule, with the bias + residual epilogue."""
     import torch
@@ -481,7 +482,7 @@ def test_gemv_multistrip_epilogues(dev, orc, postop, out_f32):
 
 
 def test_gemv_multistrip_automatic_and_rejects(dev):
-    """The automatic plan takes engine 5 at M = 1 from 160 strips of 32 columns (the same
+    """The automatic plan takes engine 5 at M = 1 past 128 strips of 32 columns (the same
     bits as the explicit engine); engine 5 rejects M > 8, K > 4096 above 4 rows,
     cols_per_lane 4 above one row, K past one window (64 groups) and tile fields other than
     cols_per_lane."""
