@@ -102,12 +102,13 @@ typedef struct {
                             3: MFMA prefill GEMM (any M, 128 x 128 tiles; the M > 16 engine);
                             4: block-scaled fp8 x fp4 MFMA GEMV (M <= 8, A 16-byte aligned;
                                the automatic choice where it applies);
-                            5: its multi-strip form (M <= 8, K <= 8192 and at M > 4 K <= 4096,
-                               A 16-byte aligned): a workgroup stages the activations once and
-                               walks many column strips, loading the next strip's weights during
-                               the current one's MFMAs (the automatic choice for N a multiple of
-                               32 above 4096); takes
-                               cols_per_lane only (1 or 2; 4 at M = 1) */
+                            5: its multi-strip form (M <= 8, K per slice <= 8192 and at
+                               M > 4 <= 4096, A 16-byte aligned): a workgroup stages the
+                               activations once and walks many column strips, loading the next
+                               strip's weights during the current one's MFMAs (the automatic
+                               choice for N a multiple of 32 above 4096); takes cols_per_lane
+                               (1 or 2; 4 at M = 1), groups_per_wave (1, 2 or 4; its waves follow)
+                               and k_slices (with the ws above) */
     int waves;           /* waves per workgroup: VALU 1..16 (M = 1) or 1..8, MFMA 1..8 */
     int cols_per_lane;   /* MFMA: adjacent columns per lane, 1, 2 or 4 (16-, 32- or 64-column strips) */
     int groups_per_wave; /* MFMA: 128-row groups per wave per LDS window, 1..16 (power of

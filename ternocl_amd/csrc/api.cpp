@@ -53,7 +53,8 @@ ternocl_status int2_gemv_f4_run(int dtype, const void *A, const uint32_t *B, con
 size_t int2_gemv_f4_ws_need(int M, int N, int K);
 ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K, int postop,
-                                  int out_f32, int cpl, hipStream_t st);
+                                  int out_f32, int cpl, int gpw, int ks, void *ws, size_t ws_bytes,
+                                  hipStream_t st);
 bool int2_gemv_f4ms_auto(int M, int N, int K);
 ternocl_status int2_f4_decode_run(const uint32_t *B, uint32_t *D, int K, int N, hipStream_t st);
 ternocl_status stream_read_run(const void *src, size_t bytes, void *sink, hipStream_t st);  // misc.hip
@@ -219,13 +220,13 @@ ternocl_status ternocl_int2_fp16_upcvt_gemm_ex(int dtype, const void *A, const u
         const bool auto_tile = t.engine == 0 && t.waves == 0 && t.cols_per_lane == 0 && t.groups_per_wave == 0 &&
                                t.k_slices == 0;
         if (t.engine == 5 || (auto_tile && int2_gemv_f4_supports(M, N, A) && int2_gemv_f4ms_auto(M, N, K))) {
-            if (t.waves || t.groups_per_wave || t.k_slices > 1)
-                FAIL(TERNOCL_ERR_INVALID_ARG, "the multi-strip GEMV (engine 5) takes cols_per_lane only "
-                                              "(its waves follow from K)");
+            if (t.waves)
+                FAIL(TERNOCL_ERR_INVALID_ARG, "the multi-strip GEMV (engine 5) takes cols_per_lane, "
+                                              "groups_per_wave and k_slices (its waves follow from them)");
             if (!int2_gemv_f4_supports(M, N, A))
-                FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the multi-strip GEMV takes M <= 4 and A 16-byte aligned");
+                FAIL(TERNOCL_ERR_UNSUPPORTED_SHAPE, "the multi-strip GEMV takes M <= 8 and A 16-byte aligned");
             return int2_gemv_f4ms_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.cols_per_lane,
-                                      (hipStream_t)stream);
+                                      t.groups_per_wave, t.k_slices, ws, ws_bytes, (hipStream_t)stream);
         }
         if (t.engine == 4 || (t.engine == 0 && int2_gemv_f4_supports(M, N, A)))
             return int2_gemv_f4_run(dtype, A, B, S, C, Other, Bias, M, N, K, postop, out_f32, t.waves,

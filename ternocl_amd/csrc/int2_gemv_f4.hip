@@ -766,13 +766,17 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // windows once the fragments are in registers.  QM 1 / 2 (MR <= 4): the s8 x
 // s2 GEMV's int8 modes (the kernel above's QM 1 / 2: A int8, or DT quantized
 // while staged; SA [K/128][ldsa]), each group's 1 / SA[g, q] held in
-// registers beside its fragments.
+// registers beside its fragments.  ksn > 1 (grid.y = ksn): K slice blockIdx.y
+// for every strip the workgroup walks; each strip's reducer stores the
+// slice's sums (part fp32 [ksn][M][N]) and arrives at the strip's counter, and
+// the last of the ksn adds the slices in order -- the kernel above's handoff.
 template <int MR, int GPW, int CPL, bool BF16, int QM = 0>
 __global__ void __launch_bounds__(MR > 4 ? 64 * 8 : 64 * 16)
 k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                  const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
                  const void *__restrict__ Bias, int M, int N, int K, int postop, int out_f32,
-                 const uint16_t *__restrict__ SA = nullptr, int ldsa = 0) {
+                 const uint16_t *__restrict__ SA = nullptr, int ldsa = 0, int ksn = 1, float *part = nullptr,
+                 uint32_t *cnt = nullptr) {
     static_assert(MR == 1 || MR == 2 || MR == 4 || MR == 8, "1, 2, 4 or 8 rows");
     static_assert(QM == 0 || ((QM == 1 || QM == 2) && MR <= 4), "DT, or int8 activations up to 4 rows");
     constexpr bool I8 = QM != 0;
@@ -783,7 +787,18 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int W = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
-    const int groups = K / kGS, g0w = wave * GPW;  // (the host keeps groups <= W GPW)
+    int groups = K / kGS;
+    const int g0w = wave * GPW;  // (the host keeps a slice's groups <= W GPW)
+    const int ks = ksn > 1 ? (int)blockIdx.y : 0;
+    if (ksn > 1) {  // slice ks: groups [ks gps, ks gps + gps) (the host keeps every slice non-empty)
+        const int gps = (groups + ksn - 1) / ksn, g_lo = ks * gps;
+        groups = min(gps, groups - g_lo);
+        if constexpr (QM == 1) A = (const uint16_t *)((const int8_t *)A + (size_t)g_lo * kGS);  // int8 rows
+        else A += (size_t)g_lo * kGS;
+        if constexpr (I8) SA += (size_t)g_lo * ldsa;
+        B += (size_t)g_lo * 8 * N;
+        S += (size_t)g_lo * N;
+    }
     const int strips = N / (16 * CPL);
     int s = blockIdx.x;
     if (s >= strips) return;  // (whole workgroup)
@@ -885,28 +900,75 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
         }
         __syncthreads();
         if (wave == it % W && q < QV) {  // (wave-uniform) this strip's reducer, lane q rows q + 4t
+            const int n0 = s * 16 * CPL + CPL * c;
+            float sum[RSETS][CPL];
 #pragma unroll
             for (int t = 0; t < RSETS; ++t) {
                 const int m = q + 4 * t;
-                float sum[CPL];
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) sum[j] = rb[(j * MR + m) * 16 + c];
+                for (int j = 0; j < CPL; ++j) sum[t][j] = rb[(j * MR + m) * 16 + c];
                 for (int w2 = 1; w2 < W; ++w2)
 #pragma unroll
-                    for (int j = 0; j < CPL; ++j) sum[j] += rb[((w2 * CPL + j) * MR + m) * 16 + c];
-                const size_t o0 = (size_t)m * N + s * 16 * CPL + CPL * c;
-                if (m < M)
-                    epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
-                        constexpr int PO = decltype(P_)::value;
-                        constexpr bool F32 = decltype(F_)::value;
-#pragma unroll
-                        for (int j = 0; j < CPL; ++j) {
-                            const float r = epi_apply_c<PO>(sum[j], ec.other(t, j), ec.bias(j, F32));
-                            if constexpr (F32) ((float *)C)[o0 + j] = r;
-                            else ((uint16_t *)C)[o0 + j] = (uint16_t)f2dt<BF16>(r);
-                        }
-                    });
+                    for (int j = 0; j < CPL; ++j) sum[t][j] += rb[((w2 * CPL + j) * MR + m) * 16 + c];
             }
+            bool last = true;
+            if (ksn > 1) {  // (uniform) the K-slice handoff of the kernel above, for strip s
+#pragma unroll
+                for (int t = 0; t < RSETS; ++t) {
+                    const int m = q + 4 * t;
+                    if (m < M)
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j)
+                            __hip_atomic_store(part + ((size_t)ks * M + m) * N + n0 + j, sum[t][j], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_s_waitcnt(0);
+                last = split_arrive(cnt + s, ksn, lane) == (uint32_t)(ksn - 1);
+                if (last) {
+                    for (int s0 = 0; s0 < ksn; s0 += 4) {
+                        float v[4][RSETS][CPL];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const int s2 = s0 + u < ksn ? s0 + u : ksn - 1;
+#pragma unroll
+                            for (int t = 0; t < RSETS; ++t) {
+                                const int m = q + 4 * t < M ? q + 4 * t : M - 1;
+#pragma unroll
+                                for (int j = 0; j < CPL; ++j)
+                                    v[u][t][j] = __hip_atomic_load(part + ((size_t)s2 * M + m) * N + n0 + j,
+                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            }
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            if (s0 + u >= ksn) break;
+#pragma unroll
+                            for (int t = 0; t < RSETS; ++t)
+#pragma unroll
+                                for (int j = 0; j < CPL; ++j)
+                                    sum[t][j] = s0 + u == 0 ? v[u][t][j] : sum[t][j] + v[u][t][j];
+                        }
+                    }
+                }
+            }
+            if (last)
+#pragma unroll
+                for (int t = 0; t < RSETS; ++t) {
+                    const int m = q + 4 * t;
+                    const size_t o0 = (size_t)m * N + n0;
+                    if (m < M)
+                        epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+                            constexpr int PO = decltype(P_)::value;
+                            constexpr bool F32 = decltype(F_)::value;
+#pragma unroll
+                            for (int j = 0; j < CPL; ++j) {
+                                const float r = epi_apply_c<PO>(sum[t][j], ec.other(t, j), ec.bias(j, F32));
+                                if constexpr (F32) ((float *)C)[o0 + j] = r;
+                                else ((uint16_t *)C)[o0 + j] = (uint16_t)f2dt<BF16>(r);
+                            }
+                        });
+                }
         }
         ++it;
         s = sn;
@@ -1254,26 +1316,47 @@ int f4ms_grid(int strips, int waves, int mr = 1) {
     return (strips + per - 1) / per;
 }
 
+// ks > 1: K slices of the workspace's split (f4_split_ws bytes; K per slice
+// within one window); gpw_req: groups per wave (0: f4ms_plan's).  Walkers per
+// slice: a grid of about 512 workgroups (256 above 8 waves or 4 rows).
 ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K, int postop,
-                                  int out_f32, int cpl, hipStream_t st) {
-    const int mr = f4_mr(M);
+                                  int out_f32, int cpl, int gpw_req, int ks_req, void *ws, size_t ws_bytes,
+                                  hipStream_t st) {
+    const int mr = f4_mr(M), groups = K / kGS;
+    const int ksn = ks_req > 1 ? f4_slices(groups, ks_req) : 1, gps = (groups + ksn - 1) / ksn;
     int gpw, waves;
-    f4ms_plan(K, gpw, waves, mr);
+    f4ms_plan(gps * kGS, gpw, waves, mr);
+    if (gpw_req > 0) {
+        gpw = gpw_req;
+        waves = (gps + gpw - 1) / gpw;
+        if (gpw != 1 && gpw != 2 && gpw != 4) waves = 0;
+        if (waves > (mr > 4 ? 8 : 16)) waves = 0;
+    }
     if (cpl == 0) cpl = N % (16 * kF4msCpl) == 0 ? kF4msCpl : N % 32 == 0 ? 2 : 1;
     if (M < 1 || M > 8 || waves == 0 || (cpl != 1 && cpl != 2 && cpl != 4) || (cpl == 4 && mr > 1) ||
         N % (16 * cpl) || f4ms_lds(mr, gpw, waves, cpl) > kF4msMaxLds) {
-        set_error("the multi-strip GEMV (engine 5) takes M <= 8, K <= 8192 (M > 4: K <= 4096), cols_per_lane "
-                  "1 or 2 (4 at M = 1) and N % (16 * cols_per_lane) == 0");
+        set_error("the multi-strip GEMV (engine 5) takes M <= 8, K per slice <= 8192 (M > 4: <= 4096), "
+                  "groups_per_wave 1, 2 or 4 with at most 16 waves, cols_per_lane 1 or 2 (4 at M = 1) and "
+                  "N % (16 * cols_per_lane) == 0");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
+    if (ksn > 1 && !(f4_cnt_fit(N) && ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= f4_split_ws(M, N, ksn))) {
+        set_error("k_slices > 1 needs a 16-byte aligned workspace of ternocl_int2_gemm_ws_bytes() bytes for "
+                  "that split (and at most 16384 column strips)");
+        return TERNOCL_ERR_WORKSPACE;
+    }
     const int strips = N / (16 * cpl);
-    const dim3 grid(f4ms_grid(strips, waves, mr)), block(64 * waves);
+    const int walkers = ksn > 1 ? std::min(strips, std::max(1, (waves > 8 || mr > 4 ? 256 : 512) / ksn))
+                                : f4ms_grid(strips, waves, mr);
+    const dim3 grid(walkers, ksn), block(64 * waves);
     const size_t lds = f4ms_lds(mr, gpw, waves, cpl);
     const uint16_t *a = (const uint16_t *)A, *s = (const uint16_t *)S, *o = (const uint16_t *)Other;
+    float *part = ksn > 1 ? (float *)((uint8_t *)ws + kWsHeader) : nullptr;
+    uint32_t *cnt = ksn > 1 ? (uint32_t *)ws : nullptr;
 #define TCL_F4MS(R, G, CP, BF)                                                                                 \
     hipLaunchKernelGGL((k_int2_gemv_f4ms<R, G, CP, BF>), grid, block, lds, st, a, B, s, C, o, Bias, M, N, K,  \
-                       postop, out_f32)
+                       postop, out_f32, nullptr, 0, ksn, part, cnt)
 #define TCL_F4MS_G(R, CP, BF)                \
     do {                                     \
         if (gpw == 4) TCL_F4MS(R, 4, CP, BF);     \

@@ -481,11 +481,56 @@ def test_gemv_multistrip_epilogues(dev, orc, postop, out_f32):
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
 
+# (M, K, N, k_slices, groups per wave): one window per slice (K = 17408: 5 slices,
+# the last of 24 groups), one strip per workgroup and many (N = 40960: 1280
+# strips of 32 columns over 128 walkers per slice), 8 rows (two row sets)
+MS_KSPLIT = [(1, 14336, 4096, 4, 2), (1, 14336, 4096, 2, 4), (3, 17408, 5120, 5, 4), (4, 8192, 4096, 4, 2),
+             (8, 4096, 8192, 2, 2), (1, 16384, 40960, 4, 4), (2, 32768, 1024, 8, 4)]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N,ks,gpw", MS_KSPLIT)
+def test_gemv_multistrip_k_slices(dev, orc, M, K, N, ks, gpw, bf16):
+    """Engine 5 over K slices (the workspace's slice sums and strip counters): engine 4's
+    bits on the same slices, waves and groups per wave (the same per-column sums, added
+    in slice order), bit-identical over repeated calls, the counters back at zero, and
+    the gold within 1e-3 + 1e-2 |ref|, with and without the bias + residual epilogue."""
+    import torch
+    import ternocl_amd as T
+    groups = K // 128
+    gps = -(-groups // ks)
+    waves = -(-gps // gpw)
+    print(f"gemv multi-strip k-slices M={M} K={K} N={N} ks={ks} gpw={gpw} waves={waves} bf16={bf16}", flush=True)
+    A, B, S, other, bias_f = _inputs(171 + M + ks + gpw, M, K, N, bf16)
+    dA, dB, dS, dO = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16), dev_dt(other, bf16)
+    dBias = dev_dt(formats.f32_to_dt(bias_f, bf16), bf16)
+    ws = torch.zeros(T.WS_HEADER_BYTES + ks * M * N * 4, dtype=torch.uint8, device="cuda")
+    cnt_bytes = (N // 16) * 4
+    for postop in (0, 5):
+        outs = []
+        for _ in range(3):
+            dC = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+            T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, postop, False, ws=ws,
+                                   tile=T.gemv_tile(T.F4MS, 0, 0, gpw, 0, ks))
+            torch.cuda.synchronize()
+            outs.append(host_u16(dC))
+        assert all(np.array_equal(outs[0], o) for o in outs[1:]), "non-deterministic"
+        assert not ws[:cnt_bytes].any().item(), "strip counters not left at zero"
+        dC4 = torch.zeros((M, N), dtype=dA.dtype, device="cuda")
+        T.int2_fp16_upcvt_gemm(dA, dB, dS, dC4, dO, dBias, M, N, K, postop, False, ws=ws,
+                               tile=T.gemv_tile(T.F4, waves, 1, gpw, 0, ks))
+        torch.cuda.synchronize()
+        assert np.array_equal(outs[0], host_u16(dC4)), f"postop {postop}: engine 5 differs from engine 4"
+        want, _ = _gold(orc, A, B, S, other, bias_f, M, K, N, bf16, postop, False)
+        bad, dmax = allclose_report(formats.dt_to_f32(outs[0], bf16), formats.dt_to_f32(want, bf16))
+        assert bad == 0, f"postop {postop}: {bad} bad (max |d| {dmax})"
+
+
 def test_gemv_multistrip_automatic_and_rejects(dev):
     """The automatic plan takes engine 5 at M = 1 past 128 strips of 32 columns (the same
     bits as the explicit engine); engine 5 rejects M > 8, K > 4096 above 4 rows,
-    cols_per_lane 4 above one row, K past one window (64 groups) and tile fields other than
-    cols_per_lane."""
+    cols_per_lane 4 above one row, K past one window (64 groups) and an explicit wave
+    count."""
     import torch
     import ternocl_amd as T
     K, N = 4096, 5120
