@@ -766,11 +766,13 @@ k_int2_gemv_f4(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 // windows once the fragments are in registers.  QM 1 / 2 (MR <= 4): the s8 x
 // s2 GEMV's int8 modes (the kernel above's QM 1 / 2: A int8, or DT quantized
 // while staged; SA [K/128][ldsa]), each group's 1 / SA[g, q] held in
-// registers beside its fragments.  ksn > 1 (grid.y = ksn): K slice blockIdx.y
-// for every strip the workgroup walks; each strip's reducer stores the
-// slice's sums (part fp32 [ksn][M][N]) and arrives at the strip's counter, and
-// the last of the ksn adds the slices in order -- the kernel above's handoff.
-template <int MR, int GPW, int CPL, bool BF16, int QM = 0>
+// registers beside its fragments.  KS (ksn > 1, grid.y = ksn): K slice
+// blockIdx.y for every strip the workgroup walks; each strip's reducer stores
+// the slice's sums (part fp32 [ksn][M][N]) and arrives at the strip's counter,
+// and the last of the ksn adds the slices in order -- the kernel above's
+// handoff.  (A variant of its own: the handoff's registers would make the
+// unsplit kernel spill.)
+template <int MR, int GPW, int CPL, bool BF16, int QM = 0, bool KS = false>
 __global__ void __launch_bounds__(MR > 4 ? 64 * 8 : 64 * 16)
 k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                  const uint16_t *__restrict__ S, void *__restrict__ C, const uint16_t *__restrict__ Other,
@@ -779,6 +781,7 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                  uint32_t *cnt = nullptr) {
     static_assert(MR == 1 || MR == 2 || MR == 4 || MR == 8, "1, 2, 4 or 8 rows");
     static_assert(QM == 0 || ((QM == 1 || QM == 2) && MR <= 4), "DT, or int8 activations up to 4 rows");
+    static_assert(!KS || QM == 0, "K slices: DT activations");
     constexpr bool I8 = QM != 0;
     constexpr int RS = kF4RowStride, RR = RS * MR, P = I8 ? 2 : f4_pieces(BF16);
     constexpr int RSETS = f4_rsets(MR), RR1 = RR < 16 ? RR : 16, QV = MR < 4 ? MR : 4;
@@ -789,13 +792,11 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
     const int c = lane & 15, q = lane >> 4;
     int groups = K / kGS;
     const int g0w = wave * GPW;  // (the host keeps a slice's groups <= W GPW)
-    const int ks = ksn > 1 ? (int)blockIdx.y : 0;
-    if (ksn > 1) {  // slice ks: groups [ks gps, ks gps + gps) (the host keeps every slice non-empty)
+    const int ks = KS ? (int)blockIdx.y : 0;
+    if constexpr (KS) {  // slice ks: groups [ks gps, ks gps + gps) (the host keeps every slice non-empty)
         const int gps = (groups + ksn - 1) / ksn, g_lo = ks * gps;
         groups = min(gps, groups - g_lo);
-        if constexpr (QM == 1) A = (const uint16_t *)((const int8_t *)A + (size_t)g_lo * kGS);  // int8 rows
-        else A += (size_t)g_lo * kGS;
-        if constexpr (I8) SA += (size_t)g_lo * ldsa;
+        A += (size_t)g_lo * kGS;
         B += (size_t)g_lo * 8 * N;
         S += (size_t)g_lo * N;
     }
@@ -899,7 +900,32 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
                 }
         }
         __syncthreads();
-        if (wave == it % W && q < QV) {  // (wave-uniform) this strip's reducer, lane q rows q + 4t
+        if constexpr (!KS) {
+            if (wave == it % W && q < QV) {  // (wave-uniform) this strip's reducer, lane q rows q + 4t
+#pragma unroll
+                for (int t = 0; t < RSETS; ++t) {
+                    const int m = q + 4 * t;
+                    float sum[CPL];
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) sum[j] = rb[(j * MR + m) * 16 + c];
+                    for (int w2 = 1; w2 < W; ++w2)
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j) sum[j] += rb[((w2 * CPL + j) * MR + m) * 16 + c];
+                    const size_t o0 = (size_t)m * N + s * 16 * CPL + CPL * c;
+                    if (m < M)
+                        epi_dispatch(postop, out_f32, [&](auto P_, auto F_) __attribute__((always_inline)) {
+                            constexpr int PO = decltype(P_)::value;
+                            constexpr bool F32 = decltype(F_)::value;
+#pragma unroll
+                            for (int j = 0; j < CPL; ++j) {
+                                const float r = epi_apply_c<PO>(sum[j], ec.other(t, j), ec.bias(j, F32));
+                                if constexpr (F32) ((float *)C)[o0 + j] = r;
+                                else ((uint16_t *)C)[o0 + j] = (uint16_t)f2dt<BF16>(r);
+                            }
+                        });
+                }
+            }
+        } else if (wave == it % W && q < QV) {  // (wave-uniform) the reducer, then the K-slice handoff
             const int n0 = s * 16 * CPL + CPL * c;
             float sum[RSETS][CPL];
 #pragma unroll
@@ -911,8 +937,8 @@ k_int2_gemv_f4ms(const uint16_t *__restrict__ A, const uint32_t *__restrict__ B,
 #pragma unroll
                     for (int j = 0; j < CPL; ++j) sum[t][j] += rb[((w2 * CPL + j) * MR + m) * 16 + c];
             }
-            bool last = true;
-            if (ksn > 1) {  // (uniform) the K-slice handoff of the kernel above, for strip s
+            bool last;  // the K-slice handoff of the kernel above, for strip s
+            {
 #pragma unroll
                 for (int t = 0; t < RSETS; ++t) {
                     const int m = q + 4 * t;
@@ -1341,6 +1367,10 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
                   "N % (16 * cols_per_lane) == 0");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
+    if (ksn > 1 && (cpl != 2 || gpw == 1)) {
+        set_error("the multi-strip GEMV over k_slices > 1 takes cols_per_lane 2 and groups_per_wave 2 or 4");
+        return TERNOCL_ERR_UNSUPPORTED_SHAPE;
+    }
     if (ksn > 1 && !(f4_cnt_fit(N) && ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= f4_split_ws(M, N, ksn))) {
         set_error("k_slices > 1 needs a 16-byte aligned workspace of ternocl_int2_gemm_ws_bytes() bytes for "
                   "that split (and at most 16384 column strips)");
@@ -1356,12 +1386,31 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
     uint32_t *cnt = ksn > 1 ? (uint32_t *)ws : nullptr;
 #define TCL_F4MS(R, G, CP, BF)                                                                                 \
     hipLaunchKernelGGL((k_int2_gemv_f4ms<R, G, CP, BF>), grid, block, lds, st, a, B, s, C, o, Bias, M, N, K,  \
-                       postop, out_f32, nullptr, 0, ksn, part, cnt)
+                       postop, out_f32)
+#define TCL_F4MS_KS(R, G, BF)                                                                                  \
+    hipLaunchKernelGGL((k_int2_gemv_f4ms<R, G, 2, BF, 0, true>), grid, block, lds, st, a, B, s, C, o, Bias, M, \
+                       N, K, postop, out_f32, nullptr, 0, ksn, part, cnt)
 #define TCL_F4MS_G(R, CP, BF)                \
     do {                                     \
         if (gpw == 4) TCL_F4MS(R, 4, CP, BF);     \
         else if (gpw == 2) TCL_F4MS(R, 2, CP, BF); \
         else TCL_F4MS(R, 1, CP, BF);         \
+    } while (0)
+#define TCL_F4MS_KR(BF)                                             \
+    do {                                                            \
+        if (mr == 1) {                                              \
+            if (gpw == 4) TCL_F4MS_KS(1, 4, BF);                    \
+            else TCL_F4MS_KS(1, 2, BF);                             \
+        } else if (mr == 2) {                                       \
+            if (gpw == 4) TCL_F4MS_KS(2, 4, BF);                    \
+            else TCL_F4MS_KS(2, 2, BF);                             \
+        } else if (mr == 4) {                                       \
+            if (gpw == 4) TCL_F4MS_KS(4, 4, BF);                    \
+            else TCL_F4MS_KS(4, 2, BF);                             \
+        } else {                                                    \
+            if (gpw == 4) TCL_F4MS_KS(8, 4, BF);                    \
+            else TCL_F4MS_KS(8, 2, BF);                             \
+        }                                                           \
     } while (0)
 #define TCL_F4MS_R(BF)                                                    \
     do {                                                                  \
@@ -1380,10 +1429,18 @@ ternocl_status int2_gemv_f4ms_run(int dtype, const void *A, const uint32_t *B, c
             else TCL_F4MS_G(8, 1, BF);                                    \
         }                                                                 \
     } while (0)
-    if (dtype == TERNOCL_BF16) TCL_F4MS_R(true);
-    else TCL_F4MS_R(false);
+    if (ksn > 1) {
+        if (dtype == TERNOCL_BF16) TCL_F4MS_KR(true);
+        else TCL_F4MS_KR(false);
+    } else if (dtype == TERNOCL_BF16) {
+        TCL_F4MS_R(true);
+    } else {
+        TCL_F4MS_R(false);
+    }
+#undef TCL_F4MS_KR
 #undef TCL_F4MS_R
 #undef TCL_F4MS_G
+#undef TCL_F4MS_KS
 #undef TCL_F4MS
     return launch_status(hipGetLastError());
 }
