@@ -707,21 +707,25 @@ struct GemmPlan {
     int nmb, ncb, wvm, wvn;
 };
 
-// Tile choice between the two shapes the engine compiles.  The 128 x 512 tile
+// Tile choice between the shapes the engine compiles.  The 128 x 512 tile
 // of eight 128 x 64 waves is the fastest per FLOP (measured 1.1-1.2 PFLOPS at
 // M = 1024..4096), so it is taken whenever it yields at least 192 tiles (three
 // quarters of the CUs busy in its first round; at N = 21504 its second,
 // partial round still beats the 128 x 128 tile).  Below that the 128 x 128
 // tile of 2 x 2 waves, two resident workgroups per CU (measured at 0.78 of
 // the wide tile's MAC rate), wins while all of its tiles fit in one round of
-// 512; past that one round of the wide tile is shorter.  (Scoring 256 x 256,
+// 512; past that one round of the wide tile is shorter.  Where the 128 x 128
+// tiles number at most 256 (one workgroup per CU) the tile runs as eight
+// waves of 64 x 32 (two per SIMD) instead of four of 64 x 64: fp16, M = 1024
+// K = N = 4096 47.5 -> 44.8 us, M = 512 47.2 -> 40.5 us.  (Scoring 256 x 256,
 // 256 x 128 and 128 x 256 tiles the same way never selects them: a shape
 // small enough to run any of them in one round runs the 128 x 128 tile in
 // one round too, and the 256 x 256 tile is slower per FLOP than the wide one.)
 GemmPlan gemm_plan(int M, int N) {
     auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
-    const GemmPlan wide = {8, 4, 1, 8}, square = {4, 4, 2, 2};
+    const GemmPlan wide = {8, 4, 1, 8}, square = {4, 4, 2, 2}, square8 = {4, 2, 2, 4};
     if (tiles(128, 512) >= 192) return wide;
+    if (tiles(128, 128) <= 256) return square8;
     return tiles(128, 128) <= 512 ? square : wide;
 }
 
@@ -739,6 +743,7 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
     if (p.wvn == 8) gemm_launch<TileCfg<8, 4, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.wvn == 4) gemm_launch<TileCfg<4, 2, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
@@ -847,12 +852,20 @@ ternocl_status int2_gemm_decode_run(int dtype, const uint32_t *B, uint32_t *D, i
 
 // Split-K slices for a shape whose 128 x 512 tiles would leave CUs idle: the
 // fewest slices (2, 4 or 8) that make >= 192 work units, each slice a
-// multiple of 128 rows and at least 1024 rows of K; 1 = no split.
+// multiple of 128 rows and at least 2048 rows of K (1024 up to M = 256); 1 =
+// no split.  The slices' partials cost 8 bytes per output and slice of
+// memory traffic against 2 K flops per output of the GEMM, so short slices
+// lose to the unsplit 128 x 128 tiles.  Same box, fp16 / int8 with quant_a,
+// the 1024-row minimum against this rule: M = 1024 K = N = 4096 53.3 / 52.8
+// -> 47.5 / 51.7 us, M = 1024 K = 6144 N = 5120 101.1 / 97.7 -> 94.7 / 94.6,
+// M = 1000 K = 4096 N = 4112 76.0 / 75.1 -> 62.0 / 66.8; at M = 200 K = 5120
+// N = 16384 the 1280-row slices still win (int8 52.4 against 58.1 unsplit).
 int gemm_splits(int M, int N, int K) {
     const long tiles = (long)((M + 127) / 128) * ((N + 511) / 512);
     if (tiles >= 192) return 1;
+    const int kmin = M <= 256 ? 1024 : 2048;
     for (int s = 2; s <= 8; s *= 2)
-        if (K % (128 * s) == 0 && K / s >= 1024 && tiles * s >= 192) return s;
+        if (K % (128 * s) == 0 && K / s >= kmin && tiles * s >= 192) return s;
     return 1;
 }
 

@@ -184,7 +184,7 @@ def test_decode_workload_sweep(dev, orc, M, K, N):
 # Split-K (a workspace of ternocl_int2_gemm_ws_bytes): shapes whose 128 x 512
 # tiles would leave CUs idle, including a ragged one (last row tile 104 rows,
 # last column tile 16 columns).
-SPLITK_SHAPES = [(1024, 14336, 4096), (1024, 17408, 5120), (200, 5120, 16384), (1000, 4096, 4112)]
+SPLITK_SHAPES = [(1024, 14336, 4096), (1024, 17408, 5120), (200, 5120, 16384), (1000, 8192, 4112)]
 
 
 def _splitk_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
