@@ -854,10 +854,11 @@ int int8_moe_tile_rows() { return WideTile::BM; }
 
 // Tile planner: the 128 x 512 wide tile whenever it yields at least 192 tiles
 // (three quarters of the 256 CUs, one workgroup each); else 128 x 128 tiles
-// (2 x 2 waves of 64 x 64, two workgroups per CU), which fill the chip at a
-// quarter of the wide tile's width (at M = 1024, K = 14336, N = 4096: 64 wide
-// tiles, 252 us, against 147 us on 256 narrow ones).  QMODE 1 (DT A quantized
-// while staged) always runs the 128 x 128 engine.
+// (2 x 2 waves of 64 x 64, two workgroups per CU; 2 x 4 waves of 64 x 32 where
+// they number at most 256), which fill the chip at a quarter of the wide
+// tile's width (at M = 1024, K = 14336, N = 4096: 64 wide tiles, 252 us,
+// against 147 us on 256 narrow ones).  QMODE 1 (DT A quantized while staged)
+// always runs the 2 x 2-wave 128 x 128 engine.
 ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
                                   const uint32_t *B, const void *SB, void *C, const void *Other,
                                   const void *Bias, int M, int N, int K, int postop, int out_f32,
@@ -875,8 +876,15 @@ ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, co
         return launch_status(int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st,
                                                 splits, (float *)((uint8_t *)ws + kWsHeader)));
     const bool wide = Aq && (size_t)((M + WideTile::BM - 1) / WideTile::BM) * ((N + WideTile::BN - 1) / WideTile::BN) >= 192;
+    // 128 x 128 tiles numbering at most 256 (one workgroup per CU) as eight
+    // waves of 64 x 32, two per SIMD: M = 1024 K = N = 4096 51.7 -> 46.3 us,
+    // M = 512 47.2 -> 41.3 us (quant_a included)
+    const bool one_round = (size_t)((M + 127) / 128) * ((N + 127) / 128) <= 256;
     const hipError_t e =
         wide  ? int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+        : (Aq && one_round)
+              ? int8_gemm_launch<QTile<4, 2, 2, 4>, false>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop,
+                                                           out_f32, st)
         : Aq  ? int8_gemm_launch<Tile, false>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
               : int8_gemm_launch<Tile, true>(dtype, A, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st);
     return launch_status(e);
