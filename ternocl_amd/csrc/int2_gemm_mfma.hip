@@ -714,18 +714,18 @@ struct GemmPlan {
 // partial round still beats the 128 x 128 tile).  Below that the 128 x 128
 // tile of 2 x 2 waves, two resident workgroups per CU (measured at 0.78 of
 // the wide tile's MAC rate), wins while all of its tiles fit in one round of
-// 512; past that one round of the wide tile is shorter.  Where the 128 x 128
-// tiles number at most 256 (one workgroup per CU) the tile runs as eight
-// waves of 64 x 32 (two per SIMD) instead of four of 64 x 64: fp16, M = 1024
-// K = N = 4096 47.5 -> 44.8 us, M = 512 47.2 -> 40.5 us.  (Scoring 256 x 256,
+// 512; past that one round of the wide tile is shorter.  The 128 x 128 tile
+// runs as eight waves of 64 x 32 (two per SIMD with one workgroup per CU)
+// rather than four of 64 x 64: fp16, M = 1024 K = N = 4096 47.5 -> 44.8 us,
+// M = 512 47.2 -> 40.5 us, M = 1024 K = 2048 N = 6144 (384 tiles) 37.4 ->
+// 35.9 us, M = 1000 K = 4096 N = 4112 61.9 -> 60.4 us.  (Scoring 256 x 256,
 // 256 x 128 and 128 x 256 tiles the same way never selects them: a shape
 // small enough to run any of them in one round runs the 128 x 128 tile in
 // one round too, and the 256 x 256 tile is slower per FLOP than the wide one.)
 GemmPlan gemm_plan(int M, int N) {
     auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
-    const GemmPlan wide = {8, 4, 1, 8}, square = {4, 4, 2, 2}, square8 = {4, 2, 2, 4};
+    const GemmPlan wide = {8, 4, 1, 8}, square = {4, 2, 2, 4};
     if (tiles(128, 512) >= 192) return wide;
-    if (tiles(128, 128) <= 256) return square8;
     return tiles(128, 128) <= 512 ? square : wide;
 }
 
@@ -743,8 +743,7 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
     if (p.wvn == 8) gemm_launch<TileCfg<8, 4, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else if (p.wvn == 4) gemm_launch<TileCfg<4, 2, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
-    else gemm_launch<TileCfg<4, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else gemm_launch<TileCfg<4, 2, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
 template <class Cfg, bool BF16, bool DUAL = false>
