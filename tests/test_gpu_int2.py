@@ -529,8 +529,9 @@ def test_gemv_multistrip_k_slices(dev, orc, M, K, N, ks, gpw, bf16):
 def test_gemv_multistrip_automatic_and_rejects(dev):
     """The automatic plan takes engine 5 at M = 1 past 128 strips of 32 columns (the same
     bits as the explicit engine); engine 5 rejects M > 8, K > 4096 above 4 rows,
-    cols_per_lane 4 above one row, K past one window (64 groups) and an explicit wave
-    count."""
+    cols_per_lane 4 above one row, K past one window (64 groups), an explicit wave
+    count, and K slices without the workspace, at one column per lane or at one group
+    per wave."""
     import torch
     import ternocl_amd as T
     K, N = 4096, 5120
@@ -561,6 +562,15 @@ def test_gemv_multistrip_automatic_and_rejects(dev):
     with pytest.raises(T.TernoclError) as e:
         T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS, 8))
     assert e.value.status == 1
+    with pytest.raises(T.TernoclError) as e:  # K slices need the workspace
+        T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K, tile=T.gemv_tile(T.F4MS, 0, 2, 2, 0, 2))
+    assert e.value.status == 3
+    ws = torch.zeros(T.WS_HEADER_BYTES + 2 * N * 4, dtype=torch.uint8, device="cuda")
+    for cpl, gpw in ((1, 2), (2, 1)):
+        with pytest.raises(T.TernoclError) as e:
+            T.int2_fp16_upcvt_gemm(A, B, S, c0, None, None, 1, N, K, ws=ws,
+                                   tile=T.gemv_tile(T.F4MS, 0, cpl, gpw, 0, 2))
+        assert e.value.status == 2
     K2 = 8320
     A3 = torch.zeros((1, K2), dtype=torch.bfloat16, device="cuda")
     B3 = torch.zeros((K2 // 16, 64), dtype=torch.int32, device="cuda")
