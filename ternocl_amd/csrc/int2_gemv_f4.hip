@@ -1335,9 +1335,14 @@ size_t f4ms_lds(int mr, int gpw, int waves, int cpl) {
 // N = 28672 16.5 -> 14.7, K = 8192 N = 14336 11.4 -> 9.9, K = 3072 N = 32768
 // 10.0 -> 8.9; 8-wave workgroups lose that way (K = 4096 N = 151680 33.9 ->
 // 36.3, K = 2048 N = 65536 10.5 -> 12.8).  8 rows: one per CU too (their
-// staging windows take most of a CU's LDS).
+// staging windows take most of a CU's LDS).  2 to 4 rows with at most 512
+// strips: one per CU as well -- a strip's staging and MFMA work grows with
+// the rows, and the CUs that would hold two workgroups set the launch's
+// length (same box, bf16, bias + residual, K = 4096 N = 14336, M = 2 / 3 / 4:
+// 6.61 / 8.08 / 7.88 -> 6.34 / 6.90 / 7.00 us; N = 6144 level); with more
+// strips two per CU stay ahead (K = 2048 N = 65536, M = 2: 10.2 against 13.6).
 int f4ms_grid(int strips, int waves, int mr = 1) {
-    if (waves <= 8 && mr <= 4) return std::min(strips, 512);
+    if (waves <= 8 && mr <= 4 && (mr == 1 || strips > 512)) return std::min(strips, 512);
     const int per = (strips + 255) / 256;
     return (strips + per - 1) / per;
 }
@@ -1615,7 +1620,9 @@ static hipError_t f4ms_q_launch(const void *A, const void *SA, int ldsa, const u
     int gpw, waves;
     f4ms_plan(K, gpw, waves);
     const int mr = M <= 1 ? 1 : M <= 2 ? 2 : 4, strips = N / 32;
-    const dim3 grid(f4ms_grid(strips, waves)), block(64 * waves);
+    // (the rows count in the grid rule here too: M = 2 / 3 / 4 at K = 4096
+    // N = 14336, 7.24 / 8.1 / 8.15 -> 7.06 / 7.46 / 7.47 us)
+    const dim3 grid(f4ms_grid(strips, waves, mr)), block(64 * waves);
     const size_t lds = f4ms_lds(mr, gpw, waves, 2);
     auto go = [&](auto R_, auto G_) {
         hipLaunchKernelGGL((k_int2_gemv_f4ms<decltype(R_)::value, decltype(G_)::value, 2, BF16, QM>), grid, block,
