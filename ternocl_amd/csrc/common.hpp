@@ -58,6 +58,21 @@ __device__ __forceinline__ uint32_t f2dt(float f) {
     }
 }
 
+// The expert owning row tile `tile` of a grouped GEMM (int2_moe_prefill.cl:79-88
+// searches it): the last e whose first tile meta[E + 1 + e] is <= tile.  The
+// offsets never decrease, so that is the count of such experts less one: one
+// load per lane, 64 experts at a time, and a ballot, in place of a binary
+// search's chain of dependent loads.  (tile >= meta[E + 1] = 0.)
+__device__ __forceinline__ int moe_tile_expert(const int *meta, int E, int tile, int lane) {
+    int n = 0;
+    for (int b = 0; b < E; b += 64) {
+        const int i = b + lane;
+        const bool le = i < E && meta[E + 1 + i] <= tile;
+        n += __builtin_popcountll(__ballot(le));
+    }
+    return __builtin_amdgcn_readfirstlane(n - 1);
+}
+
 // A K-split workgroup's arrival at its column strip's counter (lane 0's atomic,
 // broadcast): the value before this arrival.  atomic_inc wraps to 0 at the
 // last of ksn arrivals, so the counters return to zero after every call.  A

@@ -649,8 +649,8 @@ k_bitcos_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc, c
 // Grouped GEMM of the MoE prefill (int2_moe/int2_moe_prefill.cl:72-141): the
 // rows of each expert e are meta[e] .. meta[e+1]-1 of the expert-sorted order,
 // cut into tiles of moe_tile_rows() rows numbered from meta[E+1+e]; workgroup
-// (tile, column block) finds its expert by binary search over the tile
-// offsets.  A rows come from A_all[perm[p] / topk] when perm is given (the
+// (tile, column block) finds its expert by a ballot over the tile offsets
+// (moe_tile_expert).  A rows come from A_all[perm[p] / topk] when perm is given (the
 // gather fused into the A-tile load), else from A_all[p].  Expert e's weights:
 // B_all + e*(K/16)*N, S_all + e*(K/128)*N; C and Other are indexed by the
 // sorted row p.
@@ -664,14 +664,10 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
     static_assert(Cfg::BM == kMoeTileRows, "MoE row tiles are kMoeTileRows rows");
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
-    if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {  // the last expert whose first tile is <= tile
-        const int mid = (lo + hi + 1) >> 1;
-        if (meta[E + 1 + mid] <= tile) lo = mid;
-        else hi = mid - 1;
-    }
-    const int e = lo, row0 = meta[e];
+    const int tiles = meta[2 * E + 1];
+    const int e = moe_tile_expert(meta, E, tile, threadIdx.x & 63);
+    if (tile >= tiles) return;  // whole workgroup: past the last row tile
+    const int row0 = meta[e];
     const int m0 = (tile - meta[E + 1 + e]) * Cfg::BM;
     const int mrows = min(Cfg::BM, meta[e + 1] - row0 - m0);
     // A rows: token rows of A_all through perm (arows rows in all), or the

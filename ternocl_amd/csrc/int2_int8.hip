@@ -428,8 +428,8 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
 // GRP (the int8 MoE prefill's grouped GEMM, int2_moe/int2_moe_prefill_int8.cl:
 // 86-176): M = G sorted rows, SA [K/128][ldsa(G)]; expert e owns rows meta[e]
 // .. meta[e+1]-1 cut into BM-row tiles numbered from meta[E+1+e] (BM equals the
-// route's tile rows); workgroup (tile, column block) finds its expert by binary
-// search and runs the GEMM on its segment: weights B + e (K/16) N, SB + e
+// route's tile rows); workgroup (tile, column block) finds its expert with a
+// ballot over the tile offsets and runs the GEMM on its segment: weights B + e (K/16) N, SB + e
 // (K/128) N, and Aq, SA's columns, C and Other shifted to the segment's rows.
 // With perm, the A rows are gathered instead: sorted row p reads row
 // perm[p] / topk of Aq [arows][K] and its column of SA [K/128][ldsa(arows)]
@@ -483,15 +483,11 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         const int ntn = (N + BN - 1) / BN;
         const int tile = blockIdx.x / ntn;
         tn = blockIdx.x - tile * ntn;
-        if (tile >= meta[2 * E + 1]) return;  // whole workgroup: past the last row tile
-        int lo = 0, hi = E - 1;
-        while (lo < hi) {  // the last expert whose first tile is <= tile
-            const int mid = (lo + hi + 1) >> 1;
-            if (meta[E + 1 + mid] <= tile) lo = mid;
-            else hi = mid - 1;
-        }
+        const int tiles = meta[2 * E + 1];
+        const int e = moe_tile_expert(meta, E, tile, threadIdx.x & 63);
+        if (tile >= tiles) return;  // whole workgroup: past the last row tile
         // (wave-uniform values: kept in scalar registers)
-        const int e = __builtin_amdgcn_readfirstlane(lo), row0 = __builtin_amdgcn_readfirstlane(meta[e]);
+        const int row0 = __builtin_amdgcn_readfirstlane(meta[e]);
         tm = __builtin_amdgcn_readfirstlane(tile - meta[E + 1 + e]);
         M = __builtin_amdgcn_readfirstlane(meta[e + 1] - row0);
         if (gat) {
