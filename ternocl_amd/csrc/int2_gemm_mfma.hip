@@ -663,7 +663,8 @@ k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all
                 int ntn, int arows, const uint32_t *__restrict__ B2_all, const uint16_t *__restrict__ S2_all) {
     static_assert(Cfg::BM == kMoeTileRows, "MoE row tiles are kMoeTileRows rows");
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
-    const int tile = blockIdx.x / ntn, tn = blockIdx.x - tile * ntn;
+    int tile, tn;
+    moe_tile_of(blockIdx.x, ntn, tile, tn);
     const int tiles = meta[2 * E + 1];
     const int e = moe_tile_expert(meta, E, tile, threadIdx.x & 63);
     if (tile >= tiles) return;  // whole workgroup: past the last row tile
@@ -747,7 +748,7 @@ void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, c
                 const void *S_all, void *C_all, const void *Other_all, int E, int G, int N, int K, int postop,
                 int out_f32, hipStream_t st, const uint32_t *B2_all = nullptr, const void *S2_all = nullptr) {
     const int ntn = (N + Cfg::BN - 1) / Cfg::BN;
-    const int max_tiles = (G + Cfg::BM - 1) / Cfg::BM + E;  // each expert's ragged tail adds at most one tile
+    const int max_tiles = moe_grid_tiles(G, Cfg::BM, E);
     hipLaunchKernelGGL((k_int2_moe_gemm<Cfg, BF16, DUAL>), dim3((unsigned)(max_tiles * ntn)), dim3(Cfg::THREADS), 0,
                        st, meta, (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
                        (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn, perm ? G / topk : G, B2_all,

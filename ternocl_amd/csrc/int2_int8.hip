@@ -481,8 +481,8 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     [[maybe_unused]] const int *prow = nullptr;  // gat: perm of the segment's rows
     if constexpr (GRP) {
         const int ntn = (N + BN - 1) / BN;
-        const int tile = blockIdx.x / ntn;
-        tn = blockIdx.x - tile * ntn;
+        int tile;
+        moe_tile_of(blockIdx.x, ntn, tile, tn);
         const int tiles = meta[2 * E + 1];
         const int e = moe_tile_expert(meta, E, tile, threadIdx.x & 63);
         if (tile >= tiles) return;  // whole workgroup: past the last row tile
@@ -806,7 +806,7 @@ static hipError_t int8_moe_launch(int dtype, const int *meta, const int8_t *Aq, 
     const bool bf = dtype == TERNOCL_BF16;
     const uint16_t *sa = (const uint16_t *)SA, *sb = (const uint16_t *)SB, *oth = (const uint16_t *)Other;
     typedef WideTile TC;
-    const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
+    const int ntn = (N + TC::BN - 1) / TC::BN, max_tiles = moe_grid_tiles(G, TC::BM, E);
     const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
     if (bf)
         hipLaunchKernelGGL((k_int2_int8_gemm_w<TC, true, true>), grid, block, 0, st, Aq, sa, B, sb, C, oth,
@@ -834,7 +834,7 @@ ternocl_status int8_moe_dual_run(int dtype, const int *meta, const int8_t *Aq, c
                                  int E, int G, int N, int K, hipStream_t st, const int *perm, int topk, int arows) {
     typedef WideTile TC;
     constexpr int BN = 32 * TC::WVN;
-    const int ntn = (N + BN - 1) / BN, max_tiles = (G + TC::BM - 1) / TC::BM + E;
+    const int ntn = (N + BN - 1) / BN, max_tiles = moe_grid_tiles(G, TC::BM, E);
     const dim3 grid((unsigned)(max_tiles * ntn)), block(TC::THREADS);
     const uint16_t *sa = (const uint16_t *)SA, *su = (const uint16_t *)Su, *sg = (const uint16_t *)Sg;
     if (dtype == TERNOCL_BF16)
