@@ -102,13 +102,15 @@ ternocl_status bitcos_fwht_gemv_run(int dtype, const void *x, const int8_t *sign
                                     size_t ws_bytes);  // bitcos.hip
 // kernels (moe.hip, int2_gemm_mfma.hip)
 int moe_tile_rows();
-ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st);
+ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st,
+                             int4 *desc = nullptr);
 ternocl_status moe_gather_run(const void *X, const int *perm, void *Xs, int G, int K, int topk, hipStream_t st);
 ternocl_status moe_combine_run(int dtype, const float *Y, const int *inv, const void *RW, void *O, int T,
                                int topk, int N, hipStream_t st);
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
-                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st);
+                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st,
+                            const int4 *desc = nullptr);
 MoeWs moe_ws_layout(int T, int E, int topk, int H, int I);  // moe.hip
 ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const void *RW, int T, int E,
                                int topk, int H, int I, const uint32_t *Bg, const void *Sg,

@@ -273,7 +273,7 @@ __device__ __forceinline__ void xcd_tile_of(int id, int mt, int nt, int &tm, int
 namespace tcl {
 // Byte offsets of the MoE layer's workspace regions (moe.hip: moe_ws_layout).
 struct MoeWs {
-    size_t meta, perm, inv, h, y, total;
+    size_t meta, desc, perm, inv, h, y, total;
 };
 // The int8 MoE prefill layer's workspace (byte offsets, each 256-byte aligned).
 struct MoeI8Ws {

@@ -122,17 +122,33 @@ __device__ __forceinline__ void chunk_interleave(const uint32_t v[8], uint32_t o
 
 // Row source of the A tile: a plain row-major [M, K] matrix, or rows gathered
 // through an index (the MoE path reads token rows of X through perm).
+// Rows from `split` on form a second segment (a tile holding two experts'
+// rows): row r >= split is A + (idx2[r - split] / div) * K, or without an
+// index A + (base2 + r - split) * K.
 struct ARows {
     const uint16_t *A;
     const int *idx;  // nullptr: row r is A + r * K; else A + (idx[r] / div) * K
     int div;
-    __device__ __forceinline__ const uint16_t *row(int r, int K) const {
-        return A + (size_t)(idx ? idx[r] / div : r) * K;
-    }
+    const int *idx2 = nullptr;
+    int base2 = 0, split = 1 << 30;
     // byte offset of row r from A (the A operand stays below 2^31 bytes)
     __device__ __forceinline__ uint32_t rowoff(int r, int K) const {
+        if (r >= split) return (uint32_t)(idx2 ? idx2[r - split] / div : base2 + r - split) * (uint32_t)K * 2u;
         return (uint32_t)(idx ? idx[r] / div : r) * (uint32_t)K * 2u;
     }
+};
+
+// A row tile of the MoE layer holding two experts' short tails: rows
+// [0, kPairSplit) are expert a's (nA of them, C rows from crow0), rows
+// [kPairSplit, 2 kPairSplit) expert b's (nB, C rows from crowB), and the waves
+// of the second half read expert b's weights (Bb, Sb; DUAL: B2b, S2b).
+constexpr int kPairSplit = 64;
+struct PairTile {
+    const uint32_t *Bb = nullptr;
+    const uint16_t *Sb = nullptr;
+    const uint32_t *B2b = nullptr;
+    const uint16_t *S2b = nullptr;
+    int nA = 0, nB = 0, crowB = 0;
 };
 
 constexpr int kEpPitch = 36;  // epilogue floats per row: 32 + 4 (16-byte aligned rows)
@@ -163,7 +179,8 @@ template <int NMB_, int NCB_, int WVM_ = 2, int WVN_ = 2> struct TileCfg {
 // pad), decoded in the tile into the int2 words the int2 path loads (the
 // M-tiled BITCOS GEMM with no re-pack); bclut is the 256-byte table of
 // k_bitcos_gemm.  Unsplit only (kseg == K).
-template <class Cfg, bool BF16, bool DUAL = false, bool SHORT = false, bool BC = false>
+// PAIR: a tile of two experts' tails (PairTile; Cfg of two 64-row wave rows).
+template <class Cfg, bool BF16, bool DUAL = false, bool SHORT = false, bool BC = false, bool PAIR = false>
 __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int mrows,
                                           const uint32_t *__restrict__ B, const uint16_t *__restrict__ S,
                                           void *__restrict__ C, const uint16_t *__restrict__ Other,
@@ -171,11 +188,22 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
                                           int n0, int postop, int out_f32, uint16_t *lds,
                                           const uint32_t *__restrict__ B2 = nullptr,
                                           const uint16_t *__restrict__ S2 = nullptr,
-                                          const uint8_t *__restrict__ bclut = nullptr) {
+                                          const uint8_t *__restrict__ bclut = nullptr,
+                                          const PairTile &pt = PairTile{}) {
     constexpr int NMB = Cfg::NMB, NCB = Cfg::NCB, TH = Cfg::THREADS;
+    static_assert(!PAIR || (SHORT && Cfg::BM == 2 * kPairSplit && 16 * NMB == kPairSplit), "pair tiles: two 64-row wave rows");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = SHORT ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int wm = (wave / Cfg::WVN) * 16 * NMB, wn = (wave % Cfg::WVN) * 16 * NCB;
+    const bool hb = PAIR && wm >= kPairSplit;  // (uniform) this wave computes expert b's rows
+    if constexpr (PAIR) {
+        if (hb) {
+            B = pt.Bb;
+            S = pt.Sb;
+            B2 = pt.B2b;
+            S2 = pt.S2b;
+        }
+    }
     const int stages = kseg / BK;
 
     // All operand loads are buffer loads with per-lane offsets set up once and
@@ -190,7 +218,9 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
 #pragma unroll
     for (int u = 0; u < Cfg::ACH; ++u) {
         const int id = tid + TH * u, r = id >> 2;
-        va[u] = ar.rowoff(r < mrows ? r : mrows - 1, K) + 32u * (id & 3);
+        const int rc = PAIR ? (r < kPairSplit ? min(r, pt.nA - 1) : kPairSplit + min(r - kPairSplit, pt.nB - 1))
+                            : (r < mrows ? r : mrows - 1);
+        va[u] = ar.rowoff(rc, K) + 32u * (id & 3);
     }
     // two register sets: stage t's A chunks live in av[t & 1] from their load,
     // issued two stages ahead, to their LDS store in the middle of stage t - 1
@@ -379,7 +409,8 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
     // A wave is dead when its rows all lie past the tile's end (WVM > 1) or
     // its columns all lie past N (the last column tile of an N that is not a
     // multiple of BN, as the MoE gate/up's I = 1408 on 256-column tiles).
-    const int lmb = SHORT ? max(0, min(MB2, (mrows - wm + 31) / 32)) : MB2;
+    const int lmb = PAIR ? max(0, min(MB2, ((hb ? pt.nB : pt.nA) + 31) / 32))
+                         : SHORT ? max(0, min(MB2, (mrows - wm + 31) / 32)) : MB2;
     constexpr bool kDeadWaves = SHORT;
     const bool dead = (Cfg::WVM > 1 && lmb == 0) || n0 + wn >= N;
     if (kDeadWaves && dead) {
@@ -538,15 +569,18 @@ __device__ __forceinline__ void gemm_tile(const ARows &ar, uint32_t a_bytes, int
                     const int r = wm + 32 * (br >> 4) + 16 * hf + (br & 15);
                     const float4 t = *(const float4 *)(ct + br * kEpPitch + 4 * (lane & 7));
                     const float v4[4] = {t.x, t.y, t.z, t.w};
-                    if (r < mrows && n < N) {
+                    // (PAIR: row r of the second half is row r - kPairSplit of expert b's segment)
+                    const int rr = hb ? r - kPairSplit : r;
+                    const int crow = (hb ? pt.crowB : crow0) + rr;
+                    if (rr < (PAIR ? (hb ? pt.nB : pt.nA) : mrows) && n < N) {
                         if constexpr (DUAL) {
                             uint32_t o[4];
 #pragma unroll
                             for (int i = 0; i < 4; ++i) o[i] = f2dt<BF16>(epi_apply_c<1>(v4[i], up[pass][i], 0.0f));
-                            *(uint2 *)((uint16_t *)C + (size_t)(crow0 + r) * N + n) =
+                            *(uint2 *)((uint16_t *)C + (size_t)crow * N + n) =
                                 make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
                         } else {
-                            epi_store4_c<BF16, P, F32, !SHORT>(C, Other, Bias, N, crow0 + r, n, v4);  // (SHORT: MoE)
+                            epi_store4_c<BF16, P, F32, !SHORT>(C, Other, Bias, N, crow, n, v4);  // (SHORT: MoE)
                         }
                     }
                 }
@@ -654,17 +688,51 @@ k_bitcos_gemm(const uint16_t *__restrict__ A, const uint32_t *__restrict__ Bc, c
 // gather fused into the A-tile load), else from A_all[p].  Expert e's weights:
 // B_all + e*(K/16)*N, S_all + e*(K/128)*N; C and Other are indexed by the
 // sorted row p.
-template <class Cfg, bool BF16, bool DUAL>
+// PCfg (not void): the layer's tile list (desc, from k_moe_route) in place of
+// the tile offsets: desc[0].x tiles, then per tile {row0 a, e_a << 8 | rows a,
+// row0 b, e_b << 8 | rows b} with e_b < 0 for a tile of one expert; a tile of
+// two experts' tails (each <= 64 rows) runs as PCfg, two 64-row wave rows of
+// the same columns, the second row of waves on expert b's weights.
+template <class Cfg, bool BF16, bool DUAL, class PCfg = void>
 __global__ void __launch_bounds__(Cfg::THREADS)
 k_int2_moe_gemm(const int *__restrict__ meta, const uint16_t *__restrict__ A_all,
                 const int *__restrict__ perm, int topk, const uint32_t *__restrict__ B_all,
                 const uint16_t *__restrict__ S_all, void *__restrict__ C_all,
                 const uint16_t *__restrict__ Other_all, int E, int N, int K, int postop, int out_f32,
-                int ntn, int arows, const uint32_t *__restrict__ B2_all, const uint16_t *__restrict__ S2_all) {
+                int ntn, int arows, const uint32_t *__restrict__ B2_all, const uint16_t *__restrict__ S2_all,
+                const int4 *__restrict__ desc = nullptr) {
     static_assert(Cfg::BM == kMoeTileRows, "MoE row tiles are kMoeTileRows rows");
     __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::lds_elems];
     int tile, tn;
     moe_tile_of(blockIdx.x, ntn, tile, tn);
+    if constexpr (!std::is_void_v<PCfg>) {
+        static_assert(PCfg::THREADS == Cfg::THREADS && PCfg::BN == Cfg::BN && PCfg::lds_elems <= Cfg::lds_elems,
+                      "a pair tile fits the launch");
+        if (tile >= desc[0].x) return;  // whole workgroup: past the last tile
+        const int4 d = desc[1 + tile];
+        const int ea = d.y >> 8, na = d.y & 255, r0a = d.x;
+        const size_t boa = (size_t)ea * (K / 16) * N, soa = (size_t)ea * (K / kGS) * N;
+        if (d.w < 0) {  // (uniform) one expert's rows
+            const ARows ar = perm ? ARows{A_all, perm + r0a, topk} : ARows{A_all + (size_t)r0a * K, nullptr, 1};
+            const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : na) * K * 2);
+            gemm_tile<Cfg, BF16, DUAL, true>(ar, a_bytes, na, B_all + boa, S_all + soa, C_all, Other_all, nullptr, r0a,
+                                             N, K, K, tn * Cfg::BN, postop, out_f32, lds,
+                                             DUAL ? B2_all + boa : nullptr, DUAL ? S2_all + soa : nullptr);
+        } else {  // two experts' tails
+            const int eb = d.w >> 8, nb = d.w & 255, r0b = d.z;
+            const size_t bob = (size_t)eb * (K / 16) * N, sob = (size_t)eb * (K / kGS) * N;
+            const ARows ar = perm ? ARows{A_all, perm + r0a, topk, perm + r0b, 0, kPairSplit}
+                                  : ARows{A_all + (size_t)r0a * K, nullptr, 1, nullptr, r0b - r0a, kPairSplit};
+            const uint32_t a_bytes = (uint32_t)((size_t)(perm ? arows : r0b - r0a + nb) * K * 2);
+            const PairTile pt{B_all + bob, S_all + sob, DUAL ? B2_all + bob : nullptr, DUAL ? S2_all + sob : nullptr,
+                              na, nb, r0b};
+            gemm_tile<PCfg, BF16, DUAL, true, false, true>(ar, a_bytes, na, B_all + boa, S_all + soa, C_all, Other_all,
+                                                           nullptr, r0a, N, K, K, tn * Cfg::BN, postop, out_f32, lds,
+                                                           DUAL ? B2_all + boa : nullptr,
+                                                           DUAL ? S2_all + soa : nullptr, nullptr, pt);
+        }
+        return;
+    }
     const int tiles = meta[2 * E + 1];
     const int e = moe_tile_expert(meta, E, tile, threadIdx.x & 63);
     if (tile >= tiles) return;  // whole workgroup: past the last row tile
@@ -743,16 +811,17 @@ void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const vo
     else gemm_launch<TileCfg<4, 2, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
-template <class Cfg, bool BF16, bool DUAL = false>
+template <class Cfg, bool BF16, bool DUAL = false, class PCfg = void>
 void moe_launch(const int *meta, const void *A_all, const int *perm, int topk, const uint32_t *B_all,
                 const void *S_all, void *C_all, const void *Other_all, int E, int G, int N, int K, int postop,
-                int out_f32, hipStream_t st, const uint32_t *B2_all = nullptr, const void *S2_all = nullptr) {
+                int out_f32, hipStream_t st, const uint32_t *B2_all = nullptr, const void *S2_all = nullptr,
+                const int4 *desc = nullptr) {
     const int ntn = (N + Cfg::BN - 1) / Cfg::BN;
     const int max_tiles = moe_grid_tiles(G, Cfg::BM, E);
-    hipLaunchKernelGGL((k_int2_moe_gemm<Cfg, BF16, DUAL>), dim3((unsigned)(max_tiles * ntn)), dim3(Cfg::THREADS), 0,
-                       st, meta, (const uint16_t *)A_all, perm, topk, B_all, (const uint16_t *)S_all, C_all,
-                       (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn, perm ? G / topk : G, B2_all,
-                       (const uint16_t *)S2_all);
+    hipLaunchKernelGGL((k_int2_moe_gemm<Cfg, BF16, DUAL, PCfg>), dim3((unsigned)(max_tiles * ntn)),
+                       dim3(Cfg::THREADS), 0, st, meta, (const uint16_t *)A_all, perm, topk, B_all,
+                       (const uint16_t *)S_all, C_all, (const uint16_t *)Other_all, E, N, K, postop, out_f32, ntn,
+                       perm ? G / topk : G, B2_all, (const uint16_t *)S2_all, desc);
 }
 
 template <class Cfg, bool BF16>
@@ -795,7 +864,8 @@ static int moe_bn(int N, int widest) {
 
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
-                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st) {
+                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st,
+                            const int4 *desc) {
     // 128-row tiles of eight waves side by side, each wave 128 rows x 64
     // columns (the dense engine's wave shape: 0.5 LDS fragment reads and 0.25
     // weight-word decodes per MFMA) on 512-column tiles; 128 x 32 waves on 256,
@@ -803,13 +873,23 @@ ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const
     typedef TileCfg<8, 4, 1, 8> W512;
     typedef TileCfg<8, 2, 1, 8> W256;
     typedef TileCfg<4, 2, 2, 4> W128;
+    typedef TileCfg<4, 8, 2, 4> P512;  // pair tiles: 2 x 4 waves of 64 rows, the same columns
+    typedef TileCfg<4, 4, 2, 4> P256;
     const int bn = moe_bn(N, 512);
     if (dtype == TERNOCL_BF16) {
-        if (bn == 512) moe_launch<W512, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        if (desc) {  // the layer's tile list: two experts' tails may share a tile
+            if (bn == 512) moe_launch<W512, true, false, P512>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st, nullptr, nullptr, desc);
+            else if (bn == 256) moe_launch<W256, true, false, P256>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st, nullptr, nullptr, desc);
+            else moe_launch<W128, true, false, W128>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st, nullptr, nullptr, desc);
+        } else if (bn == 512) moe_launch<W512, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
         else if (bn == 256) moe_launch<W256, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
         else moe_launch<W128, true>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
     } else {
-        if (bn == 512) moe_launch<W512, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
+        if (desc) {  // the layer's tile list: two experts' tails may share a tile
+            if (bn == 512) moe_launch<W512, false, false, P512>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st, nullptr, nullptr, desc);
+            else if (bn == 256) moe_launch<W256, false, false, P256>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st, nullptr, nullptr, desc);
+            else moe_launch<W128, false, false, W128>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st, nullptr, nullptr, desc);
+        } else if (bn == 512) moe_launch<W512, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
         else if (bn == 256) moe_launch<W256, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
         else moe_launch<W128, false>(meta, A_all, perm, topk, B_all, S_all, C_all, Other_all, E, G, N, K, postop, out_f32, st);
     }
@@ -823,10 +903,21 @@ ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const
 // waves of 64 x 32 on 128.
 ternocl_status moe_gate_up_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                                const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
-                               int E, int G, int N, int K, hipStream_t st) {
+                               int E, int G, int N, int K, hipStream_t st, const int4 *desc) {
     typedef TileCfg<8, 2, 1, 8> W256;
     typedef TileCfg<4, 2, 2, 4> W128;
+    typedef TileCfg<4, 4, 2, 4> P256;  // pair tiles: 2 x 4 waves of 64 rows, the same columns
     const bool wide = moe_bn(N, 256) == 256;
+    if (desc) {  // the layer's tile list: two experts' tails may share a tile
+        if (dtype == TERNOCL_BF16) {
+            if (wide) moe_launch<W256, true, true, P256>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg, desc);
+            else moe_launch<W128, true, true, W128>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg, desc);
+        } else {
+            if (wide) moe_launch<W256, false, true, P256>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg, desc);
+            else moe_launch<W128, false, true, W128>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg, desc);
+        }
+        return check_launch();
+    }
     if (dtype == TERNOCL_BF16) {
         if (wide) moe_launch<W256, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);
         else moe_launch<W128, true, true>(meta, A_all, perm, topk, Bu, Su, Hs, nullptr, E, G, N, K, 1, 0, st, Bg, Sg);

@@ -31,10 +31,11 @@ namespace tcl {
 int moe_tile_rows();  // int2_gemm_mfma.hip
 ternocl_status moe_gemm_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                             const uint32_t *B_all, const void *S_all, void *C_all, const void *Other_all,
-                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st);
+                            int E, int G, int N, int K, int postop, int out_f32, hipStream_t st,
+                            const int4 *desc = nullptr);
 ternocl_status moe_gate_up_run(int dtype, const int *meta, const void *A_all, const int *perm, int topk,
                                const uint32_t *Bu, const void *Su, const uint32_t *Bg, const void *Sg, void *Hs,
-                               int E, int G, int N, int K, hipStream_t st);
+                               int E, int G, int N, int K, hipStream_t st, const int4 *desc = nullptr);
 
 namespace {
 
@@ -45,6 +46,13 @@ constexpr int kRouteChunk = kRouteWaves * kRoutePieces * 64;   // ids ranked per
 // 64 x 1024 ids a workgroup's chunk grows (whole passes of 1024) and the
 // total work stays linear in G (at most 64 G counts and G ranks).
 constexpr int kRouteMaxBlocks = 64;
+
+// Sum over the 64 lanes of a wave (every lane gets it).
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
 
 // Lanes of a wave holding the same valid expert id as this lane (log2(E)
 // ballots); invalid lanes get an empty set.
@@ -67,10 +75,14 @@ __device__ __forceinline__ unsigned long long route_group(bool valid, int e, int
 // order, waves in order, pieces in order, lanes in order, lanes of one expert
 // found with log2(E) ballots) and writes perm and inv.  Workgroup 0 writes
 // meta.  Ids outside [0, E) are dropped (inv = -1), and perm past the kept
-// rows is -1.
+// rows is -1.  desc (the layer's tile list, or nullptr): workgroup 0 also
+// lists the row tiles of rpt rows in expert order, each expert's last rows
+// (its tail) sharing a tile with the next tail of at most rpt / 2 rows when
+// its own has at most rpt / 2: desc[0].x = the tile count, desc[1 + t] =
+// {row0 a, e_a << 8 | rows a, row0 b, e_b << 8 | rows b}, e_b = -1 alone.
 __global__ void __launch_bounds__(kRouteThreads)
 k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict__ perm,
-            int *__restrict__ inv, int G, int E, int rpt, int chunk) {
+            int *__restrict__ inv, int G, int E, int rpt, int chunk, int4 *__restrict__ desc) {
     extern __shared__ int sh[];
     // counts of all ids tot [E] (first those from the chunk on) and of the
     // ids before the chunk bef [E], the
@@ -128,6 +140,44 @@ k_moe_route(const int *__restrict__ ids, int *__restrict__ meta, int *__restrict
                 meta[E] = r0;
                 meta[2 * E + 1] = t0;
             }
+        }
+        if (desc && blockIdx.x == 0) {
+            // The tile list: first every expert's full tiles and its tail of
+            // more than rpt / 2 rows, in expert order (a scan of the per-expert
+            // counts), then the tails of at most rpt / 2 rows in pairs, in
+            // expert order (the k-th such tail takes half k % 2 of pair k / 2;
+            // an odd last one is alone).  Each half is one int2 store.
+            const int hr = rpt / 2;
+            int s_all = 0, m_all = 0;
+            for (int e0 = 0; e0 < E; e0 += 64) {  // totals
+                const int e = e0 + lane, c = e < E ? tot[e] : 0, tail = c % rpt;
+                s_all += wave_sum(c / rpt + (tail > hr ? 1 : 0));
+                m_all += wave_sum(tail > 0 && tail <= hr ? 1 : 0);
+            }
+            int2 *d2 = (int2 *)desc;
+            int s_run = 0, m_run = 0, r_run = 0;
+            for (int e0 = 0; e0 < E; e0 += 64) {
+                const int e = e0 + lane, c = e < E ? tot[e] : 0, full = c / rpt, tail = c - full * rpt;
+                const int f = full + (tail > hr ? 1 : 0), sm = tail > 0 && tail <= hr ? 1 : 0;
+                int fi = f, si = sm, ri = c;  // inclusive scans over the 64 lanes
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int fu = __shfl_up(fi, o), su = __shfl_up(si, o), ru = __shfl_up(ri, o);
+                    if (lane >= o) { fi += fu; si += su; ri += ru; }
+                }
+                const int t0 = s_run + fi - f, rank = m_run + si - sm, row = r_run + ri - c;
+                for (int i = 0; i < full; ++i) desc[1 + t0 + i] = make_int4(row + i * rpt, (e << 8) | rpt, 0, -1);
+                if (tail > hr) desc[1 + t0 + full] = make_int4(row + full * rpt, (e << 8) | tail, 0, -1);
+                if (sm) {
+                    const int t = 1 + s_all + (rank >> 1);
+                    d2[2 * t + (rank & 1)] = make_int2(row + full * rpt, (e << 8) | tail);
+                    if ((rank & 1) == 0 && rank == m_all - 1) d2[2 * t + 1] = make_int2(0, -1);  // alone
+                }
+                s_run += __shfl(fi, 63);
+                m_run += __shfl(si, 63);
+                r_run += __shfl(ri, 63);
+            }
+            if (lane == 0) desc[0] = make_int4(s_all + (m_all + 1) / 2, 0, 0, 0);
         }
     }
 
@@ -238,13 +288,14 @@ k_moe_combine(const float *__restrict__ Y, const int *__restrict__ inv, const ui
 // per-wave total, preceding and chunk counts, and each expert's base row
 size_t moe_route_lds(int E) { return (size_t)(3 + kRouteWaves) * E * sizeof(int); }
 
-ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st) {
+ternocl_status moe_route_run(const int *ids, int *meta, int *perm, int *inv, int G, int E, hipStream_t st,
+                             int4 *desc) {
     const int passes = (G + kRouteChunk - 1) / kRouteChunk;
     const int per = (passes + kRouteMaxBlocks - 1) / kRouteMaxBlocks;  // passes per workgroup
     const int chunk = per * kRouteChunk;
     const unsigned blocks = (unsigned)((G + chunk - 1) / chunk);
     hipLaunchKernelGGL(k_moe_route, dim3(blocks), dim3(kRouteThreads), moe_route_lds(E), st, ids, meta, perm, inv,
-                       G, E, moe_tile_rows(), chunk);
+                       G, E, moe_tile_rows(), chunk, desc);
     return check_launch();
 }
 
@@ -270,6 +321,7 @@ MoeWs moe_ws_layout(int T, int E, int topk, int H, int I) {
     MoeWs w;
     size_t o = kWsHeader;
     w.meta = o; o = align_up(o + (size_t)(2 * E + 2) * 4, 256);
+    w.desc = o; o = align_up(o + (size_t)(1 + (G + moe_tile_rows() - 1) / moe_tile_rows() + E) * 16, 256);
     w.perm = o; o = align_up(o + G * 4, 256);
     w.inv = o;  o = align_up(o + G * 4, 256);
     w.h = o;    o = align_up(o + G * I * 2, 256);
@@ -285,14 +337,18 @@ ternocl_status moe_prefill_run(int dtype, const void *X, const int *ids, const v
     const MoeWs w = moe_ws_layout(T, E, topk, H, I);
     char *b = (char *)ws;
     int *meta = (int *)(b + w.meta), *perm = (int *)(b + w.perm), *inv = (int *)(b + w.inv);
+    int4 *desc = (int4 *)(b + w.desc);
     void *Hs = b + w.h;
     float *Y = (float *)(b + w.y);
     const int G = T * topk;
     ternocl_status s;
-    if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
+    // the route lists the row tiles (two experts' short tails share one)
+    if ((s = moe_route_run(ids, meta, perm, inv, G, E, st, desc)) != TERNOCL_OK) return s;
     // up and gate in one pass over the gathered rows (U never leaves the registers)
-    if ((s = moe_gate_up_run(dtype, meta, X, perm, topk, Bu, Su, Bg, Sg, Hs, E, G, I, H, st)) != TERNOCL_OK) return s;
-    if ((s = moe_gemm_run(dtype, meta, Hs, nullptr, 1, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st)) != TERNOCL_OK) return s;
+    if ((s = moe_gate_up_run(dtype, meta, X, perm, topk, Bu, Su, Bg, Sg, Hs, E, G, I, H, st, desc)) != TERNOCL_OK)
+        return s;
+    if ((s = moe_gemm_run(dtype, meta, Hs, nullptr, 1, Bd, Sd, Y, nullptr, E, G, H, I, 0, 1, st, desc)) != TERNOCL_OK)
+        return s;
     return moe_combine_run(dtype, Y, inv, RW, O, T, topk, H, st);
 }
 
@@ -347,7 +403,7 @@ ternocl_status moe_prefill_int8_run(int dtype, const void *X, const int *ids, co
     int8_t *Xq = (int8_t *)(b + w.xq), *Hq = (int8_t *)(b + w.hq);
     const int G = T * topk;
     ternocl_status s;
-    if ((s = moe_route_run(ids, meta, perm, inv, G, E, st)) != TERNOCL_OK) return s;
+    if ((s = moe_route_run(ids, meta, perm, inv, G, E, st, nullptr)) != TERNOCL_OK) return s;
     if ((s = quant_a_run(dtype, X, SA1, Xq, T, H, st)) != TERNOCL_OK) return s;
     // up and gate in one pass over the gathered int8 rows (U never leaves the registers)
     if ((s = int8_moe_dual_run(dtype, meta, Xq, SA1, Bu, Su, Bg, Sg, Hs, E, G, I, H, st, perm, topk, T)) !=
