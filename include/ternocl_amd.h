@@ -379,8 +379,9 @@ ternocl_status ternocl_int2_moe_combine(int dtype, const float *Y, const int *in
  * (POSTOP 1), Y = Hs x B_down (fp32), combine.  X DT [T, H]; gate / up
  * weights [E][H/16][I] / [E][H/128][I]; down [E][I/16][H] / [E][I/128][H];
  * O DT [T, H].  ws: device scratch of ternocl_int2_moe_prefill_ws_bytes()
- * bytes (meta, perm, inv, Hs, Y; the up and gate projections run as one
- * launch whose result equals the two-step sequence bit for bit). */
+ * bytes (meta, the row-tile list, perm, inv, Hs, Y; the up and gate
+ * projections run as one launch whose result equals the two-step sequence bit
+ * for bit, and two experts' tails of at most 64 rows may share a row tile). */
 size_t ternocl_int2_moe_prefill_ws_bytes(int T, int E, int topk, int H, int I);
 ternocl_status ternocl_int2_moe_prefill(int dtype, const void *X, const int *ids, const void *RW,
                                         int T, int E, int topk, int H, int I, const uint32_t *Bg,
