@@ -294,6 +294,33 @@ def test_moe_layer_multi_tile_experts(dev, orc, bf16):
     assert bad == 0, f"{bad} of {got.size} outputs outside the rule (max |d| {dmax})"
 
 
+# rows per expert: empty experts, tails of 1..64 rows (an odd count of them: one
+# is left alone), tails of 65 and 72 rows, whole tiles with and without a tail
+PAIR_COUNTS = [0, 64, 65, 1, 128, 129, 30, 200, 0, 63, 5, 7]
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_moe_layer_pair_tiles(dev, orc, bf16):
+    """The layer's tile list (two experts' tails of at most 64 rows share a row tile, the
+    others alone): every output within 1e-3 + 1e-2 |ref| of the oracle's stage composition,
+    at a routing made for it (top-1, the rows per expert of PAIR_COUNTS, shuffled)."""
+    import torch
+    import ternocl_amd as T
+    E, topk, H, I = len(PAIR_COUNTS), 1, 256, 384
+    g = synth.rng(777)
+    ids = np.repeat(np.arange(E, dtype=np.int32), PAIR_COUNTS)
+    g.shuffle(ids)
+    Tk = ids.size
+    print(f"moe pair tiles T={Tk} E={E} rows/expert {PAIR_COUNTS} bf16={bf16}", flush=True)
+    X = synth.activations(g, (Tk, H), bf16)
+    RW = formats.f32_to_dt(np.ones(Tk, np.float32), bf16)
+    W = _weights(g, E, H, I, bf16)
+    got = formats.dt_to_f32(_layer(T, torch, X, ids, RW, Tk, E, topk, H, I, W, bf16), bf16)
+    want = formats.dt_to_f32(_oracle_layer(orc, X, ids, RW, Tk, E, topk, H, I, W, bf16, T.moe_tile_rows()), bf16)
+    bad, dmax = allclose_report(got, want)
+    assert bad == 0, f"{bad} of {got.size} outputs outside the rule (max |d| {dmax})"
+
+
 def _c5_check_tokens(Tk, seed=2026, n_random=8):
     """Tokens of the C5 layer the double-precision check covers: the first four (the first
     rows of every expert's first tile), the last four (their rows land at the ends of the
