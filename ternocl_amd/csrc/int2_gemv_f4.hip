@@ -1687,13 +1687,16 @@ ternocl_status int2_int8_gemv_run(int dtype, const void *A, const int8_t *Aq, co
 // The grouped GEMVs of the MoE decode: C fp32 [rows][N], rows = G (one weight
 // set) or 2G (B / S for pairs 0..G-1, B2 / S2 for G..2G-1); A rows of K, row
 // g / adiv for pair g; experts ids[g] of [E][K/16][N] weights.  Tiles: the
-// automatic M = 1 tile with at most 4 groups per wave, 2 columns per lane where
-// N % 32 == 0 (else 1): the launch has a workgroup per strip and row, so the
-// wider strips halve the workgroups each row's activations are staged in
-// (the MoE decode layer at T = 1, E = 128, top-8, H = 2048, I = 768: 11.54 ->
-// 10.66 us against 1 column per lane, same box, the same bits).
+// M = 1 tile with 2 columns per lane where N % 32 == 0 (else 1) and 4 groups
+// per wave where K / 128 is a multiple of 4 (else the automatic count, at most
+// 4).  The launch has a workgroup per strip and row: the wider strips halve
+// the workgroups each row's activations are staged in, and 4 groups per wave
+// halve a workgroup's waves.  The MoE decode layer at T = 1, E = 128, top-8,
+// H = 2048, I = 768 (same box, the same bits): 1 column per lane 11.54 us,
+// 2 columns 10.66 us; then at 2 columns, (waves x groups per wave) 8 x 2
+// 10.67, 4 x 4 10.13, 4 x 2 10.46, 2 x 4 10.84, 8 x 1 11.36 us.
 static F4Plan f4_group_plan(int N, int K) {
-    F4Plan p = f4_plan(false, 1, N, K, 0, N % 32 == 0 ? 2 : 0, 0);
+    F4Plan p = f4_plan(false, 1, N, K, 0, N % 32 == 0 ? 2 : 0, (K / kGS) % 4 == 0 ? 4 : 0);
     if (p.cpl > 2 || p.gpw > 4 || p.waves > 8) p = f4_plan(false, 1, N, K, 8, p.cpl > 2 ? 2 : p.cpl, p.gpw > 4 ? 4 : p.gpw);
     return p;
 }
