@@ -783,14 +783,27 @@ struct GemmPlan {
 // runs as eight waves of 64 x 32 (two per SIMD with one workgroup per CU)
 // rather than four of 64 x 64: fp16, M = 1024 K = N = 4096 47.5 -> 44.8 us,
 // M = 512 47.2 -> 40.5 us, M = 1024 K = 2048 N = 6144 (384 tiles) 37.4 ->
-// 35.9 us, M = 1000 K = 4096 N = 4112 61.9 -> 60.4 us.  (Scoring 256 x 256,
-// 256 x 128 and 128 x 256 tiles the same way never selects them: a shape
-// small enough to run any of them in one round runs the 128 x 128 tile in
-// one round too, and the 256 x 256 tile is slower per FLOP than the wide one.)
+// 35.9 us, M = 1000 K = 4096 N = 4112 61.9 -> 60.4 us.  Where those tiles
+// number more than 256 (some CUs would hold two) and 128 x 256 tiles fit one
+// per CU, the 128 x 256 tile of eight 128 x 32 waves runs instead: the same
+// work on the busiest CU with half the weight decodes per MFMA (fp16, same
+// box, two runs each, against the 128 x 128 tile: M = 1024 K = 4096 N = 6144
+// 76.7 / 86.6 -> 69.0 / 74.1 us, M = 1024 K = 6144 N = 5120 110.0 / 115.8 ->
+// 96.2 / 99.2, M = 512 K = 4096 N = 14336 89.7 / 85.0 -> 74.2 / 74.2, M =
+// 2048 K = N = 4096 85.2 / 88.7 -> 75.0 / 79.5, M = 1024 K = 2048 N = 6144
+// 39.5 / 39.3 -> 37.2 / 36.9).  (A 256 x 256 tile is slower per FLOP than
+// the wide one, and a shape small enough to run it in one round runs the
+// 128 x 128 tile in one round too.)
+bool gemm_half_tile(int M, int N) {
+    auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
+    return tiles(128, 512) < 192 && tiles(128, 128) > 256 && tiles(128, 256) <= 256;
+}
+
 GemmPlan gemm_plan(int M, int N) {
     auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
-    const GemmPlan wide = {8, 4, 1, 8}, square = {4, 2, 2, 4};
+    const GemmPlan wide = {8, 4, 1, 8}, half = {8, 2, 1, 8}, square = {4, 2, 2, 4};
     if (tiles(128, 512) >= 192) return wide;
+    if (gemm_half_tile(M, N)) return half;
     return tiles(128, 128) <= 512 ? square : wide;
 }
 
@@ -807,7 +820,8 @@ template <bool BF16>
 void gemm_dispatch(const GemmPlan &p, const void *A, const uint32_t *B, const void *S, void *C,
                    const void *Other, const void *Bias, int M, int N, int K, int postop, int out_f32,
                    hipStream_t st) {
-    if (p.wvn == 8) gemm_launch<TileCfg<8, 4, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    if (p.wvn == 8 && p.ncb == 4) gemm_launch<TileCfg<8, 4, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    else if (p.wvn == 8) gemm_launch<TileCfg<8, 2, 1, 8>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     else gemm_launch<TileCfg<4, 2, 2, 4>, BF16>(A, B, S, C, Other, Bias, M, N, K, postop, out_f32, st);
 }
 
@@ -840,9 +854,9 @@ void bitcos_gemm_launch(const void *A, const uint32_t *Bc, const void *S, void *
 ternocl_status bitcos_gemm_mt_run(int dtype, const void *A, const uint32_t *Bc, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K, int postop,
                                   int out_f32, hipStream_t st) {
-    const GemmPlan p = gemm_plan(M, N);
+    const GemmPlan p = gemm_plan(M, N);  // (the 128 x 256 plan runs the 128 x 128 tile here)
     const bool bf = dtype == TERNOCL_BF16;
-    if (p.wvn == 8) {
+    if (p.wvn == 8 && p.ncb == 4) {
         if (bf) bitcos_gemm_launch<TileCfg<8, 4, 1, 8>, true>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         else bitcos_gemm_launch<TileCfg<8, 4, 1, 8>, false>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     } else {
@@ -980,11 +994,16 @@ size_t int2_gemm_ws_need(int M, int N, int K) {
 // With a workspace of int2_gemm_ws_need bytes (16-byte aligned), shapes that
 // split run the 128 x 512 tile over K-slices into it and a reduction kernel
 // adds the slices in order and applies the epilogue (deterministic: the same
-// bits on every run); without one they take the plan of gemm_plan.
+// bits on every run); without one they take the plan of gemm_plan.  Shapes
+// of the 128 x 256 tile take it with or without a workspace: it beat the
+// split (fp16, same box: M = 1024 K = 4096 N = 6144 72.0-76.4 -> 68.7-71.1
+// us, M = 512 K = 4096 N = 14336 81.0-84.5 -> 71.7-75.1, M = 2048 K = N =
+// 4096 84.4-94.4 -> 75.1-81.3).  (The int8 GEMM keeps its split there; the
+// workspace size covers both.)
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
                                   int postop, int out_f32, hipStream_t st, void *ws, size_t ws_bytes) {
-    const int splits = gemm_splits(M, N, K);
+    const int splits = gemm_half_tile(M, N) ? 1 : gemm_splits(M, N, K);
     const bool bf = dtype == TERNOCL_BF16;
     if (splits > 1 && ws && ws_bytes >= int2_gemm_ws_need(M, N, K) && ((uintptr_t)ws & 15) == 0) {
         typedef TileCfg<8, 4, 1, 8> Cfg;

@@ -41,6 +41,10 @@ INT8_VALIDATE = [(1024, 17408, 5120), (1024, 5120, 14336), (1024, 5120, 34816), 
 PREFILL_WORKLOAD = (1024, 4096, 14336)
 # 128 x 512 tiles with ragged M and a last column tile of 16 columns
 WIDE_RAGGED = (1000, 1024, 12304)
+# 128 x 256 tiles (more than 256 tiles of 128 x 128, at most 256 of 128 x 256),
+# the last with ragged M and a last column tile of 16 columns
+HALF_RAGGED = (1000, 2048, 6160)
+HALF_SHAPES = [(1024, 4096, 6144), (512, 4096, 14336), HALF_RAGGED]
 
 
 def sample_rows(M: int) -> np.ndarray:
@@ -173,6 +177,38 @@ def test_wide_tile_epilogues(dev, orc, bf16, postop, out_f32):
     assert bad == 0, f"int8: {bad} bad (max |d| {dmax})"
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", HALF_SHAPES)
+def test_half_tile_shapes(dev, orc, M, K, N, bf16):
+    """The 128 x 256 tile against the oracle; with the split-K workspace the call takes the same
+    tile (the same bits), since that tile beats the split on these shapes."""
+    import torch
+    import ternocl_amd as T
+    bad, dmax = _upcvt_case(dev, orc, M, K, N, bf16)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+    A, B, S, other, bias_f = _inputs(40000 + M + K + N, M, K, N, bf16)
+    dA, dB, dS = dev_dt(A, bf16), dev_raw(B), dev_dt(S, bf16)
+    outs = []
+    for use_ws in (False, True):
+        dO, dBias, dC = _device_io(torch, S, other, bias_f, M, N, bf16, False)
+        need = T.int2_gemm_ws_bytes(M, N, K)
+        ws = torch.zeros(need, dtype=torch.uint8, device="cuda") if use_ws and need else None
+        T.int2_fp16_upcvt_gemm(dA, dB, dS, dC, dO, dBias, M, N, K, 0, False, ws=ws)
+        torch.cuda.synchronize()
+        outs.append(dC)
+    assert torch.equal(outs[0], outs[1]), "the call with a workspace took another path"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_half_tile_epilogues(dev, orc, bf16, postop, out_f32):
+    """Every epilogue on the 128 x 256 tile (ragged rows, a 16-column last tile)."""
+    M, K, N = HALF_RAGGED[0], 256, HALF_RAGGED[2]
+    bad, dmax = _upcvt_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
+    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 @pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
 def test_decode_workload_sweep(dev, orc, M, K, N):
@@ -185,6 +221,10 @@ def test_decode_workload_sweep(dev, orc, M, K, N):
 # tiles would leave CUs idle, including a ragged one (last row tile 104 rows,
 # last column tile 16 columns).
 SPLITK_SHAPES = [(1024, 14336, 4096), (1024, 17408, 5120), (200, 5120, 16384), (1000, 8192, 4112)]
+# the fp16 GEMM runs the 128 x 256 tile (unsplit) at (1024, 17408, 5120) and
+# (1000, 8192, 4112); its split shapes, the last ragged (last row tile 104
+# rows, last 128 x 512 column tile 416 columns)
+FP16_SPLITK_SHAPES = [(1024, 14336, 4096), (200, 5120, 16384), (1000, 8192, 4000)]
 
 
 def _splitk_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
@@ -219,7 +259,7 @@ def _splitk_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("M,K,N", SPLITK_SHAPES)
+@pytest.mark.parametrize("M,K,N", FP16_SPLITK_SHAPES)
 def test_splitk_parity(dev, orc, M, K, N, bf16):
     bad, dmax, bad_nows = _splitk_case(dev, orc, M, K, N, bf16)
     assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
@@ -247,7 +287,7 @@ def test_int8_splitk_epilogues(dev, orc, bf16, postop, out_f32):
 @pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("out_f32", [False, True])
 def test_splitk_epilogues(dev, orc, bf16, postop, out_f32):
-    M, K, N = SPLITK_SHAPES[-1]
+    M, K, N = FP16_SPLITK_SHAPES[-1]
     bad, dmax, bad_nows = _splitk_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
     assert bad_nows == 0
