@@ -81,11 +81,11 @@ const char *ternocl_version(void);
  * (M = 1024, K = 14336, N = 4096: 4 K-slices): fp32 partial tiles per slice,
  * then a reduction that adds the slices in order and applies the epilogue,
  * the same bits on every run.  Without the scratch (NULL or short) those
- * shapes run on 128 x 128 tiles instead.  Shapes that run 128 x 256 tiles
- * (more than 256 tiles of 128 x 128, at most 256 of 128 x 256: M = 1024,
- * K = 4096, N = 6144) take them with or without the scratch and leave it
- * unused; ternocl_int2_gemm_ws_bytes() still counts the split the s8 x s2
- * GEMM makes there.  The fp8 x fp4 GEMV splits K over
+ * shapes run on 128 x 128 tiles instead.  Shapes that run 192 to 256 tiles
+ * of 128 x 256 (more than 256 tiles of 128 x 128: M = 1024, K = 4096,
+ * N = 6144) take them with or without the scratch and leave it unused;
+ * ternocl_int2_gemm_ws_bytes() still counts the split the s8 x s2 GEMM
+ * makes there.  The fp8 x fp4 GEMV splits K over
  * several workgroups per column strip where one workgroup per strip would
  * leave CUs idle or stage too much of A (K = 14336, N = 4096; M >= 3):
  * fp32 slice sums [slices][M][N] and a counter per 16-column strip, the

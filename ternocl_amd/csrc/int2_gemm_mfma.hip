@@ -995,15 +995,19 @@ size_t int2_gemm_ws_need(int M, int N, int K) {
 // split run the 128 x 512 tile over K-slices into it and a reduction kernel
 // adds the slices in order and applies the epilogue (deterministic: the same
 // bits on every run); without one they take the plan of gemm_plan.  Shapes
-// of the 128 x 256 tile take it with or without a workspace: it beat the
-// split (fp16, same box: M = 1024 K = 4096 N = 6144 72.0-76.4 -> 68.7-71.1
-// us, M = 512 K = 4096 N = 14336 81.0-84.5 -> 71.7-75.1, M = 2048 K = N =
-// 4096 84.4-94.4 -> 75.1-81.3).  (The int8 GEMM keeps its split there; the
-// workspace size covers both.)
+// of the 128 x 256 tile with at least 192 such tiles take it with or without
+// a workspace: it beat the split (fp16, same box: M = 1024 K = 4096 N = 6144
+// 72.0-76.4 -> 68.7-71.1 us, M = 512 K = 4096 N = 14336 81.0-84.5 ->
+// 71.7-75.1, M = 2048 K = N = 4096 84.4-94.4 -> 75.1-81.3); with fewer the
+// CUs it leaves idle cost more than the split (M = 1024 K = 17408 N = 5120,
+// 160 tiles: 240.2 / 237.9 us split against 255.5 / 254.7; M = 1000 K = 8192
+// N = 4112, 136 tiles: 124.3 / 129.7 against 121.4 / 123.7).  (The int8 GEMM
+// keeps its split there; the workspace size covers both.)
 ternocl_status int2_gemm_mfma_run(int dtype, const void *A, const uint32_t *B, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K,
                                   int postop, int out_f32, hipStream_t st, void *ws, size_t ws_bytes) {
-    const int splits = gemm_half_tile(M, N) ? 1 : gemm_splits(M, N, K);
+    const bool half_first = gemm_half_tile(M, N) && (long)((M + 127) / 128) * ((N + 255) / 256) >= 192;
+    const int splits = half_first ? 1 : gemm_splits(M, N, K);
     const bool bf = dtype == TERNOCL_BF16;
     if (splits > 1 && ws && ws_bytes >= int2_gemm_ws_need(M, N, K) && ((uintptr_t)ws & 15) == 0) {
         typedef TileCfg<8, 4, 1, 8> Cfg;

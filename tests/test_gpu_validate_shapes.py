@@ -181,7 +181,7 @@ def test_wide_tile_epilogues(dev, orc, bf16, postop, out_f32):
 @pytest.mark.parametrize("M,K,N", HALF_SHAPES)
 def test_half_tile_shapes(dev, orc, M, K, N, bf16):
     """The 128 x 256 tile against the oracle; with the split-K workspace the call takes the same
-    tile (the same bits), since that tile beats the split on these shapes."""
+    tile (the same bits): with at least 192 of these tiles it beats the split."""
     import torch
     import ternocl_amd as T
     bad, dmax = _upcvt_case(dev, orc, M, K, N, bf16)
@@ -221,10 +221,9 @@ def test_decode_workload_sweep(dev, orc, M, K, N):
 # tiles would leave CUs idle, including a ragged one (last row tile 104 rows,
 # last column tile 16 columns).
 SPLITK_SHAPES = [(1024, 14336, 4096), (1024, 17408, 5120), (200, 5120, 16384), (1000, 8192, 4112)]
-# the fp16 GEMM runs the 128 x 256 tile (unsplit) at (1024, 17408, 5120) and
-# (1000, 8192, 4112); its split shapes, the last ragged (last row tile 104
-# rows, last 128 x 512 column tile 416 columns)
-FP16_SPLITK_SHAPES = [(1024, 14336, 4096), (200, 5120, 16384), (1000, 8192, 4000)]
+# (the fp16 GEMM without the workspace runs 128 x 256 tiles at the second and
+# the last, fewer than 192 of them, so the split stays with the workspace)
+FP16_SPLITK_SHAPES = SPLITK_SHAPES
 
 
 def _splitk_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
