@@ -42,9 +42,10 @@ PREFILL_WORKLOAD = (1024, 4096, 14336)
 # 128 x 512 tiles with ragged M and a last column tile of 16 columns
 WIDE_RAGGED = (1000, 1024, 12304)
 # 128 x 256 tiles (more than 256 tiles of 128 x 128, at most 256 of 128 x 256),
-# the last with ragged M and a last column tile of 16 columns
+# HALF_RAGGED with ragged M and a last column tile of 16 columns, then one
+# row tile of 77 and of 17 rows (the smallest M of the prefill engine)
 HALF_RAGGED = (1000, 2048, 6160)
-HALF_SHAPES = [(1024, 4096, 6144), (512, 4096, 14336), HALF_RAGGED]
+HALF_SHAPES = [(1024, 4096, 6144), (512, 4096, 14336), HALF_RAGGED, (77, 256, 40960), (17, 256, 33040)]
 
 
 def sample_rows(M: int) -> np.ndarray:
