@@ -30,6 +30,11 @@
 #include "common.hpp"
 
 namespace tcl {
+// 128 x 256 tiles (the rule below gemm_plan's comment; also the s8 x s2 GEMM's)
+bool gemm_half_tile(int M, int N) {
+    auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
+    return tiles(128, 512) < 192 && tiles(128, 128) > 256 && tiles(128, 256) <= 256;
+}
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -794,11 +799,6 @@ struct GemmPlan {
 // 39.5 / 39.3 -> 37.2 / 36.9).  (A 256 x 256 tile is slower per FLOP than
 // the wide one, and a shape small enough to run it in one round runs the
 // 128 x 128 tile in one round too.)
-bool gemm_half_tile(int M, int N) {
-    auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
-    return tiles(128, 512) < 192 && tiles(128, 128) > 256 && tiles(128, 256) <= 256;
-}
-
 GemmPlan gemm_plan(int M, int N) {
     auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
     const GemmPlan wide = {8, 4, 1, 8}, half = {8, 2, 1, 8}, square = {4, 2, 2, 4};

@@ -41,8 +41,10 @@
 #include <cfloat>
 
 namespace tcl {
-// (int2_gemm_mfma.hip: the split-K slice count and reduction of the prefill GEMM)
+// (int2_gemm_mfma.hip: the split-K slice count and reduction of the prefill GEMM,
+// and its rule for 128 x 256 tiles)
 int gemm_splits(int M, int N, int K);
+bool gemm_half_tile(int M, int N);
 hipError_t splitk_reduce_launch(int dtype, const float *part, int splits, void *C, const void *Other,
                                 const void *Bias, int M, int N, int postop, int out_f32, hipStream_t st);
 namespace {
@@ -439,10 +441,10 @@ k_int2_int8_gemm(const void *__restrict__ Asrc, const uint16_t *__restrict__ SA,
 // blocks are the same 32 columns of B (up) and B2 (gate), BN = 32 WVN; C =
 // DT(silu(gate) * DT(up)), the bits of the up launch (postop 0, DT out)
 // followed by the gate launch (postop 1 with Other = that DT output).
-template <int RMB_, int WVN_> struct WTile {
-    static constexpr int RMB = RMB_, WVN = WVN_;
+template <int RMB_, int WVN_, int CB_ = 2> struct WTile {
+    static constexpr int RMB = RMB_, WVN = WVN_, CB = CB_;  // CB: 32-column blocks per wave
     static constexpr int THREADS = 64 * WVN;
-    static constexpr int BM = 32 * RMB, BN = 64 * WVN;
+    static constexpr int BM = 32 * RMB, BN = 32 * CB * WVN;
     static constexpr int AP = BM * 8 / THREADS;  // 16-byte A chunks per thread and stage
     static_assert(BM * 8 % THREADS == 0, "A chunks must divide evenly");
     static_assert(THREADS % BM == 0 && (BM & (BM - 1)) == 0, "threads cover the tile rows evenly");
@@ -472,7 +474,9 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
                    const uint32_t *__restrict__ B2 = nullptr, const uint16_t *__restrict__ SB2 = nullptr) {
     static_assert(!DUAL || GRP, "the dual mode is the grouped MoE GEMM's");
     constexpr int RMB = TC::RMB, BM = TC::BM, AP = TC::AP, TH = TC::THREADS;
-    constexpr int WCOLS = DUAL ? 32 : 64;  // output columns per wave
+    static_assert(!DUAL || TC::CB == 2, "dual: the two weight sets as the wave's two column blocks");
+    constexpr int NCB = TC::CB;                  // 32-column blocks per wave (DUAL: up, gate)
+    constexpr int WCOLS = DUAL ? 32 : 32 * NCB;  // output columns per wave
     constexpr int BN = WCOLS * TC::WVN;
     __shared__ __attribute__((aligned(16))) uint8_t lds[TC::LDS_BYTES];
     int tm, tn, sa_off = 0;
@@ -604,16 +608,16 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) vb[kc] = (uint32_t)(((2 * kc + h) * N + wn + c32) * 4);
     uint32_t vsb = (uint32_t)((wn + c32) * 2);
-    uint32_t bw[2][4], sraw[2];
+    uint32_t bw[NCB][4], sraw[NCB];
     auto b_load = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc)
                 bw[cb][kc] = DUAL ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(cb ? rB2 : rB, vb[kc], 0, 0)
                                   : (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rB, vb[kc] + 128 * cb, 0, 0);
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
+        for (int cb = 0; cb < NCB; ++cb)
             sraw[cb] = DUAL ? __builtin_amdgcn_raw_buffer_load_b16(cb ? rSB2 : rSB, vsb, 0, 0)
                             : __builtin_amdgcn_raw_buffer_load_b16(rSB, vsb + 64 * cb, 0, 0);
 #pragma unroll
@@ -621,11 +625,11 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         vsb += (uint32_t)(2 * N);
     };
 
-    f32x16_t acc[RMB][2];
+    f32x16_t acc[RMB][NCB];
 #pragma unroll
     for (int mb = 0; mb < RMB; ++mb)
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = f32x16_t{};
+        for (int cb = 0; cb < NCB; ++cb) acc[mb][cb] = f32x16_t{};
 
     // Stage g reads buffer g % 3.  B words and scales are loaded one stage
     // ahead, A and SA one and a half: at the middle of stage g every wave
@@ -643,12 +647,14 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
     for (int g = 0; g < groups; ++g) {
         const int nxt = cur == 2 ? 0 : cur + 1;
         const uint8_t *abuf = lds + cur * TC::SBYTES;
-        i32x4_t bf[2][4];
+        i32x4_t bf[NCB][4];
+        float sbf[NCB];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
+        for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) bf[cb][kc] = decode_s2(bw[cb][kc]);
-        const float sbf[2] = {dt2f<BF16>(sraw[0]), dt2f<BF16>(sraw[1])};
+            sbf[cb] = dt2f<BF16>(sraw[cb]);
+        }
         b_load();
 #pragma unroll
         for (int mb = 0; mb < RMB; ++mb) {
@@ -670,7 +676,7 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
 #pragma unroll
             for (int j = 0; j < 4; ++j) inv4[j] = *(const f32x4_t *)(abuf + TC::ABYTES + 4 * (32 * mb + 8 * j + 4 * h));
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
+            for (int cb = 0; cb < NCB; ++cb) {
                 i32x16_t dot = mfma_i8_32(af[0], bf[cb][0], i32x16_t{});
 #pragma unroll
                 for (int kc = 1; kc < 4; ++kc) dot = mfma_i8_32(af[kc], bf[cb][kc], dot);
@@ -704,7 +710,7 @@ k_int2_int8_gemm_w(const int8_t *__restrict__ Aq, const uint16_t *__restrict__ S
         constexpr int P = decltype(P_)::value;
         constexpr bool F32 = decltype(F_)::value;
 #pragma unroll
-        for (int cb = 0; cb < (DUAL ? 1 : 2); ++cb) {
+        for (int cb = 0; cb < (DUAL ? 1 : NCB); ++cb) {
             const int n = n0 + wn + 32 * cb + 4 * (lane & 7);
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
@@ -775,11 +781,11 @@ static hipError_t int8_gemm_launch(int dtype, const void *Asrc, const void *SA, 
 
 // The wide-tile engine (QMODE 0: int8 Aq from quant_a); splits > 1: K slices
 // into part (fp32 [splits][M][N]), then the in-order reduction.
+template <class TC = WideTile>
 static hipError_t int8_gemm_w_launch(int dtype, const int8_t *Aq, const void *SA, const uint32_t *B,
                                      const void *SB, void *C, const void *Other, const void *Bias, int M, int N,
                                      int K, int postop, int out_f32, hipStream_t st, int splits = 1,
                                      float *part = nullptr) {
-    typedef WideTile TC;
     const int mt = (M + TC::BM - 1) / TC::BM, nt = (N + TC::BN - 1) / TC::BN;
     const dim3 grid(xcd_ashare_grid(mt, nt * splits)), block(TC::THREADS);
     if (dtype == TERNOCL_BF16)
@@ -849,10 +855,12 @@ ternocl_status int8_moe_dual_run(int dtype, const int *meta, const int8_t *Aq, c
 int int8_moe_tile_rows() { return WideTile::BM; }
 
 // Tile planner: the 128 x 512 wide tile whenever it yields at least 192 tiles
-// (three quarters of the 256 CUs, one workgroup each); else 128 x 128 tiles
-// (2 x 2 waves of 64 x 64, two workgroups per CU; 2 x 4 waves of 64 x 32 where
-// they number at most 256), which fill the chip at a quarter of the wide
-// tile's width (at M = 1024, K = 14336, N = 4096: 64 wide tiles, 252 us,
+// (three quarters of the 256 CUs, one workgroup each); else the 128 x 256
+// tile of the same engine (eight waves of 128 x 32) where 128 x 128 tiles
+// would number more than 256 and 128 x 256 tiles fit one per CU; else 128 x
+// 128 tiles (2 x 2 waves of 64 x 64, two workgroups per CU; 2 x 4 waves of
+// 64 x 32 where they number at most 256), which fill the chip at a quarter of
+// the wide tile's width (at M = 1024, K = 14336, N = 4096: 64 wide tiles, 252 us,
 // against 147 us on 256 narrow ones).  QMODE 1 (DT A quantized while staged)
 // always runs the 2 x 2-wave 128 x 128 engine.
 ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, const void *SA,
@@ -865,9 +873,21 @@ ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, co
         set_error("int2_int8_gemm: the A operand and B must each be below 2^31 bytes");
         return TERNOCL_ERR_UNSUPPORTED_SHAPE;
     }
-    // the wide tile over K slices where its tiles alone leave CUs idle and the
-    // caller gives the partials' workspace (the fp16 prefill GEMM's rule)
-    const int splits = Aq ? gemm_splits(M, N, K) : 1;
+    // 128 x 256 tiles of eight 128 x 32 waves where 128 x 128 tiles would
+    // number more than 256 and 128 x 256 tiles fit one per CU (the fp16
+    // prefill GEMM's rule): they decode each weight word for 128 rows, the
+    // 128 x 128 engine for 64.  Same box, quant_a'd fp16 A, against that
+    // engine / the split (two runs each, us): M = 1024 K = 4096 N = 6144
+    // 69.3 / 67.8 -> 54.4, M = 1024 K = 6144 N = 5120 96.3 -> 76.7, M = 512
+    // K = 4096 N = 14336 72.6 / 70.4 -> 58.5, M = 2048 K = N = 4096 73.2 /
+    // 75.9 -> 58.0-62.0, M = 1000 K = 2048 N = 6160 41.3 -> 31.6; at 160 and
+    // 136 tiles too, against the split: M = 1024 K = 17408 N = 5120 207.2 /
+    // 202.6 -> 198.7 / 199.4, M = 1000 K = 8192 N = 4112 113.8 / 112.9 ->
+    // 96.9 / 96.6.  Elsewhere the wide tile over K slices where its tiles
+    // alone leave CUs idle and the caller gives the partials' workspace (the
+    // fp16 prefill GEMM's rule).
+    const bool half = Aq && gemm_half_tile(M, N);
+    const int splits = Aq && !half ? gemm_splits(M, N, K) : 1;
     if (splits > 1 && ws && ((uintptr_t)ws & 15) == 0 && ws_bytes >= kWsHeader + (size_t)splits * M * N * 4)
         return launch_status(int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st,
                                                 splits, (float *)((uint8_t *)ws + kWsHeader)));
@@ -878,6 +898,7 @@ ternocl_status int2_int8_gemm_run(int dtype, const void *A, const int8_t *Aq, co
     const bool one_round = (size_t)((M + 127) / 128) * ((N + 127) / 128) <= 256;
     const hipError_t e =
         wide  ? int8_gemm_w_launch(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
+        : half ? int8_gemm_w_launch<WTile<4, 8, 1>>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop, out_f32, st)
         : (Aq && one_round)
               ? int8_gemm_launch<QTile<4, 2, 2, 4>, false>(dtype, Aq, SA, B, SB, C, Other, Bias, M, N, K, postop,
                                                            out_f32, st)

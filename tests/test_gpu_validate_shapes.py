@@ -204,10 +204,39 @@ def test_half_tile_shapes(dev, orc, M, K, N, bf16):
 @pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("out_f32", [False, True])
 def test_half_tile_epilogues(dev, orc, bf16, postop, out_f32):
-    """Every epilogue on the 128 x 256 tile (ragged rows, a 16-column last tile)."""
+    """Every epilogue on the 128 x 256 tile (ragged rows, a 16-column last tile), fp16 upcvt and
+    s8 x s2."""
     M, K, N = HALF_RAGGED[0], 256, HALF_RAGGED[2]
     bad, dmax = _upcvt_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
-    assert bad == 0, f"{bad} bad (max |d| {dmax})"
+    assert bad == 0, f"upcvt: {bad} bad (max |d| {dmax})"
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop)
+    assert bad == 0, f"int8: {bad} bad (max |d| {dmax})"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", HALF_SHAPES + [(1024, 17408, 5120)])
+def test_int8_half_tile_shapes(dev, orc, M, K, N, bf16):
+    """The s8 x s2 GEMM's 128 x 256 tile against the oracle (row sample, every column); with the
+    split-K workspace the call takes the same tile (the same bits), at any count of these tiles."""
+    import torch
+    import ternocl_amd as T
+    bad, dmax = _int8_case(dev, orc, M, K, N, bf16)
+    assert bad == 0, f"{bad} elements outside 1e-3 + 1e-2*|ref| (max |d| {dmax})"
+    A, B, SB, other, bias_f = _inputs(50000 + M + K + N, M, K, N, bf16)
+    dA = dev_dt(A, bf16)
+    dSA = torch.zeros((K // 128, T.ldsa(M)), dtype=dA.dtype, device="cuda")
+    dAq = torch.zeros((M, K), dtype=torch.int8, device="cuda")
+    T.quant_a(dA, dSA, dAq, M, K)
+    dB, dSB = dev_raw(B), dev_dt(SB, bf16)
+    outs = []
+    for use_ws in (False, True):
+        dO, dBias, dC = _device_io(torch, SB, other, bias_f, M, N, bf16, False)
+        need = T.int2_int8_gemm_ws_bytes(M, N, K)
+        ws = torch.zeros(need, dtype=torch.uint8, device="cuda") if use_ws and need else None
+        T.int2_int8_gemm(None, dAq, dSA, dB, dSB, dC, dO, dBias, M, N, K, 0, False, ws=ws)
+        torch.cuda.synchronize()
+        outs.append(dC)
+    assert torch.equal(outs[0], outs[1]), "the call with a workspace took another path"
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
@@ -223,8 +252,12 @@ def test_decode_workload_sweep(dev, orc, M, K, N):
 # last column tile 16 columns).
 SPLITK_SHAPES = [(1024, 14336, 4096), (1024, 17408, 5120), (200, 5120, 16384), (1000, 8192, 4112)]
 # (the fp16 GEMM without the workspace runs 128 x 256 tiles at the second and
-# the last, fewer than 192 of them, so the split stays with the workspace)
+# the last, fewer than 192 of them, so the split stays with the workspace; the
+# s8 x s2 GEMM runs those tiles there with or without it, and splits at the
+# others and at a ragged shape of 128 x 128 tiles: last row tile 104 rows,
+# last 128 x 512 column tile 416 columns)
 FP16_SPLITK_SHAPES = SPLITK_SHAPES
+INT8_SPLITK_SHAPES = [(1024, 14336, 4096), (200, 5120, 16384), (1000, 8192, 4000)]
 
 
 def _splitk_case(dev, orc, M, K, N, bf16, postop=0, out_f32=False, seed=0):
@@ -267,7 +300,7 @@ def test_splitk_parity(dev, orc, M, K, N, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("M,K,N", SPLITK_SHAPES)
+@pytest.mark.parametrize("M,K,N", INT8_SPLITK_SHAPES)
 def test_int8_splitk_parity(dev, orc, M, K, N, bf16):
     """The s8 x s2 GEMM's K split (ternocl_int2_int8_gemm_ws) on the same shapes."""
     bad, dmax = _int8_case(dev, orc, M, K, N, bf16, split=True)
@@ -278,7 +311,7 @@ def test_int8_splitk_parity(dev, orc, M, K, N, bf16):
 @pytest.mark.parametrize("postop", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("out_f32", [False, True])
 def test_int8_splitk_epilogues(dev, orc, bf16, postop, out_f32):
-    M, K, N = SPLITK_SHAPES[-1]
+    M, K, N = INT8_SPLITK_SHAPES[-1]
     bad, dmax = _int8_case(dev, orc, M, K, N, bf16, postop, out_f32, seed=postop, split=True)
     assert bad == 0, f"{bad} bad (max |d| {dmax})"
 
