@@ -83,9 +83,9 @@ const char *ternocl_version(void);
  * the same bits on every run.  Without the scratch (NULL or short) those
  * shapes run on 128 x 128 tiles instead.  Shapes that run 192 to 256 tiles
  * of 128 x 256 (more than 256 tiles of 128 x 128: M = 1024, K = 4096,
- * N = 6144) take them with or without the scratch and leave it unused;
- * ternocl_int2_gemm_ws_bytes() still counts the split the s8 x s2 GEMM
- * makes there.  The fp8 x fp4 GEMV splits K over
+ * N = 6144) take them with or without the scratch and leave it unused
+ * (ternocl_int2_gemm_ws_bytes() still counts a split there: the sizes are
+ * upper bounds).  The fp8 x fp4 GEMV splits K over
  * several workgroups per column strip where one workgroup per strip would
  * leave CUs idle or stage too much of A (K = 14336, N = 4096; M >= 3):
  * fp32 slice sums [slices][M][N] and a counter per 16-column strip, the
@@ -206,7 +206,8 @@ ternocl_status ternocl_int2_int8_gemm(int dtype, const void *A, const int8_t *Aq
  * (Aq) on shapes whose 128 x 512 tiles would leave CUs idle (M = 1024,
  * K = 14336, N = 4096) runs those tiles over 2, 4 or 8 K slices into fp32
  * partials there, then a reduction adds the slices in order and applies the
- * epilogue.  The decode GEMV (M <= 4, both modes) splits long K (>= 8192)
+ * epilogue (shapes that run 128 x 256 tiles instead, M = 1024 K = 4096
+ * N = 6144, leave the scratch unused).  The decode GEMV (M <= 4, both modes) splits long K (>= 8192)
  * over narrow N (< 6144 columns) the same way, a counter per 16-column strip
  * electing the workgroup that adds the slices in order.  Either way the same
  * bits on every run.  ws: ternocl_int2_int8_gemm_ws_bytes(M, N, K) bytes (0:
