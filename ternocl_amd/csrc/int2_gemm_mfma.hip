@@ -854,11 +854,17 @@ void bitcos_gemm_launch(const void *A, const uint32_t *Bc, const void *S, void *
 ternocl_status bitcos_gemm_mt_run(int dtype, const void *A, const uint32_t *Bc, const void *S, void *C,
                                   const void *Other, const void *Bias, int M, int N, int K, int postop,
                                   int out_f32, hipStream_t st) {
-    const GemmPlan p = gemm_plan(M, N);  // (the 128 x 256 plan runs the 128 x 128 tile here)
+    // (the 128 x 256 tile against the 128 x 128 one here, same box, z = .5, two
+    // runs each: M = 512 K = 5120 N = 14336 149.9 / 153.0 -> 110.6 / 113.4 us,
+    // M = 1024 K = 4096 N = 6144 115.0 / 115.5 -> 85.7 / 84.8 us)
+    const GemmPlan p = gemm_plan(M, N);
     const bool bf = dtype == TERNOCL_BF16;
     if (p.wvn == 8 && p.ncb == 4) {
         if (bf) bitcos_gemm_launch<TileCfg<8, 4, 1, 8>, true>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         else bitcos_gemm_launch<TileCfg<8, 4, 1, 8>, false>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+    } else if (p.wvn == 8) {
+        if (bf) bitcos_gemm_launch<TileCfg<8, 2, 1, 8>, true>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
+        else bitcos_gemm_launch<TileCfg<8, 2, 1, 8>, false>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
     } else {
         if (bf) bitcos_gemm_launch<TileCfg<4, 4>, true>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);
         else bitcos_gemm_launch<TileCfg<4, 4>, false>(A, Bc, S, C, Other, Bias, M, N, K, postop, out_f32, st);

@@ -339,6 +339,8 @@ BITCOS_VALIDATE_MT = [(64, 4096, 4096, 0.4, 0, False), (77, 4096, 2064, 0.05, 0,
                       (129, 17408, 5120, 0.4, 0, False), (512, 5120, 14336, 0.4, 0, False),
                       (9, 6144, 1024, 0.95, 0, False), (77, 4096, 2048, 0.4, 1, False),
                       (77, 4096, 2048, 0.4, 3, True)]
+# and two lines of 128 x 256 tiles (ragged rows and a 16-column last tile; one row tile of 77)
+BITCOS_HALF_MT = [(1000, 512, 6160, 0.4, 5, False), (77, 512, 40960, 0.3, 3, True)]
 
 
 def _bitcos_inputs(seed, M, K, N, z, bf16):
@@ -395,7 +397,7 @@ def test_bitcos_validate_gemv(dev, orc, M, K, N, ls, z, postop, out_f32, bf16):
 
 @pytest.mark.parametrize("in_tile", [False, True])
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("M,K,N,z,postop,out_f32", BITCOS_VALIDATE_MT)
+@pytest.mark.parametrize("M,K,N,z,postop,out_f32", BITCOS_VALIDATE_MT + BITCOS_HALF_MT)
 def test_bitcos_validate_mt(dev, orc, M, K, N, z, postop, out_f32, bf16, in_tile):
     """Each M-tiled line through ternocl_bitcos_fp16_upcvt_gemm_mt: with the re-pack workspace
     and without (the reference's call: the tiles decode BITCOS), row-sampled above 127 rows."""
