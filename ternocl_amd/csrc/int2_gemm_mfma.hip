@@ -30,7 +30,10 @@
 #include "common.hpp"
 
 namespace tcl {
-// 128 x 256 tiles (the rule below gemm_plan's comment; also the s8 x s2 GEMM's)
+// Whether a prefill GEMM below the 128 x 512 tile's 192-tile mark runs 128 x
+// 256 tiles: where 128 x 128 tiles would number more than 256 (some CUs would
+// hold two) and 128 x 256 tiles fit one per CU.  Used by gemm_plan (the
+// measurements are at its comment) and by the s8 x s2 GEMM's planner.
 bool gemm_half_tile(int M, int N) {
     auto tiles = [&](int BM, int BN) { return (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN); };
     return tiles(128, 512) < 192 && tiles(128, 128) > 256 && tiles(128, 256) <= 256;
